@@ -1,0 +1,239 @@
+/*
+ * u15h.h -- C ABI for the SenseNova-U1.5 Mixture-of-Transformers projection
+ * GEMMs on AMD MI355X (gfx950).
+ *
+ * This is the drop-in boundary for the GEMM half of the reference's op
+ * vocabulary, `u15::MetalOps` (src/u15-metal-ops.h:59-531 in
+ * tgo-app-dev/vpipe-sensenova-u1.5). Every entry point below names the
+ * reference interface it replaces.
+ *
+ * Conventions (the reference's, src/u15-metal-ops.h:102-103 and
+ * src/u15-ref.h:13-17):
+ *   activations  x [M][K]  row-major (token-major), bf16
+ *   weights      w [N][K]  row-major ([out][in], as torch stores them), bf16
+ *   output       y [M][N]  row-major, bf16
+ *   y[m][n] = sum_k x[m][k] * w[n][k]  (+ bias[n]),  fp32 accumulation
+ *
+ * Mixture-of-Transformers routing: every projection exists twice, the base
+ * ("und") weight set used by understanding tokens and the `_mot_gen` ("gen")
+ * set used by generated-image tokens (reference src/u15-backbone.cc:189,
+ * src/u15-weights.h:97-117).  In the grouped entry points the activation
+ * rows are split in two contiguous groups: rows [0, M_und) use the und
+ * weights and rows [M_und, M_und + M_gen) use the gen weights.  Both groups
+ * run in ONE kernel launch.  u15h_route_rows() builds the gather/scatter
+ * row map for the case where token types are interleaved.
+ *
+ * Memory: the caller owns every pointer passed in; all are device pointers
+ * (hipMalloc / torch) unless stated.  The context owns only its scratch.
+ * Alignment: every pointer must be 16-byte aligned.
+ *
+ * Ordering: every call enqueues on the caller's hipStream_t and returns
+ * without synchronising.  A context is not thread-safe: use one per host
+ * thread, or serialise.
+ *
+ * Errors: every call returns a u15h_status.  On any non-OK status from a
+ * shape / argument check NOTHING has been launched (the reference's
+ * "encoder untouched on a decline", src/u15-metal-ops.cc:297-299).
+ * u15h_last_error() gives a human-readable reason.
+ */
+#ifndef U15H_H
+#define U15H_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct u15h_ctx u15h_ctx;
+typedef void*           u15h_stream;   /* a hipStream_t; NULL = the null stream */
+typedef uint16_t        u15h_bf16;     /* bf16 bit pattern */
+
+typedef enum {
+  U15H_OK      = 0,
+  U15H_EINVAL  = 1, /* bad shape, alignment, null pointer, or limit exceeded */
+  U15H_ENODEV  = 2, /* no usable gfx950 device / kernels not loadable        */
+  U15H_ELAUNCH = 3, /* the HIP runtime rejected a launch                     */
+  U15H_ENOMEM  = 4  /* scratch allocation failed                             */
+} u15h_status;
+
+#define U15H_ABI_VERSION 1
+/* Grouped entry points take at most this many projections per launch. */
+#define U15H_MAX_PROJ 4
+
+/* ------------------------------------------------------------------ */
+/* context                                                             */
+/* ------------------------------------------------------------------ */
+
+/* Replaces MetalOps::init (src/u15-metal-ops.cc:39-245): binds a device,
+ * checks that it is gfx950 and that every kernel of this library is
+ * loadable, and refuses otherwise (ENODEV) instead of running a silent
+ * no-op.  `device` is a HIP device ordinal. */
+u15h_status u15h_create(int device, u15h_ctx** out);
+void        u15h_destroy(u15h_ctx* ctx);
+int         u15h_abi_version(void);
+const char* u15h_status_str(u15h_status s);
+/* Reason for the last non-OK status on this context ("" if none). */
+const char* u15h_last_error(const u15h_ctx* ctx);
+
+/* ------------------------------------------------------------------ */
+/* dense bf16 GEMM                                                     */
+/* ------------------------------------------------------------------ */
+
+/* Replaces MetalOps::linear(enc, x, w, bias, y, M, K, N)
+ * (src/u15-metal-ops.h:102-109, src/u15-metal-ops.cc:327-346) and its
+ * BN=64 twin MetalOps::linear_wide (src/u15-metal-ops.h:111-119).
+ * y[M][N] = x[M][K] . w[N][K]^T (+ bias[N]).  bias may be NULL.
+ * If the int8 tier is on (u15h_enable_i8_gemm) and the shape qualifies
+ * (M >= the tier's row floor, K % 128 == 0) the call is served by the int8
+ * path with per-call quantisation of both operands -- the interception
+ * MetalOps::linear_mma_ makes (src/u15-metal-ops.cc:283-306).
+ * Limits: M >= 0, N > 0, K > 0, K % 8 == 0, N % 8 == 0. */
+u15h_status u15h_linear(u15h_ctx* ctx, u15h_stream stream,
+                        const u15h_bf16* x, const u15h_bf16* w,
+                        const u15h_bf16* bias, u15h_bf16* y,
+                        int M, int K, int N);
+
+/* One projection of a MoT layer: both weight sets and its output. */
+typedef struct {
+  const u15h_bf16* w_und;    /* [N][K] base weights (understanding rows)  */
+  const u15h_bf16* w_gen;    /* [N][K] _mot_gen weights (generated rows)  */
+  const u15h_bf16* bias_und; /* [N] or NULL                               */
+  const u15h_bf16* bias_gen; /* [N] or NULL                               */
+  u15h_bf16*       y;        /* [M_und + M_gen][N]                        */
+  int              N;
+} u15h_mot_proj;
+
+/* The two-group grouped GEMM: for each of `nproj` projections sharing the
+ * same input x (e.g. q, k and v; or gate and up), rows [0, M_und) of x are
+ * multiplied by w_und and rows [M_und, M_und+M_gen) by w_gen, all in one
+ * launch.  Row-wise this equals MetalOps::linear with that row's expert's
+ * weights (src/u15-backbone.cc:189 selects `L.gen : L.und` per pass; this
+ * call does the selection per row group instead of per pass).
+ * Limits: 1 <= nproj <= U15H_MAX_PROJ, K % 8 == 0, every N % 8 == 0. */
+u15h_status u15h_mot_linear(u15h_ctx* ctx, u15h_stream stream,
+                            const u15h_bf16* x, int M_und, int M_gen, int K,
+                            const u15h_mot_proj* proj, int nproj);
+
+/* ------------------------------------------------------------------ */
+/* SwiGLU                                                              */
+/* ------------------------------------------------------------------ */
+
+/* Replaces MetalOps::swiglu (src/u15-metal-ops.cc:634-646):
+ * out[i] = silu(gate[i]) * up[i], bf16 in/out, fp32 math
+ * (reference formula: src/u15-ref.cc:51-58 and :303-304). */
+u15h_status u15h_swiglu(u15h_ctx* ctx, u15h_stream stream,
+                        const u15h_bf16* gate, const u15h_bf16* up,
+                        u15h_bf16* out, int64_t n);
+
+/* Replaces MetalOps::swiglu_fused (src/u15-metal-ops.h:121-135,
+ * src/u15-metal-ops.cc:470-491) in grouped form: one launch computes, for
+ * each row group, h[M][I] = silu(x.Wg^T) * (x.Wu^T) with the gate and up
+ * weights given SEPARATELY (no interleaved repack needed: each output tile
+ * reads the matching gate and up rows).  Rounding follows the unfused
+ * reference sequence: gate and up are rounded to bf16 first, then the
+ * silu-product is computed in fp32 and rounded to bf16.
+ * Limits: K % 8 == 0, I % 8 == 0. */
+u15h_status u15h_mot_gate_up_swiglu(u15h_ctx* ctx, u15h_stream stream,
+                                    const u15h_bf16* x, int M_und, int M_gen,
+                                    int K, const u15h_bf16* wg_und,
+                                    const u15h_bf16* wu_und,
+                                    const u15h_bf16* wg_gen,
+                                    const u15h_bf16* wu_gen, u15h_bf16* h,
+                                    int I);
+
+/* ------------------------------------------------------------------ */
+/* int8 tier                                                           */
+/* ------------------------------------------------------------------ */
+
+/* Replaces MetalOps::enable_i8_gemm(bool want) (src/u15-metal-ops.h:71-92,
+ * src/u15-metal-ops.cc:262-275).  Returns whether the tier is ON afterwards,
+ * which is not the same as `want`: the environment variable U15H_I8_GEMM
+ * ("0"/"1") overrides either way.  When on, u15h_linear() routes qualifying
+ * shapes through the int8 path. */
+int  u15h_enable_i8_gemm(u15h_ctx* ctx, int want);
+/* Replaces MetalOps::release_i8_scratch (src/u15-metal-ops.h:94-98). */
+void u15h_release_i8_scratch(u15h_ctx* ctx);
+/* Row floor of the int8 route of u15h_linear (default 1024, env
+ * U15H_I8_MIN_M); the reference's tier declines below ~1k rows
+ * (src/u15-metal-ops.h:71-83). */
+int  u15h_i8_min_m(const u15h_ctx* ctx);
+
+/* Symmetric per-row int8 quantisation of a bf16 matrix [rows][K]:
+ *   s[r] = max_k |x[r][k]| / 127            (fp32, correctly rounded)
+ *   q[r][k] = clamp(round_half_away(x[r][k] / s[r]), -127, 127)
+ *   (s[r] == 0 gives q = 0)
+ * Used both for per-token activations and for per-output-channel weights
+ * (a weight [N][K] quantised per row is quantised per output channel).
+ * No reference counterpart computes these numerics (the reference's int8
+ * tier uses per-512-group scales inside an unvendored library); the
+ * rounding rule is the one the reference's quantisation fixture uses
+ * (std::lround, tests/u15-m5-test.cc:295). */
+u15h_status u15h_quant_rows_i8(u15h_ctx* ctx, u15h_stream stream,
+                               const u15h_bf16* x, int rows, int K,
+                               int8_t* q, float* s);
+
+/* One int8 projection: quantised weights of both sets, their per-channel
+ * scales, and the output.  `y` is int32 [M][N] for u15h_mot_gemm_i8_i32
+ * and bf16 [M][N] for u15h_mot_gemm_i8. */
+typedef struct {
+  const int8_t* wq_und;  /* [N][K] */
+  const float*  sw_und;  /* [N]    */
+  const int8_t* wq_gen;  /* [N][K] */
+  const float*  sw_gen;  /* [N]    */
+  void*         y;
+  int           N;
+} u15h_mot_proj_i8;
+
+/* int8 x int8 -> raw int32 accumulators, grouped like u15h_mot_linear.
+ * Exact: |acc| <= 127*127*K < 2^31 for K <= 133143.  Scales are ignored.
+ * Limits: K % 128 == 0, K <= 131072, N % 8 == 0. */
+u15h_status u15h_mot_gemm_i8_i32(u15h_ctx* ctx, u15h_stream stream,
+                                 const int8_t* xq, int M_und, int M_gen,
+                                 int K, const u15h_mot_proj_i8* proj,
+                                 int nproj);
+
+/* int8 GEMM with the fused dequant epilogue:
+ *   y[m][n] = bf16_rne( ((float)acc[m][n] * sx[m]) * sw[n] )
+ * (int32 -> fp32 conversion round-to-nearest-even, two fp32 multiplies in
+ * that order, then round-to-nearest-even to bf16).
+ * Replaces the int8 route of MetalOps::linear_mma_
+ * (src/u15-metal-ops.cc:300-306) with BASELINE numerics: per-token
+ * activation scales, per-output-channel weight scales.
+ * Limits as u15h_mot_gemm_i8_i32. */
+u15h_status u15h_mot_gemm_i8(u15h_ctx* ctx, u15h_stream stream,
+                             const int8_t* xq, const float* sx, int M_und,
+                             int M_gen, int K, const u15h_mot_proj_i8* proj,
+                             int nproj);
+
+/* ------------------------------------------------------------------ */
+/* per-token routing                                                   */
+/* ------------------------------------------------------------------ */
+
+/* Per-token expert routing for interleaved token types (the grouped entry
+ * points above assume und rows first, then gen rows).  Given
+ * expert[M] (0 = und / base weights, 1 = gen / _mot_gen weights; host
+ * memory), writes perm[M] (host memory) such that rows perm[0..M_und) are
+ * the und tokens and perm[M_und..M) the gen tokens, each in their original
+ * order (a stable partition), and returns the counts.  The reference makes
+ * this split by pass (src/u15-generator.cc:379 prefill = und,
+ * :548 denoise = gen); this is the row-level equivalent. */
+u15h_status u15h_route_rows(const uint8_t* expert, int M, int32_t* perm,
+                            int* M_und, int* M_gen);
+
+/* Gather rows into expert order: dst[i][:] = src[perm[i]][:]
+ * (bf16, row length `cols`, perm in device memory). */
+u15h_status u15h_gather_rows(u15h_ctx* ctx, u15h_stream stream,
+                             const u15h_bf16* src, const int32_t* perm,
+                             int M, int cols, u15h_bf16* dst);
+/* Scatter rows back to token order: dst[perm[i]][:] = src[i][:]. */
+u15h_status u15h_scatter_rows(u15h_ctx* ctx, u15h_stream stream,
+                              const u15h_bf16* src, const int32_t* perm,
+                              int M, int cols, u15h_bf16* dst);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif /* U15H_H */

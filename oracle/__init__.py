@@ -1,0 +1,268 @@
+"""CPU oracle for the MoT projection GEMMs -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+import this package.  It is the checker, never the thing measured or
+shipped: the product library (libu15h.so) neither links nor calls it.
+
+numpy wrappers over liboracle.so (u15_oracle.c, u15_refrand.cc) and, when
+built, over _ref/libu15ref.so -- the reference's own CPU path compiled
+from /root/reference/src/u15-ref.cc where it lies.
+"""
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import subprocess
+
+import numpy as np
+
+ORACLE_DIR = pathlib.Path(__file__).resolve().parent
+LIB_PATH = ORACLE_DIR / "liboracle.so"
+REF_LIB_PATH = ORACLE_DIR / "_ref" / "libu15ref.so"
+
+_lib = None
+_ref = None
+
+
+def build(quiet: bool = True) -> None:
+    """Compile liboracle.so (and _ref/ when the reference is present)."""
+    out = subprocess.run(["make", "-C", str(ORACLE_DIR), "-B", "all"],
+                         capture_output=True, text=True)
+    if out.returncode != 0:
+        raise RuntimeError("oracle build failed:\n" + out.stdout + out.stderr)
+    if not quiet:
+        print(out.stdout)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        L = ctypes.CDLL(str(LIB_PATH))
+        vp, sz = ctypes.c_void_p, ctypes.c_size_t
+        L.u15o_f32_to_bf16.restype = ctypes.c_uint16
+        L.u15o_f32_to_bf16.argtypes = [ctypes.c_float]
+        L.u15o_bf16_to_f32.restype = ctypes.c_float
+        L.u15o_bf16_to_f32.argtypes = [ctypes.c_uint16]
+        for n, a in {
+            "u15o_f32_to_bf16_n": [vp, sz, vp],
+            "u15o_bf16_to_f32_n": [vp, sz, vp],
+            "u15o_linear": [vp, vp, vp, sz, sz, sz, vp],
+            "u15o_linear_bf16": [vp, vp, vp, vp, sz, sz, sz, vp],
+            "u15o_mot_linear_bf16": [vp, vp, vp, sz, sz, sz, sz, vp],
+            "u15o_silu": [vp, sz],
+            "u15o_swiglu_bf16": [vp, vp, sz, vp],
+            "u15o_quant_rows_i8": [vp, sz, sz, vp, vp],
+            "u15o_i8_product_sums": [vp, vp, sz, sz, sz, vp, vp],
+            "u15o_dequant_bf16": [vp, vp, vp, sz, sz, vp],
+            "u15o_dequant_f64": [vp, vp, vp, sz, sz, vp],
+            "u15o_randn_mt": [ctypes.c_uint32, ctypes.c_float, sz, vp],
+        }.items():
+            getattr(L, n).restype = None
+            getattr(L, n).argtypes = a
+        L.u15o_gemm_i8_i32.restype = ctypes.c_int
+        L.u15o_gemm_i8_i32.argtypes = [vp, vp, vp, sz, sz, sz, vp]
+        for n in ("u15o_rel_l2", "u15o_max_rel"):
+            getattr(L, n).restype = ctypes.c_double
+            getattr(L, n).argtypes = [vp, vp, sz]
+        _lib = L
+    return _lib
+
+
+def ref_lib():
+    """The reference's own u15::ref functions, or None if not built."""
+    global _ref
+    if _ref is None and REF_LIB_PATH.exists():
+        R = ctypes.CDLL(str(REF_LIB_PATH))
+        vp, sz = ctypes.c_void_p, ctypes.c_size_t
+        R.u15ref_linear.restype = None
+        R.u15ref_linear.argtypes = [vp, vp, vp, sz, sz, sz, vp]
+        R.u15ref_silu.restype = None
+        R.u15ref_silu.argtypes = [vp, sz]
+        _ref = R
+    return _ref
+
+
+def _c(a, dtype):
+    a = np.ascontiguousarray(a, dtype=dtype)
+    return a, a.ctypes.data
+
+
+# ---- conversions -----------------------------------------------------
+def f32_to_bf16(x) -> np.ndarray:
+    """RNE f32 -> bf16 bit patterns (uint16)."""
+    x, p = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().u15o_f32_to_bf16_n(p, x.size, out.ctypes.data)
+    return out
+
+
+def bf16_to_f32(h) -> np.ndarray:
+    h, p = _c(h, np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().u15o_bf16_to_f32_n(p, h.size, out.ctypes.data)
+    return out
+
+
+# ---- GEMMs ---------------------------------------------------------------
+def linear(x, w, b=None) -> np.ndarray:
+    """ref::linear restated: f32 operands, double accumulation."""
+    x, px = _c(x, np.float32)
+    w, pw = _c(w, np.float32)
+    rows, K = x.shape
+    N = w.shape[0]
+    pb = None
+    if b is not None:
+        b, pb = _c(b, np.float32)
+    y = np.empty((rows, N), np.float32)
+    lib().u15o_linear(px, pw, pb, rows, K, N, y.ctypes.data)
+    return y
+
+
+def linear_bf16(x_bits, w_bits, b_bits=None, row_ids=None) -> np.ndarray:
+    """linear on bf16 bit patterns; optional subset of rows (f32 out)."""
+    x, px = _c(x_bits, np.uint16)
+    w, pw = _c(w_bits, np.uint16)
+    K = x.shape[1]
+    N = w.shape[0]
+    pb = None
+    if b_bits is not None:
+        b_bits, pb = _c(b_bits, np.uint16)
+    pr = None
+    rows = x.shape[0]
+    if row_ids is not None:
+        row_ids, pr = _c(row_ids, np.int32)
+        rows = row_ids.size
+    y = np.empty((rows, N), np.float32)
+    lib().u15o_linear_bf16(px, pw, pb, pr, rows, K, N, y.ctypes.data)
+    return y
+
+
+def mot_linear_bf16(x_bits, w_und, w_gen, M_und, M_gen) -> np.ndarray:
+    x, px = _c(x_bits, np.uint16)
+    wu, pu = _c(w_und, np.uint16)
+    wg, pg = _c(w_gen, np.uint16)
+    K = x.shape[1]
+    N = wu.shape[0]
+    y = np.empty((M_und + M_gen, N), np.float32)
+    lib().u15o_mot_linear_bf16(px, pu, pg, M_und, M_gen, K, N, y.ctypes.data)
+    return y
+
+
+def silu(x) -> np.ndarray:
+    x = np.array(x, dtype=np.float32, copy=True)
+    lib().u15o_silu(x.ctypes.data, x.size)
+    return x
+
+
+def swiglu_bf16(g_bits, u_bits) -> np.ndarray:
+    g, pg = _c(g_bits, np.uint16)
+    u, pu = _c(u_bits, np.uint16)
+    out = np.empty(g.shape, np.float32)
+    lib().u15o_swiglu_bf16(pg, pu, g.size, out.ctypes.data)
+    return out
+
+
+# ---- int8 ------------------------------------------------------------------
+def quant_rows_i8(x_bits):
+    x, px = _c(x_bits, np.uint16)
+    rows, K = x.shape
+    q = np.empty((rows, K), np.int8)
+    s = np.empty(rows, np.float32)
+    lib().u15o_quant_rows_i8(px, rows, K, q.ctypes.data, s.ctypes.data)
+    return q, s
+
+
+def gemm_i8_i32(a, w, row_ids=None) -> np.ndarray:
+    a, pa = _c(a, np.int8)
+    w, pw = _c(w, np.int8)
+    K = a.shape[1]
+    N = w.shape[0]
+    pr = None
+    rows = a.shape[0]
+    if row_ids is not None:
+        row_ids, pr = _c(row_ids, np.int32)
+        rows = row_ids.size
+    acc = np.empty((rows, N), np.int32)
+    if lib().u15o_gemm_i8_i32(pa, pw, pr, rows, K, N, acc.ctypes.data) != 0:
+        raise OverflowError("int8 product does not fit in int32")
+    return acc
+
+
+def i8_product_sums(a, w):
+    a, pa = _c(a, np.int8)
+    w, pw = _c(w, np.int8)
+    rows, K = a.shape
+    N = w.shape[0]
+    rs = np.empty(rows, np.int64)
+    cs = np.empty(N, np.int64)
+    lib().u15o_i8_product_sums(pa, pw, rows, K, N, rs.ctypes.data,
+                               cs.ctypes.data)
+    return rs, cs
+
+
+def dequant_bf16(acc, sa, sw) -> np.ndarray:
+    acc, pa = _c(acc, np.int32)
+    sa, ps = _c(sa, np.float32)
+    sw, pw = _c(sw, np.float32)
+    rows, N = acc.shape
+    y = np.empty((rows, N), np.uint16)
+    lib().u15o_dequant_bf16(pa, ps, pw, rows, N, y.ctypes.data)
+    return y
+
+
+def dequant_f64(acc, sa, sw) -> np.ndarray:
+    acc, pa = _c(acc, np.int32)
+    sa, ps = _c(sa, np.float32)
+    sw, pw = _c(sw, np.float32)
+    rows, N = acc.shape
+    y = np.empty((rows, N), np.float64)
+    lib().u15o_dequant_f64(pa, ps, pw, rows, N, y.ctypes.data)
+    return y
+
+
+# ---- metrics / generator ------------------------------------------------------
+def rel_l2(a, b) -> float:
+    a, pa = _c(a, np.float32)
+    b, pb = _c(b, np.float32)
+    return float(lib().u15o_rel_l2(pa, pb, a.size))
+
+
+def max_rel(a, b) -> float:
+    a, pa = _c(a, np.float32)
+    b, pb = _c(b, np.float32)
+    return float(lib().u15o_max_rel(pa, pb, a.size))
+
+
+def randn_mt(seed: int, n: int, stddev: float = 1.0) -> np.ndarray:
+    """The reference tests' generator (std::mt19937 + normal_distribution)."""
+    out = np.empty(n, np.float32)
+    lib().u15o_randn_mt(seed, stddev, n, out.ctypes.data)
+    return out
+
+
+# ---- the reference's own CPU path (oracle/_ref) ------------------------------
+def ref_linear(x, w, b=None):
+    R = ref_lib()
+    if R is None:
+        return None
+    x, px = _c(x, np.float32)
+    w, pw = _c(w, np.float32)
+    rows, K = x.shape
+    N = w.shape[0]
+    pb = None
+    if b is not None:
+        b, pb = _c(b, np.float32)
+    y = np.empty((rows, N), np.float32)
+    R.u15ref_linear(px, pw, pb, rows, K, N, y.ctypes.data)
+    return y
+
+
+def ref_silu(x):
+    R = ref_lib()
+    if R is None:
+        return None
+    x = np.array(x, dtype=np.float32, copy=True)
+    R.u15ref_silu(x.ctypes.data, x.size)
+    return x

@@ -1,0 +1,267 @@
+/*
+ * u15_oracle.c -- CPU oracle for the MoT projection GEMMs.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker, never the thing measured or
+ * shipped.  See u15_oracle.h for the contract of each function.
+ *
+ * How each function is pinned (tests/test_oracle.py):
+ *   u15o_f32_to_bf16      exhaustive against numpy's RNE rule over a sweep of
+ *                         bit patterns + ties; against the reference's own
+ *                         RNE via the compiled reference (oracle/_ref).
+ *   u15o_linear(_bf16)    against the compiled reference u15::ref::linear
+ *                         (oracle/_ref, built from src/u15-ref.cc) on the
+ *                         reference test's own inputs (golden fixture);
+ *                         closed forms: identity / permutation weights,
+ *                         one-hot rows, K=1 outer product, exact small ints.
+ *   u15o_mot_linear_bf16  reference linear per group; exchange control
+ *                         (swapping the two weight sets changes the result).
+ *   u15o_silu/swiglu      against the compiled reference u15::ref::silu;
+ *                         closed forms silu(0)=0, silu(x)->x, odd symmetry
+ *                         silu(x)-silu(-x)=x.
+ *   u15o_quant_rows_i8    brute-force Python on tiny inputs using exact
+ *                         rational arithmetic (fractions); invariants:
+ *                         |q|<=127, the absmax element maps to +-127, zero
+ *                         rows, ties away from zero.
+ *   u15o_gemm_i8_i32      brute-force Python integer sums; the exact
+ *                         row/column-sum identity; +-127 extremes.
+ *   u15o_dequant_*        float32 numpy evaluation of the same expression.
+ */
+#include "u15_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+uint16_t
+u15o_f32_to_bf16(float f)
+{
+  /* src/u15-weights.cc:51-64: round to nearest even on the upper half. */
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  const uint32_t r = ((u >> 16) & 1u) + 0x7fffu;
+  return (uint16_t)((u + r) >> 16);
+}
+
+float
+u15o_bf16_to_f32(uint16_t h)
+{
+  const uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+void
+u15o_f32_to_bf16_n(const float* in, size_t n, uint16_t* out)
+{
+  for (size_t i = 0; i < n; ++i) { out[i] = u15o_f32_to_bf16(in[i]); }
+}
+
+void
+u15o_bf16_to_f32_n(const uint16_t* in, size_t n, float* out)
+{
+  for (size_t i = 0; i < n; ++i) { out[i] = u15o_bf16_to_f32(in[i]); }
+}
+
+void
+u15o_linear(const float* x, const float* w, const float* b, size_t rows,
+            size_t in_dim, size_t out_dim, float* y)
+{
+  /* src/u15-ref.cc:33-49: one double accumulator per output, seeded with
+   * the bias, summed in input-index order, narrowed to f32 once. */
+  for (size_t r = 0; r < rows; ++r) {
+    const float* xr = x + r * in_dim;
+    float* yr = y + r * out_dim;
+    for (size_t o = 0; o < out_dim; ++o) {
+      const float* wr = w + o * in_dim;
+      double acc = (b != NULL) ? (double)b[o] : 0.0;
+      for (size_t i = 0; i < in_dim; ++i) {
+        acc += (double)xr[i] * (double)wr[i];
+      }
+      yr[o] = (float)acc;
+    }
+  }
+}
+
+void
+u15o_linear_bf16(const uint16_t* x, const uint16_t* w, const uint16_t* b,
+                 const int32_t* row_ids, size_t rows, size_t in_dim,
+                 size_t out_dim, float* y)
+{
+  /* Same arithmetic as u15o_linear with the operands widened exactly from
+   * bf16 (the reference's upload path rounds to bf16 and the kernel widens,
+   * tests/u15-kernels-test.cc:83-90). Rows are widened one at a time. */
+  float* xr = (float*)malloc(in_dim * sizeof(float));
+  if (xr == NULL) { return; }
+  for (size_t rr = 0; rr < rows; ++rr) {
+    const size_t r = row_ids ? (size_t)row_ids[rr] : rr;
+    for (size_t i = 0; i < in_dim; ++i) {
+      xr[i] = u15o_bf16_to_f32(x[r * in_dim + i]);
+    }
+    float* yr = y + rr * out_dim;
+    for (size_t o = 0; o < out_dim; ++o) {
+      const uint16_t* wr = w + o * in_dim;
+      double acc = (b != NULL) ? (double)u15o_bf16_to_f32(b[o]) : 0.0;
+      for (size_t i = 0; i < in_dim; ++i) {
+        acc += (double)xr[i] * (double)u15o_bf16_to_f32(wr[i]);
+      }
+      yr[o] = (float)acc;
+    }
+  }
+  free(xr);
+}
+
+void
+u15o_mot_linear_bf16(const uint16_t* x, const uint16_t* w_und,
+                     const uint16_t* w_gen, size_t M_und, size_t M_gen,
+                     size_t K, size_t N, float* y)
+{
+  /* src/u15-backbone.cc:189: `w = (e == Gen) ? L.gen : L.und`, applied to
+   * the und row group and the gen row group in turn. */
+  u15o_linear_bf16(x, w_und, NULL, NULL, M_und, K, N, y);
+  u15o_linear_bf16(x + M_und * K, w_gen, NULL, NULL, M_gen, K, N,
+                   y + M_und * N);
+}
+
+void
+u15o_silu(float* x, size_t n)
+{
+  /* src/u15-ref.cc:51-58 */
+  for (size_t i = 0; i < n; ++i) {
+    const double v = (double)x[i];
+    x[i] = (float)(v / (1.0 + exp(-v)));
+  }
+}
+
+void
+u15o_swiglu_bf16(const uint16_t* g, const uint16_t* u, size_t n, float* out)
+{
+  /* src/u15-ref.cc:303-304: silu(gate) in place, then gate *= up. */
+  for (size_t i = 0; i < n; ++i) {
+    float gv = u15o_bf16_to_f32(g[i]);
+    u15o_silu(&gv, 1);
+    out[i] = gv * u15o_bf16_to_f32(u[i]);
+  }
+}
+
+void
+u15o_quant_rows_i8(const uint16_t* x, size_t rows, size_t K, int8_t* q,
+                   float* s)
+{
+  for (size_t r = 0; r < rows; ++r) {
+    const uint16_t* xr = x + r * K;
+    float amax = 0.0f;
+    for (size_t k = 0; k < K; ++k) {
+      const float v = fabsf(u15o_bf16_to_f32(xr[k]));
+      if (v > amax) { amax = v; }
+    }
+    const float sc = amax / 127.0f;      /* f32 division, round-to-nearest */
+    s[r] = sc;
+    for (size_t k = 0; k < K; ++k) {
+      long c = 0;
+      if (sc != 0.0f) {
+        const float t = u15o_bf16_to_f32(xr[k]) / sc;
+        c = lroundf(t);                  /* half away from zero */
+        if (c > 127) { c = 127; }
+        if (c < -127) { c = -127; }
+      }
+      q[r * K + k] = (int8_t)c;
+    }
+  }
+}
+
+int
+u15o_gemm_i8_i32(const int8_t* a, const int8_t* w, const int32_t* row_ids,
+                 size_t rows, size_t K, size_t N, int32_t* acc)
+{
+  int ok = 0;
+  for (size_t rr = 0; rr < rows; ++rr) {
+    const size_t r = row_ids ? (size_t)row_ids[rr] : rr;
+    const int8_t* ar = a + r * K;
+    for (size_t n = 0; n < N; ++n) {
+      const int8_t* wr = w + n * K;
+      int64_t t = 0;
+      for (size_t k = 0; k < K; ++k) { t += (int32_t)ar[k] * (int32_t)wr[k]; }
+      if (t > INT32_MAX || t < INT32_MIN) { ok = -1; }
+      acc[rr * N + n] = (int32_t)t;
+    }
+  }
+  return ok;
+}
+
+void
+u15o_i8_product_sums(const int8_t* a, const int8_t* w, size_t rows, size_t K,
+                     size_t N, int64_t* rowsum, int64_t* colsum)
+{
+  /* rowsum = A . (W^T 1) and colsum = (1^T A) . W^T, exact in int64. */
+  int64_t* wk = (int64_t*)calloc(K, sizeof(int64_t));
+  int64_t* ak = (int64_t*)calloc(K, sizeof(int64_t));
+  if (!wk || !ak) { free(wk); free(ak); return; }
+  for (size_t n = 0; n < N; ++n) {
+    for (size_t k = 0; k < K; ++k) { wk[k] += w[n * K + k]; }
+  }
+  for (size_t r = 0; r < rows; ++r) {
+    int64_t t = 0;
+    for (size_t k = 0; k < K; ++k) {
+      t += (int64_t)a[r * K + k] * wk[k];
+      ak[k] += a[r * K + k];
+    }
+    rowsum[r] = t;
+  }
+  for (size_t n = 0; n < N; ++n) {
+    int64_t t = 0;
+    for (size_t k = 0; k < K; ++k) { t += ak[k] * (int64_t)w[n * K + k]; }
+    colsum[n] = t;
+  }
+  free(wk);
+  free(ak);
+}
+
+void
+u15o_dequant_bf16(const int32_t* acc, const float* sa, const float* sw,
+                  size_t rows, size_t N, uint16_t* y)
+{
+  for (size_t r = 0; r < rows; ++r) {
+    for (size_t n = 0; n < N; ++n) {
+      const float a = (float)acc[r * N + n];      /* RNE int32 -> f32 */
+      const float v = (a * sa[r]) * sw[n];
+      y[r * N + n] = u15o_f32_to_bf16(v);
+    }
+  }
+}
+
+void
+u15o_dequant_f64(const int32_t* acc, const float* sa, const float* sw,
+                 size_t rows, size_t N, double* y)
+{
+  for (size_t r = 0; r < rows; ++r) {
+    for (size_t n = 0; n < N; ++n) {
+      y[r * N + n] = (double)acc[r * N + n] * (double)sa[r] * (double)sw[n];
+    }
+  }
+}
+
+double
+u15o_rel_l2(const float* a, const float* b, size_t n)
+{
+  /* tests/u15-kernels-test.cc:95-105 */
+  double num = 0.0, den = 0.0;
+  for (size_t i = 0; i < n; ++i) {
+    const double d = (double)a[i] - (double)b[i];
+    num += d * d;
+    den += (double)b[i] * (double)b[i];
+  }
+  return den > 0.0 ? sqrt(num / den) : sqrt(num);
+}
+
+double
+u15o_max_rel(const float* a, const float* b, size_t n)
+{
+  double md = 0.0, mb = 0.0;
+  for (size_t i = 0; i < n; ++i) {
+    const double d = fabs((double)a[i] - (double)b[i]);
+    if (d > md) { md = d; }
+    if (fabs((double)b[i]) > mb) { mb = fabs((double)b[i]); }
+  }
+  return mb > 0.0 ? md / mb : md;
+}

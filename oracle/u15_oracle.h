@@ -1,0 +1,103 @@
+/*
+ * u15_oracle.h -- CPU oracle for the MoT projection GEMMs.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker the GPU path is
+ * compared against.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it; the product library never links it and has
+ * no CPU fallback.
+ *
+ * Each function restates the reference's algorithm and cites the
+ * reference file:line it follows (tgo-app-dev/vpipe-sensenova-u1.5).
+ * Everything is single-threaded, like the reference's CPU path.
+ *
+ * Pinning (what checks each function against something other than itself)
+ * is listed in the header comment of u15_oracle.c.
+ */
+#ifndef U15_ORACLE_H
+#define U15_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* bf16 <-> f32.  to: round-to-nearest-even as src/u15-weights.cc:51-64
+ * (and the tests' to_bf16, tests/u15-kernels-test.cc:65-73); from: a
+ * 16-bit shift, tests/u15-kernels-test.cc:75-81. */
+uint16_t u15o_f32_to_bf16(float f);
+float    u15o_bf16_to_f32(uint16_t h);
+void     u15o_f32_to_bf16_n(const float* in, size_t n, uint16_t* out);
+void     u15o_bf16_to_f32_n(const uint16_t* in, size_t n, float* out);
+
+/* y[r][o] = sum_i x[r][i]*w[o][i] (+ b[o]): f32 operands, DOUBLE
+ * accumulation in index order, f32 result.  src/u15-ref.cc:33-49. */
+void u15o_linear(const float* x, const float* w, const float* b,
+                 size_t rows, size_t in_dim, size_t out_dim, float* y);
+
+/* The same on bf16 operands (widened exactly), f32 result (not rounded).
+ * `row_ids` selects which rows of x to compute (NULL = all `rows`);
+ * y has one row per computed row. */
+void u15o_linear_bf16(const uint16_t* x, const uint16_t* w,
+                      const uint16_t* b, const int32_t* row_ids,
+                      size_t rows, size_t in_dim, size_t out_dim, float* y);
+
+/* The two-group MoT linear: rows [0,M_und) with w_und, rows
+ * [M_und, M_und+M_gen) with w_gen -- row-wise the reference's
+ * per-pass expert selection, src/u15-backbone.cc:189. */
+void u15o_mot_linear_bf16(const uint16_t* x, const uint16_t* w_und,
+                          const uint16_t* w_gen, size_t M_und, size_t M_gen,
+                          size_t K, size_t N, float* y);
+
+/* silu in double, src/u15-ref.cc:51-58; swiglu = silu(g)*u,
+ * src/u15-ref.cc:303-304.  The bf16 variant takes bf16 gate/up (the
+ * GEMMs' rounded outputs) and returns f32. */
+void u15o_silu(float* x, size_t n);
+void u15o_swiglu_bf16(const uint16_t* g, const uint16_t* u, size_t n,
+                      float* out);
+
+/* Symmetric per-row int8 quantisation (BASELINE numerics; rounding rule of
+ * the reference's only quantisation fixture, std::lround,
+ * tests/u15-m5-test.cc:295):
+ *   s = absmax/127 (f32, correctly rounded), q = clamp(lround(x/s),-127,127)
+ *   s == 0  ->  q = 0. */
+void u15o_quant_rows_i8(const uint16_t* x, size_t rows, size_t K, int8_t* q,
+                        float* s);
+
+/* Exact int8 GEMM: acc[r][n] = sum_k a[r][k]*w[n][k] in int64, stored int32
+ * (checked to fit).  row_ids as u15o_linear_bf16.  Returns 0, or -1 if an
+ * accumulator does not fit in int32. */
+int u15o_gemm_i8_i32(const int8_t* a, const int8_t* w, const int32_t* row_ids,
+                     size_t rows, size_t K, size_t N, int32_t* acc);
+
+/* Exact row / column sums of the int8 product, computed WITHOUT forming
+ * it: rowsum[r] = sum_k a[r][k] * (sum_n w[n][k]),
+ *         colsum[n] = sum_k (sum_r a[r][k]) * w[n][k]   (int64). */
+void u15o_i8_product_sums(const int8_t* a, const int8_t* w, size_t rows,
+                          size_t K, size_t N, int64_t* rowsum,
+                          int64_t* colsum);
+
+/* Dequant epilogue: y = bf16_rne(((float)acc * sa[r]) * sw[n]). */
+void u15o_dequant_bf16(const int32_t* acc, const float* sa, const float* sw,
+                       size_t rows, size_t N, uint16_t* y);
+/* The same in double without rounding (the "exact" dequantised value). */
+void u15o_dequant_f64(const int32_t* acc, const float* sa, const float* sw,
+                      size_t rows, size_t N, double* y);
+
+/* rel-L2 = sqrt(sum (a-b)^2 / sum b^2), tests/u15-kernels-test.cc:95-105;
+ * max-rel = max|a-b| / max|b|. */
+double u15o_rel_l2(const float* a, const float* b, size_t n);
+double u15o_max_rel(const float* a, const float* b, size_t n);
+
+/* The reference tests' input generator: std::mt19937(seed) with
+ * std::normal_distribution<float>(0, stddev) from this toolchain's
+ * libstdc++ (tests/u15-kernels-test.cc:110-118,
+ * tests/u15-m5-test.cc:87-94).  Lets a fixture be regenerated exactly. */
+void u15o_randn_mt(uint32_t seed, float stddev, size_t n, float* out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,254 @@
+"""Pins the CPU oracle (oracle/) to things other than itself.
+
+Each check is chosen so a plausible mistake in the oracle (a dropped term,
+a swapped operand, a wrong rounding rule) fails it:
+  * the reference's own compiled CPU path (oracle/_ref, from
+    src/u15-ref.cc) on the reference test's own inputs;
+  * committed golden fixtures written from that reference path;
+  * closed forms and brute force with independent arithmetic
+    (numpy int64, Python fractions, torch's bf16 rounding).
+"""
+import math
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+REF = oracle.ref_lib() is not None
+
+
+def torch_bf16_bits(a):
+    t = torch.from_numpy(np.ascontiguousarray(a, np.float32))
+    return t.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+# ---- bf16 conversion ---------------------------------------------------------
+def test_bf16_rne_matches_torch_over_bit_sweep():
+    rng = np.random.default_rng(0)
+    u = rng.integers(0, 2**32, size=400_000, dtype=np.uint64).astype(np.uint32)
+    # every low-half pattern that decides a tie, on a spread of exponents
+    ties = (np.arange(0, 2**16, dtype=np.uint32) | (0x3F81 << 16))
+    u = np.concatenate([u, ties, ties | 0x80000000,
+                        np.array([0x3F808000, 0x3F818000, 0x7F7FFFFF],
+                                 np.uint32)])
+    f = u.view(np.float32)
+    f = f[np.isfinite(f)]
+    assert np.array_equal(oracle.f32_to_bf16(f), torch_bf16_bits(f))
+
+
+def test_bf16_widen_is_exact():
+    h = np.arange(0, 2**16, dtype=np.uint16)
+    f = oracle.bf16_to_f32(h)
+    t = torch.from_numpy(h.view(np.int16)).view(torch.bfloat16).float().numpy()
+    fin = np.isfinite(t)
+    assert np.array_equal(f[fin].view(np.uint32), t[fin].view(np.uint32))
+
+
+# ---- linear ------------------------------------------------------------------
+@pytest.mark.skipif(not REF, reason="oracle/_ref not built (no reference)")
+def test_linear_equals_reference_on_its_test_inputs():
+    # tests/u15-kernels-test.cc:433-455: M=9 K=64 N=48, seeds 31/32.
+    x = oracle.randn_mt(31, 9 * 64).reshape(9, 64)
+    w = oracle.randn_mt(32, 48 * 64).reshape(48, 64)
+    ours = oracle.linear(x, w)
+    ref = oracle.ref_linear(x, w)
+    assert np.array_equal(ours, ref)          # same double accumulation
+    b = oracle.randn_mt(5, 48)
+    assert np.array_equal(oracle.linear(x, w, b), oracle.ref_linear(x, w, b))
+
+
+@pytest.mark.skipif(not REF, reason="oracle/_ref not built (no reference)")
+def test_linear_equals_reference_random_shapes():
+    rng = np.random.default_rng(1)
+    for (M, K, N) in [(1, 1, 8), (7, 130, 24), (33, 512, 40)]:
+        x = rng.standard_normal((M, K), dtype=np.float32)
+        w = rng.standard_normal((N, K), dtype=np.float32)
+        assert np.array_equal(oracle.linear(x, w), oracle.ref_linear(x, w))
+
+
+def test_golden_linear_case(golden):
+    g = golden("linear_test_case.npz")
+    # the generator reproduces the reference test's inputs exactly
+    assert np.array_equal(oracle.randn_mt(31, 9 * 64).reshape(9, 64), g["x"])
+    assert np.array_equal(oracle.linear(g["x"], g["w"]), g["y_ref"])
+    assert np.array_equal(oracle.linear_bf16(g["x_bf16"], g["w_bf16"]),
+                          g["y_ref_bf16in"])
+    assert np.array_equal(
+        oracle.linear_bf16(g["x_bf16"], g["w_bf16"], g["bias_bf16"]),
+        g["y_ref_bias"])
+
+
+def test_golden_mot_case(golden):
+    g = golden("mot_linear_case.npz")
+    mu, mg = (int(v) for v in g["m"])
+    y = oracle.mot_linear_bf16(g["x"], g["w_und"], g["w_gen"], mu, mg)
+    assert np.array_equal(y, g["y_ref"])
+    # exchange control: the two weight sets are not interchangeable
+    y_swapped = oracle.mot_linear_bf16(g["x"], g["w_gen"], g["w_und"], mu, mg)
+    assert oracle.rel_l2(y_swapped, g["y_ref"]) > 0.5
+
+
+def test_linear_closed_forms():
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((5, 16), dtype=np.float32)
+    # identity and permutation weights gather x exactly
+    assert np.array_equal(oracle.linear(x, np.eye(16, dtype=np.float32)), x)
+    perm = rng.permutation(16)
+    assert np.array_equal(oracle.linear(x, np.eye(16, dtype=np.float32)[perm]),
+                          x[:, perm])
+    # K=1: an outer product, exact in f32 after one rounding
+    a = rng.standard_normal((6, 1), dtype=np.float32)
+    b = rng.standard_normal((9, 1), dtype=np.float32)
+    assert np.array_equal(oracle.linear(a, b),
+                          (a.astype(np.float64) @ b.T.astype(np.float64)).astype(np.float32))
+    # small integers: exact
+    xi = rng.integers(-8, 9, (4, 40)).astype(np.float32)
+    wi = rng.integers(-8, 9, (12, 40)).astype(np.float32)
+    exact = (xi.astype(np.int64) @ wi.T.astype(np.int64)).astype(np.float32)
+    assert np.array_equal(oracle.linear(xi, wi), exact)
+    # bias is added once, not per term; a transposed operand would fail
+    bias = np.arange(12, dtype=np.float32)
+    assert np.array_equal(oracle.linear(xi, wi, bias), exact + bias)
+    xr = rng.integers(-8, 9, (3, 5)).astype(np.float32)
+    wr = rng.integers(-8, 9, (7, 5)).astype(np.float32)
+    assert np.array_equal(oracle.linear(xr, wr),
+                          (xr.astype(np.int64) @ wr.T.astype(np.int64)).astype(np.float32))
+
+
+def test_linear_bf16_row_subset():
+    rng = np.random.default_rng(3)
+    x = torch_bf16_bits(rng.standard_normal((10, 24), dtype=np.float32))
+    w = torch_bf16_bits(rng.standard_normal((8, 24), dtype=np.float32))
+    full = oracle.linear_bf16(x, w)
+    ids = np.array([9, 0, 4], np.int32)
+    assert np.array_equal(oracle.linear_bf16(x, w, row_ids=ids), full[ids])
+
+
+# ---- silu / swiglu --------------------------------------------------------
+@pytest.mark.skipif(not REF, reason="oracle/_ref not built (no reference)")
+def test_silu_equals_reference():
+    x = np.linspace(-30, 30, 4001, dtype=np.float32)
+    assert np.array_equal(oracle.silu(x), oracle.ref_silu(x))
+
+
+def test_silu_closed_forms():
+    assert oracle.silu(np.array([0.0], np.float32))[0] == 0.0
+    big = np.array([40.0, 80.0], np.float32)
+    assert np.array_equal(oracle.silu(big), big)      # sigmoid -> 1
+    x = np.linspace(0.1, 8, 200, dtype=np.float32)
+    # silu(x) - silu(-x) = x (to f32 rounding of each term)
+    d = oracle.silu(x).astype(np.float64) - oracle.silu(-x).astype(np.float64)
+    assert np.max(np.abs(d - x)) < 2e-6 * 8
+
+
+def test_golden_swiglu(golden):
+    g = golden("swiglu_case.npz")
+    assert np.array_equal(oracle.swiglu_bf16(g["g_bf16"], g["u_bf16"]),
+                          g["h_ref"])
+
+
+# ---- int8 quantisation -----------------------------------------------------
+def _quant_bruteforce(row_f32):
+    """Exact-rational restatement: s = f32(absmax/127), q = round-half-away
+    of f32(x/s) clamped; f32 divisions are numpy's IEEE divisions."""
+    amax = np.float32(np.max(np.abs(row_f32))) if row_f32.size else np.float32(0)
+    s = np.float32(amax) / np.float32(127.0)
+    q = []
+    for v in row_f32:
+        if s == 0:
+            q.append(0)
+            continue
+        t = Fraction(float(np.float32(v) / s))
+        mag = math.floor(abs(t) + Fraction(1, 2))
+        c = mag if t >= 0 else -mag
+        q.append(max(-127, min(127, c)))
+    return np.array(q, np.int8), np.float32(s)
+
+
+def test_quant_rows_bruteforce():
+    rng = np.random.default_rng(4)
+    rows = [rng.standard_normal(37, dtype=np.float32) * 3,
+            np.zeros(37, np.float32),
+            np.array([0.0] * 36 + [-5.0], np.float32),
+            rng.standard_normal(37, dtype=np.float32) * 1e-30]
+    # exact ties: absmax 127 -> s = 1, so k + 0.5 is a tie
+    rows.append(np.array([127.0, 2.5, -2.5, 0.5, -0.5, 1.5, -126.5] + [0.0] * 30,
+                         np.float32))
+    x = torch_bf16_bits(np.stack(rows))
+    q, s = oracle.quant_rows_i8(x)
+    xf = oracle.bf16_to_f32(x)
+    for r in range(x.shape[0]):
+        qb, sb = _quant_bruteforce(xf[r])
+        assert s[r] == sb
+        assert np.array_equal(q[r], qb), r
+    assert list(q[4][:7]) == [127, 3, -3, 1, -1, 2, -127]
+    assert np.all(q[1] == 0) and s[1] == 0
+
+
+def test_quant_invariants():
+    rng = np.random.default_rng(5)
+    x = torch_bf16_bits(rng.standard_normal((50, 256), dtype=np.float32))
+    q, s = oracle.quant_rows_i8(x)
+    xf = oracle.bf16_to_f32(x)
+    assert np.all(np.abs(q.astype(np.int32)) <= 127)
+    i = np.argmax(np.abs(xf), axis=1)
+    assert np.all(np.abs(q[np.arange(50), i].astype(np.int32)) == 127)
+    # reconstruction error is at most half a step (plus f32 slack)
+    err = np.abs(q.astype(np.float64) * s[:, None] - xf)
+    assert np.all(err <= 0.5 * s[:, None] * (1 + 1e-5))
+
+
+# ---- int8 GEMM ------------------------------------------------------------------
+def test_gemm_i8_bruteforce_and_extremes():
+    rng = np.random.default_rng(6)
+    a = rng.integers(-127, 128, (13, 384), dtype=np.int8)
+    w = rng.integers(-127, 128, (24, 384), dtype=np.int8)
+    ref = a.astype(np.int64) @ w.T.astype(np.int64)
+    assert np.array_equal(oracle.gemm_i8_i32(a, w), ref)
+    ext = np.full((2, 4096), 127, np.int8)
+    ext[1] = -127
+    wext = np.full((3, 4096), 127, np.int8)
+    out = oracle.gemm_i8_i32(ext, wext)
+    assert out[0, 0] == 127 * 127 * 4096 and out[1, 2] == -127 * 127 * 4096
+    ids = np.array([12, 3], np.int32)
+    assert np.array_equal(oracle.gemm_i8_i32(a, w, row_ids=ids), ref[ids])
+
+
+def test_i8_product_sums_identity():
+    rng = np.random.default_rng(7)
+    a = rng.integers(-127, 128, (9, 200), dtype=np.int8)
+    w = rng.integers(-127, 128, (11, 200), dtype=np.int8)
+    full = a.astype(np.int64) @ w.T.astype(np.int64)
+    rs, cs = oracle.i8_product_sums(a, w)
+    assert np.array_equal(rs, full.sum(axis=1))
+    assert np.array_equal(cs, full.sum(axis=0))
+
+
+def test_dequant_against_numpy_f32():
+    rng = np.random.default_rng(8)
+    acc = rng.integers(-2**27, 2**27, (6, 16), dtype=np.int64).astype(np.int32)
+    sa = (rng.random(6, dtype=np.float32) * 0.03).astype(np.float32)
+    sw = (rng.random(16, dtype=np.float32) * 0.001).astype(np.float32)
+    ours = oracle.dequant_bf16(acc, sa, sw)
+    v = (acc.astype(np.float32) * sa[:, None]).astype(np.float32) * sw[None, :]
+    assert np.array_equal(ours, torch_bf16_bits(v.astype(np.float32)))
+    f64 = oracle.dequant_f64(acc, sa, sw)
+    assert np.allclose(f64, acc.astype(np.float64) * sa[:, None] * sw[None, :],
+                       rtol=0, atol=0)
+
+
+def test_quantised_gemm_tracks_bf16_linear():
+    """The int8 tier approximates the bf16 product: at K=4096 with N(0,1)
+    activations and N(0,0.02) weights the dequantised result stays within a
+    few percent rel-L2 of the exact product."""
+    rng = np.random.default_rng(9)
+    x = torch_bf16_bits(rng.standard_normal((4, 4096), dtype=np.float32))
+    w = torch_bf16_bits(rng.standard_normal((32, 4096), dtype=np.float32) * 0.02)
+    xq, sx = oracle.quant_rows_i8(x)
+    wq, sw = oracle.quant_rows_i8(w)
+    y = oracle.dequant_f64(oracle.gemm_i8_i32(xq, wq), sx, sw)
+    ref = oracle.linear_bf16(x, w)
+    assert oracle.rel_l2(y.astype(np.float32), ref) < 0.03

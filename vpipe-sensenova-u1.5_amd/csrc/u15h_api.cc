@@ -1,0 +1,622 @@
+// u15h_api.cc -- the C ABI (include/u15h.h) over the gfx950 kernels.
+//
+// Host side of the boundary: argument checks (nothing is launched on a
+// refusal), the batch tables the kernels read, the int8 tier's on/decline
+// state and its grow-only scratch.
+#include "u15h.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "u15h_internal.h"
+
+struct u15h_ctx {
+  int device = 0;
+  bool i8_on = false;
+  int i8_min_m = 1024;
+  // Grow-only scratch of the int8 route of u15h_linear: activation and
+  // weight codes + scales.
+  void* i8_scratch = nullptr;
+  size_t i8_scratch_bytes = 0;
+  std::string err;
+};
+
+namespace {
+
+using u15h::Epi;
+using u15h::GemmBatch;
+using u15h::GemmProblem;
+
+u15h_status
+fail(u15h_ctx* ctx, u15h_status st, const char* fmt, ...)
+{
+  if (ctx != nullptr) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    ctx->err = buf;
+  }
+  return st;
+}
+
+bool
+aligned16(const void* p)
+{
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+// Makes the context's device current for the calling thread.
+u15h_status
+bind_device(u15h_ctx* ctx)
+{
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess) {
+    return fail(ctx, U15H_ENODEV, "hipGetDevice failed");
+  }
+  if (cur != ctx->device && hipSetDevice(ctx->device) != hipSuccess) {
+    return fail(ctx, U15H_ENODEV, "hipSetDevice(%d) failed", ctx->device);
+  }
+  return U15H_OK;
+}
+
+u15h_status
+launched(u15h_ctx* ctx, hipError_t e, const char* what)
+{
+  if (e != hipSuccess) {
+    return fail(ctx, U15H_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
+  }
+  ctx->err.clear();
+  return U15H_OK;
+}
+
+// Appends one problem (one weight set applied to one row range) to a
+// batch.  Empty row ranges add no tiles.
+void
+add_problem(GemmBatch& b, const void* a, const void* w, const void* w2,
+            void* y, const uint16_t* bias, const float* sa, const float* sw,
+            int rows, int n, int ldy, int tile_cols)
+{
+  if (rows <= 0) { return; }
+  GemmProblem& p = b.p[b.nprob++];
+  p.a = a;
+  p.w = w;
+  p.w2 = w2;
+  p.y = y;
+  p.bias = bias;
+  p.sa = sa;
+  p.sw = sw;
+  p.rows = rows;
+  p.n = n;
+  p.ldy = ldy;
+  p.tiles_m = (rows + u15h::kBM - 1) / u15h::kBM;
+  p.tiles_n = (n + tile_cols - 1) / tile_cols;
+  p.tile_begin = b.total_tiles;
+  b.total_tiles += p.tiles_m * p.tiles_n;
+}
+
+GemmBatch
+empty_batch(int kbytes)
+{
+  GemmBatch b;
+  std::memset(&b, 0, sizeof b);
+  b.kbytes = kbytes;
+  return b;
+}
+
+// Shape limits shared by every GEMM entry point.  Byte offsets inside a
+// tile are 32-bit, so one row of K may be at most 2^31 / 256 / 2 bytes.
+u15h_status
+check_k(u15h_ctx* ctx, int K, int elem, int kmult)
+{
+  if (K <= 0 || K % kmult != 0) {
+    return fail(ctx, U15H_EINVAL, "K=%d must be a positive multiple of %d", K,
+                kmult);
+  }
+  if ((long long)K * elem > (1 << 22)) {
+    return fail(ctx, U15H_EINVAL, "K=%d too large", K);
+  }
+  return U15H_OK;
+}
+
+u15h_status
+check_rows(u15h_ctx* ctx, int M_und, int M_gen)
+{
+  if (M_und < 0 || M_gen < 0) {
+    return fail(ctx, U15H_EINVAL, "negative row count (M_und=%d M_gen=%d)",
+                M_und, M_gen);
+  }
+  if ((long long)M_und + M_gen > (1 << 24)) {
+    return fail(ctx, U15H_EINVAL, "too many rows");
+  }
+  return U15H_OK;
+}
+
+u15h_status
+check_n(u15h_ctx* ctx, int N)
+{
+  if (N <= 0 || N % 8 != 0) {
+    return fail(ctx, U15H_EINVAL, "N=%d must be a positive multiple of 8", N);
+  }
+  return U15H_OK;
+}
+
+// Grid-size guard: the tile count must fit a 1-D grid.
+u15h_status
+check_tiles(u15h_ctx* ctx, const GemmBatch& b)
+{
+  if (b.total_tiles < 0 || b.total_tiles > (1 << 30)) {
+    return fail(ctx, U15H_EINVAL, "tile count out of range");
+  }
+  return U15H_OK;
+}
+
+int
+env_int(const char* name, int dflt)
+{
+  const char* s = std::getenv(name);
+  if (s == nullptr || *s == '\0') { return dflt; }
+  return std::atoi(s);
+}
+
+hipStream_t
+as_stream(u15h_stream s)
+{
+  return reinterpret_cast<hipStream_t>(s);
+}
+
+// The int8 route of u15h_linear: quantise x per row and w per output
+// channel into the context's scratch, then the int8 GEMM with the fused
+// dequant epilogue.
+u15h_status
+linear_i8_route(u15h_ctx* ctx, hipStream_t s, const u15h_bf16* x,
+                const u15h_bf16* w, const u15h_bf16* bias, u15h_bf16* y,
+                int M, int K, int N)
+{
+  const size_t xq = (size_t)M * K, wq = (size_t)N * K;
+  const size_t off_wq = (xq + 255) & ~size_t(255);
+  const size_t off_sx = (off_wq + wq + 255) & ~size_t(255);
+  const size_t off_sw = (off_sx + (size_t)M * 4 + 255) & ~size_t(255);
+  const size_t need = off_sw + (size_t)N * 4;
+  if (ctx->i8_scratch_bytes < need) {
+    if (ctx->i8_scratch != nullptr) {
+      // The old scratch may still be read by queued work on `s`.
+      (void)hipStreamSynchronize(s);
+      (void)hipFree(ctx->i8_scratch);
+      ctx->i8_scratch = nullptr;
+      ctx->i8_scratch_bytes = 0;
+    }
+    if (hipMalloc(&ctx->i8_scratch, need) != hipSuccess) {
+      ctx->i8_scratch = nullptr;
+      return fail(ctx, U15H_ENOMEM, "int8 scratch of %zu bytes", need);
+    }
+    ctx->i8_scratch_bytes = need;
+  }
+  char* base = static_cast<char*>(ctx->i8_scratch);
+  int8_t* xqp = reinterpret_cast<int8_t*>(base);
+  int8_t* wqp = reinterpret_cast<int8_t*>(base + off_wq);
+  float* sx = reinterpret_cast<float*>(base + off_sx);
+  float* sw = reinterpret_cast<float*>(base + off_sw);
+  hipError_t e = u15h::launch_quant_rows_i8(x, M, K, xqp, sx, s);
+  if (e == hipSuccess) { e = u15h::launch_quant_rows_i8(w, N, K, wqp, sw, s); }
+  if (e != hipSuccess) { return launched(ctx, e, "quant_rows_i8"); }
+  GemmBatch b = empty_batch(K);
+  add_problem(b, xqp, wqp, nullptr, y, bias, sx, sw, M, N, N,
+              u15h::tile_cols(Epi::kDequantBf16));
+  return launched(ctx, u15h::launch_gemm_i8(b, Epi::kDequantBf16, s),
+                  "gemm_i8");
+}
+
+}  // namespace
+
+extern "C" {
+
+int
+u15h_abi_version(void)
+{
+  return U15H_ABI_VERSION;
+}
+
+const char*
+u15h_status_str(u15h_status s)
+{
+  switch (s) {
+    case U15H_OK: return "ok";
+    case U15H_EINVAL: return "invalid argument";
+    case U15H_ENODEV: return "no usable gfx950 device";
+    case U15H_ELAUNCH: return "launch failed";
+    case U15H_ENOMEM: return "out of device memory";
+  }
+  return "unknown status";
+}
+
+u15h_status
+u15h_create(int device, u15h_ctx** out)
+{
+  if (out == nullptr) { return U15H_EINVAL; }
+  *out = nullptr;
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+    return U15H_ENODEV;
+  }
+  if (device < 0 || device >= count) { return U15H_EINVAL; }
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) {
+    return U15H_ENODEV;
+  }
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+    return U15H_ENODEV;
+  }
+  int prev = -1;
+  (void)hipGetDevice(&prev);
+  if (hipSetDevice(device) != hipSuccess) { return U15H_ENODEV; }
+  // Every kernel must load: a missing one is a refusal, not a silent no-op
+  // (the reference validates every function at init,
+  // src/u15-metal-ops.cc:205-243).
+  const bool ok = u15h::kernels_loadable();
+  if (prev >= 0 && prev != device) { (void)hipSetDevice(prev); }
+  if (!ok) { return U15H_ENODEV; }
+  u15h_ctx* ctx = new u15h_ctx;
+  ctx->device = device;
+  ctx->i8_min_m = std::max(1, env_int("U15H_I8_MIN_M", 1024));
+  *out = ctx;
+  return U15H_OK;
+}
+
+void
+u15h_destroy(u15h_ctx* ctx)
+{
+  if (ctx == nullptr) { return; }
+  u15h_release_i8_scratch(ctx);
+  delete ctx;
+}
+
+const char*
+u15h_last_error(const u15h_ctx* ctx)
+{
+  return ctx != nullptr ? ctx->err.c_str() : "null context";
+}
+
+u15h_status
+u15h_linear(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
+            const u15h_bf16* w, const u15h_bf16* bias, u15h_bf16* y, int M,
+            int K, int N)
+{
+  if (ctx == nullptr) { return U15H_EINVAL; }
+  if (M < 0) { return fail(ctx, U15H_EINVAL, "M=%d", M); }
+  u15h_status st = check_k(ctx, K, 2, 8);
+  if (st == U15H_OK) { st = check_n(ctx, N); }
+  if (st == U15H_OK) { st = check_rows(ctx, M, 0); }
+  if (st != U15H_OK) { return st; }
+  if (M == 0) { ctx->err.clear(); return U15H_OK; }
+  if (x == nullptr || w == nullptr || y == nullptr) {
+    return fail(ctx, U15H_EINVAL, "null x/w/y");
+  }
+  if (!aligned16(x) || !aligned16(w) || !aligned16(y) ||
+      (bias != nullptr && !aligned16(bias))) {
+    return fail(ctx, U15H_EINVAL, "pointers must be 16-byte aligned");
+  }
+  if ((st = bind_device(ctx)) != U15H_OK) { return st; }
+  hipStream_t s = as_stream(stream);
+  // The int8 interception, as MetalOps::linear_mma_ does it
+  // (src/u15-metal-ops.cc:291-306): taken only when the tier is on and the
+  // shape qualifies; otherwise the bf16 path runs exactly as before.
+  if (ctx->i8_on && M >= ctx->i8_min_m && K % 128 == 0) {
+    return linear_i8_route(ctx, s, x, w, bias, y, M, K, N);
+  }
+  GemmBatch b = empty_batch(K * 2);
+  add_problem(b, x, w, nullptr, y, bias, nullptr, nullptr, M, N, N,
+              u15h::tile_cols(Epi::kBf16));
+  return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kBf16, s), "gemm_bf16");
+}
+
+u15h_status
+u15h_mot_linear(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
+                int M_und, int M_gen, int K, const u15h_mot_proj* proj,
+                int nproj)
+{
+  if (ctx == nullptr) { return U15H_EINVAL; }
+  u15h_status st = check_k(ctx, K, 2, 8);
+  if (st == U15H_OK) { st = check_rows(ctx, M_und, M_gen); }
+  if (st != U15H_OK) { return st; }
+  if (proj == nullptr || nproj < 1 || nproj > U15H_MAX_PROJ) {
+    return fail(ctx, U15H_EINVAL, "nproj=%d must be in [1, %d]", nproj,
+                U15H_MAX_PROJ);
+  }
+  if (M_und + M_gen > 0 && (x == nullptr || !aligned16(x))) {
+    return fail(ctx, U15H_EINVAL, "x null or misaligned");
+  }
+  for (int i = 0; i < nproj; ++i) {
+    const u15h_mot_proj& p = proj[i];
+    if ((st = check_n(ctx, p.N)) != U15H_OK) { return st; }
+    if (p.y == nullptr || !aligned16(p.y)) {
+      return fail(ctx, U15H_EINVAL, "proj[%d].y null or misaligned", i);
+    }
+    if (M_und > 0 && (p.w_und == nullptr || !aligned16(p.w_und) ||
+                      (p.bias_und != nullptr && !aligned16(p.bias_und)))) {
+      return fail(ctx, U15H_EINVAL, "proj[%d] und weights", i);
+    }
+    if (M_gen > 0 && (p.w_gen == nullptr || !aligned16(p.w_gen) ||
+                      (p.bias_gen != nullptr && !aligned16(p.bias_gen)))) {
+      return fail(ctx, U15H_EINVAL, "proj[%d] gen weights", i);
+    }
+  }
+  if (M_und + M_gen == 0) { ctx->err.clear(); return U15H_OK; }
+  if ((st = bind_device(ctx)) != U15H_OK) { return st; }
+  const int tc = u15h::tile_cols(Epi::kBf16);
+  const size_t kb = (size_t)K * 2;
+  GemmBatch b = empty_batch(K * 2);
+  // Gen problems first: they are the bulk of the tiles; the small und
+  // group fills in behind them.
+  for (int i = 0; i < nproj; ++i) {
+    const u15h_mot_proj& p = proj[i];
+    add_problem(b, reinterpret_cast<const char*>(x) + (size_t)M_und * kb,
+                p.w_gen, nullptr, p.y + (size_t)M_und * p.N, p.bias_gen,
+                nullptr, nullptr, M_gen, p.N, p.N, tc);
+  }
+  for (int i = 0; i < nproj; ++i) {
+    const u15h_mot_proj& p = proj[i];
+    add_problem(b, x, p.w_und, nullptr, p.y, p.bias_und, nullptr, nullptr,
+                M_und, p.N, p.N, tc);
+  }
+  if ((st = check_tiles(ctx, b)) != U15H_OK) { return st; }
+  return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kBf16, as_stream(stream)),
+                  "mot_gemm_bf16");
+}
+
+u15h_status
+u15h_swiglu(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* gate,
+            const u15h_bf16* up, u15h_bf16* out, int64_t n)
+{
+  if (ctx == nullptr) { return U15H_EINVAL; }
+  if (n < 0 || n % 8 != 0) {
+    return fail(ctx, U15H_EINVAL, "n=%lld must be a multiple of 8",
+                (long long)n);
+  }
+  if (n == 0) { ctx->err.clear(); return U15H_OK; }
+  if (gate == nullptr || up == nullptr || out == nullptr ||
+      !aligned16(gate) || !aligned16(up) || !aligned16(out)) {
+    return fail(ctx, U15H_EINVAL, "null or misaligned swiglu operand");
+  }
+  u15h_status st = bind_device(ctx);
+  if (st != U15H_OK) { return st; }
+  return launched(ctx, u15h::launch_swiglu(gate, up, out, n, as_stream(stream)),
+                  "swiglu");
+}
+
+u15h_status
+u15h_mot_gate_up_swiglu(u15h_ctx* ctx, u15h_stream stream,
+                        const u15h_bf16* x, int M_und, int M_gen, int K,
+                        const u15h_bf16* wg_und, const u15h_bf16* wu_und,
+                        const u15h_bf16* wg_gen, const u15h_bf16* wu_gen,
+                        u15h_bf16* h, int I)
+{
+  if (ctx == nullptr) { return U15H_EINVAL; }
+  u15h_status st = check_k(ctx, K, 2, 8);
+  if (st == U15H_OK) { st = check_rows(ctx, M_und, M_gen); }
+  if (st == U15H_OK) { st = check_n(ctx, I); }
+  if (st != U15H_OK) { return st; }
+  if (M_und + M_gen == 0) { ctx->err.clear(); return U15H_OK; }
+  if (x == nullptr || h == nullptr || !aligned16(x) || !aligned16(h)) {
+    return fail(ctx, U15H_EINVAL, "x/h null or misaligned");
+  }
+  if (M_und > 0 && (wg_und == nullptr || wu_und == nullptr ||
+                    !aligned16(wg_und) || !aligned16(wu_und))) {
+    return fail(ctx, U15H_EINVAL, "und gate/up weights");
+  }
+  if (M_gen > 0 && (wg_gen == nullptr || wu_gen == nullptr ||
+                    !aligned16(wg_gen) || !aligned16(wu_gen))) {
+    return fail(ctx, U15H_EINVAL, "gen gate/up weights");
+  }
+  if ((st = bind_device(ctx)) != U15H_OK) { return st; }
+  const int tc = u15h::tile_cols(Epi::kSwiglu);
+  const size_t kb = (size_t)K * 2;
+  GemmBatch b = empty_batch(K * 2);
+  add_problem(b, reinterpret_cast<const char*>(x) + (size_t)M_und * kb,
+              wg_gen, wu_gen, h + (size_t)M_und * I, nullptr, nullptr,
+              nullptr, M_gen, I, I, tc);
+  add_problem(b, x, wg_und, wu_und, h, nullptr, nullptr, nullptr, M_und, I, I,
+              tc);
+  if ((st = check_tiles(ctx, b)) != U15H_OK) { return st; }
+  return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kSwiglu, as_stream(stream)),
+                  "mot_gate_up_swiglu");
+}
+
+int
+u15h_enable_i8_gemm(u15h_ctx* ctx, int want)
+{
+  if (ctx == nullptr) { return 0; }
+  // U15H_I8_GEMM overrides `want` either way, which is how an A/B is run
+  // without touching the caller (src/u15-metal-ops.h:85-92).
+  const char* e = std::getenv("U15H_I8_GEMM");
+  bool on = want != 0;
+  if (e != nullptr && *e != '\0') { on = std::atoi(e) != 0; }
+  ctx->i8_on = on;
+  if (!on) { u15h_release_i8_scratch(ctx); }
+  return ctx->i8_on ? 1 : 0;
+}
+
+void
+u15h_release_i8_scratch(u15h_ctx* ctx)
+{
+  if (ctx == nullptr || ctx->i8_scratch == nullptr) { return; }
+  // Queued work may still read it.
+  (void)hipDeviceSynchronize();
+  (void)hipFree(ctx->i8_scratch);
+  ctx->i8_scratch = nullptr;
+  ctx->i8_scratch_bytes = 0;
+}
+
+int
+u15h_i8_min_m(const u15h_ctx* ctx)
+{
+  return ctx != nullptr ? ctx->i8_min_m : 0;
+}
+
+u15h_status
+u15h_quant_rows_i8(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
+                   int rows, int K, int8_t* q, float* s)
+{
+  if (ctx == nullptr) { return U15H_EINVAL; }
+  if (rows < 0 || K <= 0 || K % 8 != 0) {
+    return fail(ctx, U15H_EINVAL, "rows=%d K=%d (K must be a multiple of 8)",
+                rows, K);
+  }
+  if (rows == 0) { ctx->err.clear(); return U15H_OK; }
+  if (x == nullptr || q == nullptr || s == nullptr || !aligned16(x) ||
+      !aligned16(q) || !aligned16(s)) {
+    return fail(ctx, U15H_EINVAL, "null or misaligned quant operand");
+  }
+  u15h_status st = bind_device(ctx);
+  if (st != U15H_OK) { return st; }
+  return launched(
+      ctx, u15h::launch_quant_rows_i8(x, rows, K, q, s, as_stream(stream)),
+      "quant_rows_i8");
+}
+
+static u15h_status
+mot_gemm_i8_common(u15h_ctx* ctx, u15h_stream stream, const int8_t* xq,
+                   const float* sx, int M_und, int M_gen, int K,
+                   const u15h_mot_proj_i8* proj, int nproj, Epi epi)
+{
+  if (ctx == nullptr) { return U15H_EINVAL; }
+  u15h_status st = check_k(ctx, K, 1, 128);
+  if (st == U15H_OK && K > 131072) {
+    st = fail(ctx, U15H_EINVAL, "K=%d: int32 accumulation is exact only "
+                                "up to K=131072", K);
+  }
+  if (st == U15H_OK) { st = check_rows(ctx, M_und, M_gen); }
+  if (st != U15H_OK) { return st; }
+  if (proj == nullptr || nproj < 1 || nproj > U15H_MAX_PROJ) {
+    return fail(ctx, U15H_EINVAL, "nproj=%d must be in [1, %d]", nproj,
+                U15H_MAX_PROJ);
+  }
+  const bool deq = epi == Epi::kDequantBf16;
+  if (M_und + M_gen > 0 &&
+      (xq == nullptr || !aligned16(xq) || (deq && (sx == nullptr)))) {
+    return fail(ctx, U15H_EINVAL, "xq/sx null or misaligned");
+  }
+  for (int i = 0; i < nproj; ++i) {
+    const u15h_mot_proj_i8& p = proj[i];
+    if ((st = check_n(ctx, p.N)) != U15H_OK) { return st; }
+    if (p.y == nullptr || !aligned16(p.y)) {
+      return fail(ctx, U15H_EINVAL, "proj[%d].y null or misaligned", i);
+    }
+    if (M_und > 0 && (p.wq_und == nullptr || !aligned16(p.wq_und) ||
+                      (deq && (p.sw_und == nullptr || !aligned16(p.sw_und))))) {
+      return fail(ctx, U15H_EINVAL, "proj[%d] und weights/scales", i);
+    }
+    if (M_gen > 0 && (p.wq_gen == nullptr || !aligned16(p.wq_gen) ||
+                      (deq && (p.sw_gen == nullptr || !aligned16(p.sw_gen))))) {
+      return fail(ctx, U15H_EINVAL, "proj[%d] gen weights/scales", i);
+    }
+  }
+  if (M_und + M_gen == 0) { ctx->err.clear(); return U15H_OK; }
+  if ((st = bind_device(ctx)) != U15H_OK) { return st; }
+  const int tc = u15h::tile_cols(epi);
+  const size_t esz = deq ? 2 : 4;
+  GemmBatch b = empty_batch(K);
+  for (int i = 0; i < nproj; ++i) {
+    const u15h_mot_proj_i8& p = proj[i];
+    add_problem(b, xq + (size_t)M_und * K, p.wq_gen, nullptr,
+                static_cast<char*>(p.y) + (size_t)M_und * p.N * esz, nullptr,
+                deq ? sx + M_und : nullptr, deq ? p.sw_gen : nullptr, M_gen,
+                p.N, p.N, tc);
+  }
+  for (int i = 0; i < nproj; ++i) {
+    const u15h_mot_proj_i8& p = proj[i];
+    add_problem(b, xq, p.wq_und, nullptr, p.y, nullptr, deq ? sx : nullptr,
+                deq ? p.sw_und : nullptr, M_und, p.N, p.N, tc);
+  }
+  if ((st = check_tiles(ctx, b)) != U15H_OK) { return st; }
+  return launched(ctx, u15h::launch_gemm_i8(b, epi, as_stream(stream)),
+                  deq ? "mot_gemm_i8" : "mot_gemm_i8_i32");
+}
+
+u15h_status
+u15h_mot_gemm_i8_i32(u15h_ctx* ctx, u15h_stream stream, const int8_t* xq,
+                     int M_und, int M_gen, int K,
+                     const u15h_mot_proj_i8* proj, int nproj)
+{
+  return mot_gemm_i8_common(ctx, stream, xq, nullptr, M_und, M_gen, K, proj,
+                            nproj, Epi::kI32);
+}
+
+u15h_status
+u15h_mot_gemm_i8(u15h_ctx* ctx, u15h_stream stream, const int8_t* xq,
+                 const float* sx, int M_und, int M_gen, int K,
+                 const u15h_mot_proj_i8* proj, int nproj)
+{
+  return mot_gemm_i8_common(ctx, stream, xq, sx, M_und, M_gen, K, proj, nproj,
+                            Epi::kDequantBf16);
+}
+
+u15h_status
+u15h_route_rows(const uint8_t* expert, int M, int32_t* perm, int* M_und,
+                int* M_gen)
+{
+  if (M < 0 || (M > 0 && (expert == nullptr || perm == nullptr)) ||
+      M_und == nullptr || M_gen == nullptr) {
+    return U15H_EINVAL;
+  }
+  int nu = 0;
+  for (int i = 0; i < M; ++i) {
+    if (expert[i] > 1) { return U15H_EINVAL; }
+    if (expert[i] == 0) { ++nu; }
+  }
+  // Stable partition: und tokens first, then gen, original order kept.
+  int iu = 0, ig = nu;
+  for (int i = 0; i < M; ++i) {
+    if (expert[i] == 0) { perm[iu++] = i; } else { perm[ig++] = i; }
+  }
+  *M_und = nu;
+  *M_gen = M - nu;
+  return U15H_OK;
+}
+
+static u15h_status
+gather_common(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* src,
+              const int32_t* perm, int M, int cols, u15h_bf16* dst,
+              bool scatter)
+{
+  if (ctx == nullptr) { return U15H_EINVAL; }
+  if (M < 0 || cols <= 0 || cols % 8 != 0) {
+    return fail(ctx, U15H_EINVAL, "M=%d cols=%d (cols must be a multiple of 8)",
+                M, cols);
+  }
+  if (M == 0) { ctx->err.clear(); return U15H_OK; }
+  if (src == nullptr || perm == nullptr || dst == nullptr ||
+      !aligned16(src) || !aligned16(dst)) {
+    return fail(ctx, U15H_EINVAL, "null or misaligned gather operand");
+  }
+  u15h_status st = bind_device(ctx);
+  if (st != U15H_OK) { return st; }
+  return launched(ctx,
+                  u15h::launch_gather_rows(src, perm, M, cols, dst, scatter,
+                                           as_stream(stream)),
+                  scatter ? "scatter_rows" : "gather_rows");
+}
+
+u15h_status
+u15h_gather_rows(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* src,
+                 const int32_t* perm, int M, int cols, u15h_bf16* dst)
+{
+  return gather_common(ctx, stream, src, perm, M, cols, dst, false);
+}
+
+u15h_status
+u15h_scatter_rows(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* src,
+                  const int32_t* perm, int M, int cols, u15h_bf16* dst)
+{
+  return gather_common(ctx, stream, src, perm, M, cols, dst, true);
+}
+
+}  // extern "C"

@@ -1,0 +1,70 @@
+// u15h_internal.h -- shared definitions between the C-ABI layer and the
+// gfx950 kernels.  Not installed; the public surface is include/u15h.h.
+#ifndef U15H_INTERNAL_H
+#define U15H_INTERNAL_H
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+namespace u15h {
+
+// Output tile of one workgroup and the K bytes staged per LDS stage.
+// 128 bytes of K is 64 bf16 or 128 int8: both element types share one
+// LDS byte layout and one load schedule; only the MFMA differs.
+constexpr int kBM = 256;          // activation rows per tile
+constexpr int kBN = 256;          // weight rows (output columns) per tile
+constexpr int kKB = 128;          // bytes of K per stage
+constexpr int kThreads = 256;     // 4 waves of 64
+constexpr int kMaxProb = 8;       // problems (weight sets x projections) per launch
+
+// What the epilogue does with the fp32 / int32 accumulators.
+enum class Epi : int {
+  kBf16 = 0,         // y = bf16_rne(acc (+ bias))                 [bf16 GEMM]
+  kI32 = 1,          // y = acc (int32)                            [int8 GEMM]
+  kDequantBf16 = 2,  // y = bf16_rne((float(acc)*sa[m])*sw[n] (+ bias))
+  kSwiglu = 3,       // y = bf16(silu(bf16(g)) * bf16(u)), gate/up tile pairs
+};
+
+// One GEMM of a batch: y[rows][n] = a[rows][K] . w[n][K]^T.
+struct GemmProblem {
+  const void*     a;      // activation rows [rows][K]
+  const void*     w;      // weight rows [n][K]  (gate rows for kSwiglu)
+  const void*     w2;     // up rows [n][K] for kSwiglu, else unused
+  void*           y;      // output rows, ldy elements apart
+  const uint16_t* bias;   // bf16 [n] or null
+  const float*    sa;     // per-row scale [rows] (kDequantBf16)
+  const float*    sw;     // per-column scale [n] (kDequantBf16)
+  int rows;               // activation rows of this problem
+  int n;                  // output columns of this problem
+  int ldy;                // output row pitch in elements
+  int tiles_m;            // ceil(rows / kBM)
+  int tiles_n;            // ceil(n / tile columns)
+  int tile_begin;         // first linear tile index of this problem
+};
+
+struct GemmBatch {
+  GemmProblem p[kMaxProb];
+  int nprob;
+  int kbytes;             // bytes per activation / weight row (K * elem size)
+  int total_tiles;
+};
+
+// Kernel launchers (u15h_kernels.hip).  All are asynchronous on `s`.
+hipError_t launch_gemm_bf16(const GemmBatch& b, Epi epi, hipStream_t s);
+hipError_t launch_gemm_i8(const GemmBatch& b, Epi epi, hipStream_t s);
+hipError_t launch_quant_rows_i8(const uint16_t* x, int rows, int K,
+                                int8_t* q, float* sc, hipStream_t s);
+hipError_t launch_swiglu(const uint16_t* g, const uint16_t* u, uint16_t* o,
+                         int64_t n, hipStream_t s);
+hipError_t launch_gather_rows(const uint16_t* src, const int32_t* perm,
+                              int M, int cols, uint16_t* dst, bool scatter,
+                              hipStream_t s);
+// Forces every kernel's code object to load; false if any cannot.
+bool kernels_loadable();
+
+// Tile columns per tile for an epilogue (kSwiglu tiles produce half).
+constexpr int tile_cols(Epi e) { return e == Epi::kSwiglu ? kBN / 2 : kBN; }
+
+}  // namespace u15h
+
+#endif

@@ -1,0 +1,531 @@
+// u15h_kernels.hip -- gfx950 (CDNA4) kernels for the MoT projection GEMMs.
+//
+// The GEMM (mot_gemm_kernel) computes y = a . w^T for a batch of up to
+// kMaxProb problems in ONE launch: the two MoT weight sets of a projection
+// (und rows / gen rows) and several projections sharing an input (q, k, v;
+// gate, up) all become entries of the batch's problem table, which rides in
+// the kernel arguments.  Row-wise every problem is the reference's
+// MetalOps::linear (src/u15-metal-ops.cc:327-346) with one weight set.
+//
+// Tile: 256 activation rows x 256 weight rows, 4 waves of 64 in a 2x2 grid,
+// each wave owning a 128x128 block of 4x4 MFMA 32x32 accumulators.  K is
+// staged through LDS 128 bytes at a time (64 bf16 or 128 int8): both
+// element types share one byte layout, one load schedule and one swizzle;
+// only the MFMA differs (v_mfma_f32_32x32x16_bf16 / v_mfma_i32_32x32x32_i8,
+// each taking 16 bytes of K per lane).
+//
+// Operand order: the WEIGHT fragment is the MFMA's first operand, so the
+// 32x32 accumulator's rows are output columns.  A lane then holds four
+// consecutive output columns of one activation row, which the epilogue
+// stores as one 8-byte (bf16) or 16-byte (int32) write.
+//
+// LDS: two stages of [256 weight rows | 256 activation rows] x 128 bytes.
+// Row r's 16-byte chunk c sits at chunk position c ^ (r & 7), so the eight
+// rows a fragment read touches at one k-chunk land in eight different bank
+// groups, and the 8 lanes that write one row write all eight positions.
+//
+// Global loads use buffer resources sized to the tile's valid rows, so rows
+// past M or N read as zero in hardware; a K tail (K not a multiple of the
+// stage) is zero-filled by pushing the invalid chunks' offsets out of range.
+#include <hip/hip_runtime.h>
+
+#include "u15h_internal.h"
+
+namespace u15h {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x16_t __attribute__((ext_vector_type(16)));
+
+constexpr int kStage = (kBM + kBN) * kKB;   // 64 KiB per LDS stage
+constexpr int kRsrcWord3 = 0x00020000;      // raw buffer, 32-bit data format
+constexpr int kOobOffset = 0x40000000;      // any offset past every resource
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t
+make_rsrc(const void* base, int bytes)
+{
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes,
+                                           kRsrcWord3);
+}
+
+__device__ __forceinline__ i32x4_t
+load16(__amdgpu_buffer_rsrc_t r, int voff, int soff)
+{
+  return __builtin_bit_cast(
+      i32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+__device__ __forceinline__ uint32_t
+bf16_bits(float f)
+{
+  // Round to nearest even; the same rule the oracle and the reference's
+  // weight loader use (finite values).
+  const uint32_t u = __builtin_bit_cast(uint32_t, f);
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float
+bf16_round(float f)
+{
+  return __builtin_bit_cast(float, bf16_bits(f) << 16);
+}
+
+__device__ __forceinline__ float
+bf16_to_f32(uint32_t h)
+{
+  return __builtin_bit_cast(float, h << 16);
+}
+
+struct MmaBf16 {
+  using acc_t = f32x16_t;
+  __device__ static __forceinline__ acc_t run(i32x4_t a, i32x4_t b, acc_t c)
+  {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+        0, 0, 0);
+  }
+};
+
+struct MmaI8 {
+  using acc_t = i32x16_t;
+  __device__ static __forceinline__ acc_t run(i32x4_t a, i32x4_t b, acc_t c)
+  {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+  }
+};
+
+template <class Mma, Epi E>
+__global__ __launch_bounds__(kThreads, 1) void
+mot_gemm_kernel(const GemmBatch B)
+{
+  __shared__ __attribute__((aligned(16))) char lds[2 * kStage];
+
+  // ---- which tile -----------------------------------------------------
+  // Consecutive workgroups are dealt round-robin to the 8 XCDs; remap so
+  // each XCD walks a contiguous run of the tile list (and so shares its
+  // operands in its own L2).
+  const int T = B.total_tiles;
+  const int bid = blockIdx.x;
+  const int lin = (T % 8 == 0) ? (bid % 8) * (T / 8) + bid / 8 : bid;
+  int p = 0;
+#pragma unroll
+  for (int q = 1; q < kMaxProb; ++q) {
+    if (q < B.nprob && lin >= B.p[q].tile_begin) { p = q; }
+  }
+  const GemmProblem& P = B.p[p];
+  // Grouped raster: bands of 4 row-tiles, walked column by column.
+  constexpr int GM = 4;
+  const int t = lin - P.tile_begin;
+  const int per_band = GM * P.tiles_n;
+  const int band = t / per_band;
+  const int first_m = band * GM;
+  const int gm = min(P.tiles_m - first_m, GM);
+  const int tin = t - band * per_band;
+  const int mt = first_m + tin % gm;
+  const int nt = tin / gm;
+  constexpr int TC = tile_cols(E);
+  const int row0 = mt * kBM;
+  const int col0 = nt * TC;
+
+  const int kbytes = B.kbytes;
+  const int nk = (kbytes + kKB - 1) / kKB;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave & 1;
+  const int wn = wave >> 1;
+  const int lrow = tid >> 3;   // row of a 32-row slab this thread loads
+  const int lch = tid & 7;     // 16-byte chunk of the 128-byte stage row
+
+  // ---- operand resources ----------------------------------------------
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(
+      static_cast<const char*>(P.a) + (size_t)row0 * kbytes,
+      min(kBM, P.rows - row0) * kbytes);
+  __amdgpu_buffer_rsrc_t rw, ru;
+  if constexpr (E == Epi::kSwiglu) {
+    const int nvalid = min(TC, P.n - col0) * kbytes;
+    rw = make_rsrc(static_cast<const char*>(P.w) + (size_t)col0 * kbytes,
+                   nvalid);
+    ru = make_rsrc(static_cast<const char*>(P.w2) + (size_t)col0 * kbytes,
+                   nvalid);
+  } else {
+    rw = make_rsrc(static_cast<const char*>(P.w) + (size_t)col0 * kbytes,
+                   min(kBN, P.n - col0) * kbytes);
+    ru = rw;
+  }
+  // Weight slab i (32 LDS rows) comes from which resource and which row.
+  // Plain: rows i*32.. of the weight tile.  SwiGLU: wave column wn owns 64
+  // output columns; its 128 LDS rows are 64 gate rows then the 64 matching
+  // up rows, so a lane's gate and up accumulators cover the same outputs.
+  auto wslab_row = [&](int i) {
+    if constexpr (E == Epi::kSwiglu) {
+      return (i >> 2) * 64 + (i & 1) * 32;
+    } else {
+      return i * 32;
+    }
+  };
+  auto wslab_is_up = [&](int i) {
+    return E == Epi::kSwiglu && ((i >> 1) & 1) != 0;
+  };
+
+  // The range check that zero-fills rows past M / N and the K tail applies
+  // to the per-lane (VGPR) offset, so every row offset is carried there;
+  // only the stage's K offset, common to all rows, rides in the SGPR.
+  const int voff = lrow * kbytes + lch * 16;
+  const int tail_off =
+      ((nk - 1) * kKB + lch * 16 < kbytes) ? 0 : kOobOffset;
+
+  i32x4_t wreg[8], areg[8];
+  auto gload = [&](int kt) {
+    const int ko = kt * kKB;
+    const int v = voff + (kt == nk - 1 ? tail_off : 0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      wreg[i] = load16(wslab_is_up(i) ? ru : rw, v + wslab_row(i) * kbytes, ko);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      areg[i] = load16(ra, v + i * 32 * kbytes, ko);
+    }
+  };
+
+  const int st_off = lrow * kKB + ((lch ^ (lrow & 7)) << 4);
+  auto lstore = [&](int stage) {
+    char* base = lds + stage * kStage;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      *reinterpret_cast<i32x4_t*>(base + i * 32 * kKB + st_off) = wreg[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      *reinterpret_cast<i32x4_t*>(base + kBN * kKB + i * 32 * kKB + st_off) =
+          areg[i];
+    }
+  };
+
+  const int lr = lane & 31;
+  const int lh = lane >> 5;
+  int rd[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    rd[s] = lr * kKB + (((2 * s + lh) ^ (lr & 7)) << 4);
+  }
+  const int wbase = wn * 128 * kKB;
+  const int abase = kBN * kKB + wm * 128 * kKB;
+
+  typename Mma::acc_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { acc[i][j] = typename Mma::acc_t{}; }
+  }
+
+  auto compute = [&](int stage) {
+    const char* base = lds + stage * kStage;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      i32x4_t fa[4], fb[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        fa[i] = *reinterpret_cast<const i32x4_t*>(base + wbase + i * 32 * kKB +
+                                                  rd[s]);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        fb[j] = *reinterpret_cast<const i32x4_t*>(base + abase + j * 32 * kKB +
+                                                  rd[s]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc[i][j] = Mma::run(fa[i], fb[j], acc[i][j]);
+        }
+      }
+    }
+  };
+
+  // ---- main loop: prefetch stage kt+1 into registers while the MFMAs
+  // consume stage kt from LDS; one barrier per stage. -------------------
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) { gload(kt + 1); }
+    compute(cur);
+    if (kt + 1 < nk) { lstore(cur ^ 1); }
+    __syncthreads();
+  }
+
+  // ---- epilogue ---------------------------------------------------------
+  // acc[i][j][r]: output column (within the wave's block) i*32 + (r>>2)*8 +
+  // lh*4 + (r&3), activation row j*32 + lr.
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int m = row0 + wm * 128 + j * 32 + lr;
+    if (m >= P.rows) { continue; }
+    if constexpr (E == Epi::kSwiglu) {
+      uint16_t* yrow = static_cast<uint16_t*>(P.y) + (size_t)m * P.ldy;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = col0 + wn * 64 + i * 32 + g * 8 + lh * 4;
+          if (n >= P.n) { continue; }
+          uint32_t h[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float gv = bf16_round(acc[i][j][g * 4 + e]);
+            const float uv = bf16_round(acc[i + 2][j][g * 4 + e]);
+            const float sv = gv / (1.0f + expf(-gv));
+            h[e] = bf16_bits(sv * uv);
+          }
+          uint2 o;
+          o.x = h[0] | (h[1] << 16);
+          o.y = h[2] | (h[3] << 16);
+          *reinterpret_cast<uint2*>(yrow + n) = o;
+        }
+      }
+    } else if constexpr (E == Epi::kI32) {
+      int32_t* yrow = static_cast<int32_t*>(P.y) + (size_t)m * P.ldy;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = col0 + wn * 128 + i * 32 + g * 8 + lh * 4;
+          if (n >= P.n) { continue; }
+          int4 o;
+          o.x = (int)acc[i][j][g * 4 + 0];
+          o.y = (int)acc[i][j][g * 4 + 1];
+          o.z = (int)acc[i][j][g * 4 + 2];
+          o.w = (int)acc[i][j][g * 4 + 3];
+          *reinterpret_cast<int4*>(yrow + n) = o;
+        }
+      }
+    } else {
+      uint16_t* yrow = static_cast<uint16_t*>(P.y) + (size_t)m * P.ldy;
+      float sam = 1.0f;
+      if constexpr (E == Epi::kDequantBf16) { sam = P.sa[m]; }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = col0 + wn * 128 + i * 32 + g * 8 + lh * 4;
+          if (n >= P.n) { continue; }
+          float v[4];
+          if constexpr (E == Epi::kDequantBf16) {
+            const float4 swn = *reinterpret_cast<const float4*>(P.sw + n);
+            v[0] = ((float)acc[i][j][g * 4 + 0] * sam) * swn.x;
+            v[1] = ((float)acc[i][j][g * 4 + 1] * sam) * swn.y;
+            v[2] = ((float)acc[i][j][g * 4 + 2] * sam) * swn.z;
+            v[3] = ((float)acc[i][j][g * 4 + 3] * sam) * swn.w;
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { v[e] = acc[i][j][g * 4 + e]; }
+          }
+          if (P.bias != nullptr) {
+            const uint2 bb = *reinterpret_cast<const uint2*>(P.bias + n);
+            v[0] += bf16_to_f32(bb.x & 0xffffu);
+            v[1] += bf16_to_f32(bb.x >> 16);
+            v[2] += bf16_to_f32(bb.y & 0xffffu);
+            v[3] += bf16_to_f32(bb.y >> 16);
+          }
+          uint2 o;
+          o.x = bf16_bits(v[0]) | (bf16_bits(v[1]) << 16);
+          o.y = bf16_bits(v[2]) | (bf16_bits(v[3]) << 16);
+          *reinterpret_cast<uint2*>(yrow + n) = o;
+        }
+      }
+    }
+  }
+}
+
+// ---- per-row symmetric int8 quantisation ------------------------------
+// One workgroup per row: absmax over the row (bf16 widened exactly), then
+// q = clamp(round_half_away(x / s), -127, 127) with s = absmax / 127
+// (fp32 division, correctly rounded).
+__global__ __launch_bounds__(256) void
+quant_rows_i8_kernel(const uint16_t* __restrict__ x, int K,
+                     int8_t* __restrict__ q, float* __restrict__ sc)
+{
+  __shared__ float red[4];
+  const int r = blockIdx.x;
+  const uint4* xr = reinterpret_cast<const uint4*>(x + (size_t)r * K);
+  const int nchunk = K / 8;
+  float amax = 0.0f;
+  for (int c = threadIdx.x; c < nchunk; c += 256) {
+    const uint4 v = xr[c];
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      amax = fmaxf(amax, fabsf(bf16_to_f32(w[e] & 0xffffu)));
+      amax = fmaxf(amax, fabsf(bf16_to_f32(w[e] >> 16)));
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) { amax = fmaxf(amax, __shfl_xor(amax, o)); }
+  if ((threadIdx.x & 63) == 0) { red[threadIdx.x >> 6] = amax; }
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float s = amax / 127.0f;
+  if (threadIdx.x == 0) { sc[r] = s; }
+  uint2* qr = reinterpret_cast<uint2*>(q + (size_t)r * K);
+  for (int c = threadIdx.x; c < nchunk; c += 256) {
+    const uint4 v = xr[c];
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t packed[2] = {0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t h = (e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffffu);
+      int cq = 0;
+      if (s != 0.0f) {
+        const float t = bf16_to_f32(h) / s;
+        cq = (int)roundf(t);
+        cq = max(-127, min(127, cq));
+      }
+      packed[e >> 2] |= ((uint32_t)(cq & 0xff)) << ((e & 3) * 8);
+    }
+    qr[c] = make_uint2(packed[0], packed[1]);
+  }
+}
+
+// ---- elementwise SwiGLU: out = silu(g) * u ------------------------------
+__global__ __launch_bounds__(256) void
+swiglu_kernel(const uint4* __restrict__ g, const uint4* __restrict__ u,
+              uint4* __restrict__ o, int64_t nvec)
+{
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nvec;
+       i += stride) {
+    const uint4 gv = g[i], uv = u[i];
+    const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
+    const uint32_t uw[4] = {uv.x, uv.y, uv.z, uv.w};
+    uint32_t ow[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float g0 = bf16_to_f32(gw[e] & 0xffffu), g1 = bf16_to_f32(gw[e] >> 16);
+      const float u0 = bf16_to_f32(uw[e] & 0xffffu), u1 = bf16_to_f32(uw[e] >> 16);
+      const float h0 = (g0 / (1.0f + expf(-g0))) * u0;
+      const float h1 = (g1 / (1.0f + expf(-g1))) * u1;
+      ow[e] = bf16_bits(h0) | (bf16_bits(h1) << 16);
+    }
+    o[i] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+  }
+}
+
+// ---- row gather / scatter for per-token routing ------------------------
+template <bool kScatter>
+__global__ __launch_bounds__(256) void
+gather_rows_kernel(const uint16_t* __restrict__ src,
+                   const int32_t* __restrict__ perm, int M, int cols,
+                   uint16_t* __restrict__ dst)
+{
+  const int i = blockIdx.x;
+  const int pr = perm[i];
+  // perm is caller data in device memory: an index outside [0, M) copies
+  // nothing rather than touching memory outside the two matrices.
+  if (pr < 0 || pr >= M) { return; }
+  const size_t from = (size_t)(kScatter ? i : pr) * cols;
+  const size_t to = (size_t)(kScatter ? pr : i) * cols;
+  const uint4* s = reinterpret_cast<const uint4*>(src + from);
+  uint4* d = reinterpret_cast<uint4*>(dst + to);
+  for (int c = threadIdx.x; c < cols / 8; c += 256) { d[c] = s[c]; }
+}
+
+template <class Mma, Epi E>
+hipError_t
+launch_gemm(const GemmBatch& b, hipStream_t s)
+{
+  if (b.total_tiles <= 0) { return hipSuccess; }
+  hipLaunchKernelGGL((mot_gemm_kernel<Mma, E>), dim3(b.total_tiles),
+                     dim3(kThreads), 0, s, b);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t
+launch_gemm_bf16(const GemmBatch& b, Epi epi, hipStream_t s)
+{
+  switch (epi) {
+    case Epi::kBf16: return launch_gemm<MmaBf16, Epi::kBf16>(b, s);
+    case Epi::kSwiglu: return launch_gemm<MmaBf16, Epi::kSwiglu>(b, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t
+launch_gemm_i8(const GemmBatch& b, Epi epi, hipStream_t s)
+{
+  switch (epi) {
+    case Epi::kI32: return launch_gemm<MmaI8, Epi::kI32>(b, s);
+    case Epi::kDequantBf16: return launch_gemm<MmaI8, Epi::kDequantBf16>(b, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t
+launch_quant_rows_i8(const uint16_t* x, int rows, int K, int8_t* q,
+                     float* sc, hipStream_t s)
+{
+  if (rows <= 0) { return hipSuccess; }
+  hipLaunchKernelGGL(quant_rows_i8_kernel, dim3(rows), dim3(256), 0, s, x, K,
+                     q, sc);
+  return hipGetLastError();
+}
+
+hipError_t
+launch_swiglu(const uint16_t* g, const uint16_t* u, uint16_t* o, int64_t n,
+              hipStream_t s)
+{
+  const int64_t nvec = n / 8;
+  if (nvec <= 0) { return hipSuccess; }
+  const int64_t want = (nvec + 255) / 256;
+  const int blocks = (int)(want < 8192 ? want : 8192);
+  hipLaunchKernelGGL(swiglu_kernel, dim3(blocks), dim3(256), 0, s,
+                     reinterpret_cast<const uint4*>(g),
+                     reinterpret_cast<const uint4*>(u),
+                     reinterpret_cast<uint4*>(o), nvec);
+  return hipGetLastError();
+}
+
+hipError_t
+launch_gather_rows(const uint16_t* src, const int32_t* perm, int M, int cols,
+                   uint16_t* dst, bool scatter, hipStream_t s)
+{
+  if (M <= 0) { return hipSuccess; }
+  if (scatter) {
+    hipLaunchKernelGGL(gather_rows_kernel<true>, dim3(M), dim3(256), 0, s, src,
+                       perm, M, cols, dst);
+  } else {
+    hipLaunchKernelGGL(gather_rows_kernel<false>, dim3(M), dim3(256), 0, s,
+                       src, perm, M, cols, dst);
+  }
+  return hipGetLastError();
+}
+
+bool
+kernels_loadable()
+{
+  const void* fns[] = {
+      reinterpret_cast<const void*>(&mot_gemm_kernel<MmaBf16, Epi::kBf16>),
+      reinterpret_cast<const void*>(&mot_gemm_kernel<MmaBf16, Epi::kSwiglu>),
+      reinterpret_cast<const void*>(&mot_gemm_kernel<MmaI8, Epi::kI32>),
+      reinterpret_cast<const void*>(&mot_gemm_kernel<MmaI8, Epi::kDequantBf16>),
+      reinterpret_cast<const void*>(&quant_rows_i8_kernel),
+      reinterpret_cast<const void*>(&swiglu_kernel),
+      reinterpret_cast<const void*>(&gather_rows_kernel<true>),
+      reinterpret_cast<const void*>(&gather_rows_kernel<false>),
+  };
+  for (const void* f : fns) {
+    hipFuncAttributes a;
+    if (hipFuncGetAttributes(&a, f) != hipSuccess) { return false; }
+  }
+  return true;
+}
+
+}  // namespace u15h

@@ -1,0 +1,323 @@
+"""Python host binding of the u15h C ABI (include/u15h.h).
+
+`Ops` mirrors the GEMM half of the reference's op vocabulary,
+`u15::MetalOps` (src/u15-metal-ops.h:59-531): `linear`, the int8 tier's
+`enable_i8_gemm` / `release_i8_scratch`, `swiglu`, plus the two-group MoT
+entry points that run both weight sets (base for understanding rows,
+`_mot_gen` for generated-image rows) in one launch.
+
+Every call goes through libu15h.so, built in-tree next to this package
+(`make -C vpipe-sensenova-u1.5_amd`).  There is no CPU fallback: if the
+library is missing, or there is no gfx950 device, construction raises.
+
+Tensors are torch tensors on the GPU; torch is used for device memory and
+streams only.  Shapes and dtypes are checked here, before the C ABI checks
+them again.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+import re
+
+import torch
+
+PKG_DIR = pathlib.Path(__file__).resolve().parent.parent
+REPO_DIR = PKG_DIR.parent
+LIB_PATH = PKG_DIR / "libu15h.so"
+HEADER_PATH = REPO_DIR / "include" / "u15h.h"
+
+OK, EINVAL, ENODEV, ELAUNCH, ENOMEM = 0, 1, 2, 3, 4
+MAX_PROJ = 4
+
+_lib = None
+
+
+class U15hError(RuntimeError):
+    def __init__(self, status: int, msg: str):
+        super().__init__(msg)
+        self.status = status
+
+
+class _MotProj(ctypes.Structure):
+    _fields_ = [("w_und", ctypes.c_void_p), ("w_gen", ctypes.c_void_p),
+                ("bias_und", ctypes.c_void_p), ("bias_gen", ctypes.c_void_p),
+                ("y", ctypes.c_void_p), ("N", ctypes.c_int)]
+
+
+class _MotProjI8(ctypes.Structure):
+    _fields_ = [("wq_und", ctypes.c_void_p), ("sw_und", ctypes.c_void_p),
+                ("wq_gen", ctypes.c_void_p), ("sw_gen", ctypes.c_void_p),
+                ("y", ctypes.c_void_p), ("N", ctypes.c_int)]
+
+
+def declared_symbols() -> list[str]:
+    """Every function include/u15h.h declares."""
+    text = HEADER_PATH.read_text()
+    return sorted(set(re.findall(r"\b(u15h_[a-z0-9_]+)\s*\(", text)))
+
+
+def load_library() -> ctypes.CDLL:
+    """Load libu15h.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise U15hError(ENODEV, f"{LIB_PATH} is not built; run "
+                        f"`make -C {PKG_DIR}` (or __graft_entry__.build())")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    vp, i, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+    sigs = {
+        "u15h_create": (i, [i, ctypes.POINTER(vp)]),
+        "u15h_destroy": (None, [vp]),
+        "u15h_abi_version": (i, []),
+        "u15h_status_str": (ctypes.c_char_p, [i]),
+        "u15h_last_error": (ctypes.c_char_p, [vp]),
+        "u15h_linear": (i, [vp, vp, vp, vp, vp, vp, i, i, i]),
+        "u15h_mot_linear": (i, [vp, vp, vp, i, i, i,
+                                ctypes.POINTER(_MotProj), i]),
+        "u15h_swiglu": (i, [vp, vp, vp, vp, vp, i64]),
+        "u15h_mot_gate_up_swiglu": (i, [vp, vp, vp, i, i, i, vp, vp, vp, vp,
+                                        vp, i]),
+        "u15h_enable_i8_gemm": (i, [vp, i]),
+        "u15h_release_i8_scratch": (None, [vp]),
+        "u15h_i8_min_m": (i, [vp]),
+        "u15h_quant_rows_i8": (i, [vp, vp, vp, i, i, vp, vp]),
+        "u15h_mot_gemm_i8_i32": (i, [vp, vp, vp, i, i, i,
+                                     ctypes.POINTER(_MotProjI8), i]),
+        "u15h_mot_gemm_i8": (i, [vp, vp, vp, vp, i, i, i,
+                                 ctypes.POINTER(_MotProjI8), i]),
+        "u15h_route_rows": (i, [vp, i, vp, ctypes.POINTER(i),
+                                ctypes.POINTER(i)]),
+        "u15h_gather_rows": (i, [vp, vp, vp, vp, i, i, vp]),
+        "u15h_scatter_rows": (i, [vp, vp, vp, vp, i, i, vp]),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def route_rows(expert) -> tuple[list[int], int, int]:
+    """Stable partition of token rows by expert (0 = und, 1 = gen).
+
+    Host-side; returns (perm, M_und, M_gen) with perm[:M_und] the und rows.
+    """
+    lib = load_library()
+    import numpy as np
+    e = np.ascontiguousarray(np.asarray(expert, dtype=np.uint8))
+    M = int(e.size)
+    perm = np.zeros(max(M, 1), dtype=np.int32)
+    mu, mg = ctypes.c_int(0), ctypes.c_int(0)
+    st = lib.u15h_route_rows(e.ctypes.data if M else None, M,
+                             perm.ctypes.data, ctypes.byref(mu),
+                             ctypes.byref(mg))
+    if st != OK:
+        raise U15hError(st, "u15h_route_rows: invalid expert ids")
+    return perm[:M], mu.value, mg.value
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream):
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def _need(t, dtype, shape, name):
+    if t is None:
+        raise ValueError(f"{name} is required")
+    if t.dtype != dtype:
+        raise TypeError(f"{name}: dtype {t.dtype}, expected {dtype}")
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name}: shape {tuple(t.shape)}, expected {tuple(shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be on the GPU")
+
+
+class Ops:
+    """The projection-GEMM operator surface on one gfx950 device."""
+
+    def __init__(self, device: int = 0):
+        self._lib = load_library()
+        ctx = ctypes.c_void_p()
+        st = self._lib.u15h_create(device, ctypes.byref(ctx))
+        if st != OK:
+            raise U15hError(st, f"u15h_create(device={device}): "
+                            f"{self._lib.u15h_status_str(st).decode()}")
+        self._ctx = ctx
+        self.device = device
+
+    def close(self):
+        if getattr(self, "_ctx", None):
+            self._lib.u15h_destroy(self._ctx)
+            self._ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, st, what):
+        if st != OK:
+            msg = self._lib.u15h_last_error(self._ctx).decode()
+            raise U15hError(st, f"{what}: "
+                            f"{self._lib.u15h_status_str(st).decode()}: {msg}")
+
+    # ---- dense -------------------------------------------------------
+    def linear(self, x, w, bias, y, M, K, N, stream=None):
+        """y[M][N] = x[M][K] . w[N][K]^T (+ bias) -- MetalOps::linear."""
+        _need(x, torch.bfloat16, (M, K), "x")
+        _need(w, torch.bfloat16, (N, K), "w")
+        _need(y, torch.bfloat16, (M, N), "y")
+        if bias is not None:
+            _need(bias, torch.bfloat16, (N,), "bias")
+        st = self._lib.u15h_linear(self._ctx, _stream(stream), _ptr(x),
+                                   _ptr(w), _ptr(bias), _ptr(y), M, K, N)
+        self._check(st, "u15h_linear")
+
+    def mot_linear(self, x, M_und, M_gen, K, projs, stream=None):
+        """Grouped MoT GEMM.  projs: list of dicts with keys
+        w_und, w_gen, y and optionally bias_und, bias_gen."""
+        M = M_und + M_gen
+        _need(x, torch.bfloat16, (M, K), "x")
+        if not 1 <= len(projs) <= MAX_PROJ:
+            raise ValueError(f"1..{MAX_PROJ} projections per launch")
+        arr = (_MotProj * len(projs))()
+        for i, p in enumerate(projs):
+            N = p["y"].shape[1]
+            _need(p["y"], torch.bfloat16, (M, N), f"projs[{i}].y")
+            if M_und:
+                _need(p["w_und"], torch.bfloat16, (N, K), f"projs[{i}].w_und")
+            if M_gen:
+                _need(p["w_gen"], torch.bfloat16, (N, K), f"projs[{i}].w_gen")
+            for b in ("bias_und", "bias_gen"):
+                if p.get(b) is not None:
+                    _need(p[b], torch.bfloat16, (N,), f"projs[{i}].{b}")
+            arr[i] = _MotProj(
+                p["w_und"].data_ptr() if p.get("w_und") is not None else None,
+                p["w_gen"].data_ptr() if p.get("w_gen") is not None else None,
+                p["bias_und"].data_ptr() if p.get("bias_und") is not None else None,
+                p["bias_gen"].data_ptr() if p.get("bias_gen") is not None else None,
+                p["y"].data_ptr(), N)
+        st = self._lib.u15h_mot_linear(self._ctx, _stream(stream), _ptr(x),
+                                       M_und, M_gen, K, arr, len(projs))
+        self._check(st, "u15h_mot_linear")
+
+    # ---- swiglu --------------------------------------------------------
+    def swiglu(self, gate, up, out, stream=None):
+        n = gate.numel()
+        for t, nm in ((gate, "gate"), (up, "up"), (out, "out")):
+            _need(t, torch.bfloat16, tuple(gate.shape), nm)
+        st = self._lib.u15h_swiglu(self._ctx, _stream(stream), _ptr(gate),
+                                   _ptr(up), _ptr(out), n)
+        self._check(st, "u15h_swiglu")
+
+    def mot_gate_up_swiglu(self, x, M_und, M_gen, K, wg_und, wu_und, wg_gen,
+                           wu_gen, h, stream=None):
+        M = M_und + M_gen
+        I = h.shape[1]
+        _need(x, torch.bfloat16, (M, K), "x")
+        _need(h, torch.bfloat16, (M, I), "h")
+        if M_und:
+            _need(wg_und, torch.bfloat16, (I, K), "wg_und")
+            _need(wu_und, torch.bfloat16, (I, K), "wu_und")
+        if M_gen:
+            _need(wg_gen, torch.bfloat16, (I, K), "wg_gen")
+            _need(wu_gen, torch.bfloat16, (I, K), "wu_gen")
+        st = self._lib.u15h_mot_gate_up_swiglu(
+            self._ctx, _stream(stream), _ptr(x), M_und, M_gen, K,
+            _ptr(wg_und), _ptr(wu_und), _ptr(wg_gen), _ptr(wu_gen), _ptr(h), I)
+        self._check(st, "u15h_mot_gate_up_swiglu")
+
+    # ---- int8 tier -----------------------------------------------------
+    def enable_i8_gemm(self, want: bool) -> bool:
+        """MetalOps::enable_i8_gemm: returns whether the tier is ON."""
+        return bool(self._lib.u15h_enable_i8_gemm(self._ctx, 1 if want else 0))
+
+    def release_i8_scratch(self):
+        self._lib.u15h_release_i8_scratch(self._ctx)
+
+    def i8_min_m(self) -> int:
+        return int(self._lib.u15h_i8_min_m(self._ctx))
+
+    def quant_rows_i8(self, x, q, s, stream=None):
+        rows, K = x.shape
+        _need(x, torch.bfloat16, (rows, K), "x")
+        _need(q, torch.int8, (rows, K), "q")
+        _need(s, torch.float32, (rows,), "s")
+        st = self._lib.u15h_quant_rows_i8(self._ctx, _stream(stream), _ptr(x),
+                                          rows, K, _ptr(q), _ptr(s))
+        self._check(st, "u15h_quant_rows_i8")
+
+    def _i8_projs(self, M, M_und, M_gen, K, projs, ydtype, need_scales):
+        if not 1 <= len(projs) <= MAX_PROJ:
+            raise ValueError(f"1..{MAX_PROJ} projections per launch")
+        arr = (_MotProjI8 * len(projs))()
+        for i, p in enumerate(projs):
+            N = p["y"].shape[1]
+            _need(p["y"], ydtype, (M, N), f"projs[{i}].y")
+            for g, mg in (("und", M_und), ("gen", M_gen)):
+                if mg:
+                    _need(p["wq_" + g], torch.int8, (N, K), f"projs[{i}].wq_{g}")
+                    if need_scales:
+                        _need(p["sw_" + g], torch.float32, (N,), f"projs[{i}].sw_{g}")
+
+            def g_(k):
+                t = p.get(k)
+                return t.data_ptr() if t is not None else None
+            arr[i] = _MotProjI8(g_("wq_und"), g_("sw_und"), g_("wq_gen"),
+                                g_("sw_gen"), p["y"].data_ptr(), N)
+        return arr
+
+    def mot_gemm_i8_i32(self, xq, M_und, M_gen, K, projs, stream=None):
+        M = M_und + M_gen
+        _need(xq, torch.int8, (M, K), "xq")
+        arr = self._i8_projs(M, M_und, M_gen, K, projs, torch.int32, False)
+        st = self._lib.u15h_mot_gemm_i8_i32(self._ctx, _stream(stream),
+                                            _ptr(xq), M_und, M_gen, K, arr,
+                                            len(projs))
+        self._check(st, "u15h_mot_gemm_i8_i32")
+
+    def mot_gemm_i8(self, xq, sx, M_und, M_gen, K, projs, stream=None):
+        M = M_und + M_gen
+        _need(xq, torch.int8, (M, K), "xq")
+        _need(sx, torch.float32, (M,), "sx")
+        arr = self._i8_projs(M, M_und, M_gen, K, projs, torch.bfloat16, True)
+        st = self._lib.u15h_mot_gemm_i8(self._ctx, _stream(stream), _ptr(xq),
+                                        _ptr(sx), M_und, M_gen, K, arr,
+                                        len(projs))
+        self._check(st, "u15h_mot_gemm_i8")
+
+    # ---- routing -------------------------------------------------------
+    def gather_rows(self, src, perm, dst, stream=None):
+        M, cols = dst.shape
+        _need(perm, torch.int32, (M,), "perm")
+        st = self._lib.u15h_gather_rows(self._ctx, _stream(stream), _ptr(src),
+                                        _ptr(perm), M, cols, _ptr(dst))
+        self._check(st, "u15h_gather_rows")
+
+    def scatter_rows(self, src, perm, dst, stream=None):
+        M, cols = src.shape
+        _need(perm, torch.int32, (M,), "perm")
+        st = self._lib.u15h_scatter_rows(self._ctx, _stream(stream), _ptr(src),
+                                         _ptr(perm), M, cols, _ptr(dst))
+        self._check(st, "u15h_scatter_rows")
+
+    # ---- raw access for tests of argument checking ----------------------
+    @property
+    def lib(self):
+        return self._lib
+
+    @property
+    def ctx(self):
+        return self._ctx
