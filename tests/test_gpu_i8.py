@@ -151,7 +151,8 @@ def test_i8_full_pipeline_c2_shape_q_proj(ops):
         f64 = oracle.dequant_f64(acc_h[lo:hi], sx_h[lo:hi], sw)
         assert max_rel(oracle.bf16_to_f32(y_h[lo:hi]), f64) <= 1e-2
     # and the tier approximates the bf16 product (quantisation error only)
-    ref = oracle.linear_bf16(xbits, wgbits, row_ids=np.array([200, 3000], np.int32))
+    ref = oracle.linear_bf16(xbits, wgbits,
+                             row_ids=np.array([Mu + 200, Mu + 3000], np.int32))
     assert rel_l2(host_f32(y)[[Mu + 200, Mu + 3000]], ref) < 0.03
 
 

@@ -50,13 +50,6 @@ make_rsrc(const void* base, int bytes)
                                            kRsrcWord3);
 }
 
-__device__ __forceinline__ i32x4_t
-load16(__amdgpu_buffer_rsrc_t r, int voff, int soff)
-{
-  return __builtin_bit_cast(
-      i32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-}
-
 __device__ __forceinline__ uint32_t
 bf16_bits(float f)
 {
@@ -100,7 +93,10 @@ template <class Mma, Epi E>
 __global__ __launch_bounds__(kThreads, 1) void
 mot_gemm_kernel(const GemmBatch B)
 {
-  __shared__ __attribute__((aligned(16))) char lds[2 * kStage];
+  // Two LDS stages as two objects, so the compiler can tell the fragment
+  // reads of one stage from the direct-to-LDS loads filling the other.
+  __shared__ __attribute__((aligned(1024))) char lds0[kStage];
+  __shared__ __attribute__((aligned(1024))) char lds1[kStage];
 
   // ---- which tile -----------------------------------------------------
   // Consecutive workgroups are dealt round-robin to the 8 XCDs; remap so
@@ -132,13 +128,10 @@ mot_gemm_kernel(const GemmBatch B)
   const int kbytes = B.kbytes;
   const int nk = (kbytes + kKB - 1) / kKB;
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave & 1;
   const int wn = wave >> 1;
-  const int lrow = tid >> 3;   // row of a 32-row slab this thread loads
-  const int lch = tid & 7;     // 16-byte chunk of the 128-byte stage row
 
   // ---- operand resources ----------------------------------------------
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(
@@ -156,56 +149,63 @@ mot_gemm_kernel(const GemmBatch B)
                    min(kBN, P.n - col0) * kbytes);
     ru = rw;
   }
-  // Weight slab i (32 LDS rows) comes from which resource and which row.
-  // Plain: rows i*32.. of the weight tile.  SwiGLU: wave column wn owns 64
-  // output columns; its 128 LDS rows are 64 gate rows then the 64 matching
-  // up rows, so a lane's gate and up accumulators cover the same outputs.
-  auto wslab_row = [&](int i) {
-    if constexpr (E == Epi::kSwiglu) {
-      return (i >> 2) * 64 + (i & 1) * 32;
-    } else {
-      return i * 32;
-    }
-  };
-  auto wslab_is_up = [&](int i) {
-    return E == Epi::kSwiglu && ((i >> 1) & 1) != 0;
-  };
 
+  // ---- direct-to-LDS loads --------------------------------------------
+  // A stage is 512 rows x 128 bytes: weight rows 0..255 then activation
+  // rows.  Wave w fills rows [128w, 128w+128) in 16 blocks of 8 rows; one
+  // instruction writes a 1 KiB block, lane l landing at byte 16*l: row
+  // l/8 of the block, chunk position l%8.  The swizzle (position = chunk ^
+  // (row & 7)) is applied on the global side: lane l fetches logical chunk
+  // (l%8) ^ (l/8).
+  //
+  // SwiGLU tiles: wave column wn owns 64 output columns; its 128 weight
+  // rows are 64 gate rows then the 64 matching up rows, so a lane's gate
+  // and up accumulators cover the same outputs.
+  const int lrow8 = lane >> 3;
+  const int lchunk = (lane & 7) ^ lrow8;
+  const int lane_off = lrow8 * kbytes + lchunk * 16;
   // The range check that zero-fills rows past M / N and the K tail applies
   // to the per-lane (VGPR) offset, so every row offset is carried there;
   // only the stage's K offset, common to all rows, rides in the SGPR.
-  const int voff = lrow * kbytes + lch * 16;
   const int tail_off =
-      ((nk - 1) * kKB + lch * 16 < kbytes) ? 0 : kOobOffset;
+      ((nk - 1) * kKB + lchunk * 16 < kbytes) ? 0 : kOobOffset;
 
-  i32x4_t wreg[8], areg[8];
-  auto gload = [&](int kt) {
-    const int ko = kt * kKB;
-    const int v = voff + (kt == nk - 1 ? tail_off : 0);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      wreg[i] = load16(wslab_is_up(i) ? ru : rw, v + wslab_row(i) * kbytes, ko);
+  // Per-wave load parameters (wave-uniform): the resource for blocks 0-7
+  // and 8-15, the first operand row, and the block-index mask.
+  __amdgpu_buffer_rsrc_t r_lo = ra, r_hi = ra;
+  int row_base = (wave - 2) * 128;
+  int bmask = 15;
+  if (wave < 2) {
+    if constexpr (E == Epi::kSwiglu) {
+      r_lo = rw;            // gate rows
+      r_hi = ru;            // up rows
+      row_base = wave * 64;
+      bmask = 7;
+    } else {
+      r_lo = rw;
+      r_hi = rw;
+      row_base = wave * 128;
     }
+  }
+  // Stages past the last one (kt >= nk) load nothing: their offsets are
+  // pushed out of range, so the hardware returns zeros without a memory
+  // access.  The loop below runs an even number of stages and relies on it.
+  auto issue_loads = [&](char* stage_base, int kt) {
+    const int ko = min(kt, nk - 1) * kKB;
+    const int v = lane_off + row_base * kbytes +
+                  (kt == nk - 1 ? tail_off : 0) + (kt >= nk ? kOobOffset : 0);
+    char* dst = stage_base + wave * (128 * kKB);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      areg[i] = load16(ra, v + i * 32 * kbytes, ko);
+    for (int b = 0; b < 16; ++b) {
+      const int orow8 = (b & bmask) * 8;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          b < 8 ? r_lo : r_hi,
+          (__attribute__((address_space(3))) void*)(dst + b * 1024), 16,
+          v + orow8 * kbytes, ko, 0, 0);
     }
   };
 
-  const int st_off = lrow * kKB + ((lch ^ (lrow & 7)) << 4);
-  auto lstore = [&](int stage) {
-    char* base = lds + stage * kStage;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      *reinterpret_cast<i32x4_t*>(base + i * 32 * kKB + st_off) = wreg[i];
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      *reinterpret_cast<i32x4_t*>(base + kBN * kKB + i * 32 * kKB + st_off) =
-          areg[i];
-    }
-  };
-
+  // ---- MFMA fragments ---------------------------------------------------
   const int lr = lane & 31;
   const int lh = lane >> 5;
   int rd[4];
@@ -223,43 +223,90 @@ mot_gemm_kernel(const GemmBatch B)
     for (int j = 0; j < 4; ++j) { acc[i][j] = typename Mma::acc_t{}; }
   }
 
-  auto compute = [&](int stage) {
-    const char* base = lds + stage * kStage;
+  i32x4_t fa[2][4], fb[2][4];
+  auto read_frags = [&](const char* base, int s, int buf) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      i32x4_t fa[4], fb[4];
+    for (int i = 0; i < 4; ++i) {
+      fa[buf][i] = *reinterpret_cast<const i32x4_t*>(base + wbase +
+                                                     i * 32 * kKB + rd[s]);
+    }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        fa[i] = *reinterpret_cast<const i32x4_t*>(base + wbase + i * 32 * kKB +
-                                                  rd[s]);
-      }
+    for (int j = 0; j < 4; ++j) {
+      fb[buf][j] = *reinterpret_cast<const i32x4_t*>(base + abase +
+                                                     j * 32 * kKB + rd[s]);
+    }
+  };
+  auto mma_step = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        fb[j] = *reinterpret_cast<const i32x4_t*>(base + abase + j * 32 * kKB +
-                                                  rd[s]);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          acc[i][j] = Mma::run(fa[i], fb[j], acc[i][j]);
-        }
+        acc[i][j] = Mma::run(fa[buf][i], fb[buf][j], acc[i][j]);
       }
     }
   };
+  // Scheduling masks of __builtin_amdgcn_sched_group_barrier.
+  constexpr int kSchedMfma = 0x008, kSchedVmem = 0x010, kSchedDsRead = 0x100;
+  // 8 fragment reads spread over 16 MFMAs.
+  auto interleave_reads = [&]() {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8, 0);
+  };
+  // 16 direct loads and 8 fragment reads spread over 16 MFMAs.
+  auto interleave_loads_reads = [&]() {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
+    }
+  };
 
-  // ---- main loop: prefetch stage kt+1 into registers while the MFMAs
-  // consume stage kt from LDS; one barrier per stage. -------------------
-  gload(0);
-  lstore(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) { gload(kt + 1); }
-    compute(cur);
-    if (kt + 1 < nk) { lstore(cur ^ 1); }
+  // One K stage held in LDS buffer `cur`; `nxt` is the other buffer.  On
+  // entry fragments of sub-step 0 are in fa/fb[0]; fragments of sub-step
+  // s+1 are read while the 16 MFMAs of sub-step s run.  Before the last
+  // sub-step the stage's LDS is handed back: once every wave has its last
+  // fragments in registers and its direct loads of the next stage have
+  // landed, one barrier lets the loads of stage kt+2 refill `cur` and the
+  // first fragments of stage kt+1 be read while the last 16 MFMAs run.
+  // The body is branch-free (after the final stage the extra loads fetch
+  // nothing and the extra fragment reads are unused), which keeps the 256
+  // accumulators in AGPRs across the whole loop.
+  auto stage = [&](char* cur, const char* nxt, int kt) {
+#pragma unroll
+    for (int s = 0; s < 3; ++s) {
+      read_frags(cur, s + 1, (s + 1) & 1);
+      mma_step(s & 1);
+      interleave_reads();
+    }
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     __syncthreads();
+    issue_loads(cur, kt + 2);
+    read_frags(nxt, 0, 0);
+    mma_step(1);
+    interleave_loads_reads();
+  };
+
+  // ---- main loop: an even number of stages; a padding stage (K past the
+  // end) reads as zeros and adds exactly 0 to every accumulator ------------
+  const int nk_even = (nk + 1) & ~1;
+  issue_loads(lds0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  issue_loads(lds1, 1);
+  read_frags(lds0, 0, 0);
+  for (int kt = 0; kt < nk_even; kt += 2) {
+    stage(lds0, lds1, kt);
+    stage(lds1, lds0, kt + 1);
   }
+  // No load may still be writing LDS when the workgroup retires.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // ---- epilogue ---------------------------------------------------------
   // acc[i][j][r]: output column (within the wave's block) i*32 + (r>>2)*8 +
