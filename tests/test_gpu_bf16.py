@@ -120,7 +120,9 @@ def test_mot_qkv_one_launch_c1_shape(ops):
 
 @pytest.mark.parametrize("Mu,Mg,K,N", [(37, 263, 72, 40), (0, 300, 136, 264),
                                        (5, 0, 64, 8), (1, 1, 8, 8),
-                                       (257, 511, 200, 520)])
+                                       (257, 511, 200, 520),
+                                       # split into K shares, K tail in the last
+                                       (37, 263, 1032, 264)])
 def test_mot_linear_ragged_full_check(ops, Mu, Mg, K, N):
     """Ragged tails in M (both groups), N and K (K not a multiple of the
     64-element stage); the whole output against the oracle."""
@@ -264,3 +266,51 @@ def test_invalid_shapes_launch_nothing(ops):
     assert st == u15h.EINVAL                     # misaligned x
     torch.cuda.synchronize()
     assert torch.all(y == 7.0)
+
+
+@pytest.fixture(scope="module")
+def ops_nosplit():
+    """A second context built with the split-K tail switched off
+    (U15H_SPLIT=0 read at creation) -- the in-process A/B the reference's
+    model-shape test makes with its kill switches
+    (tests/u15-m5-test.cc:391-404)."""
+    import os
+    old = os.environ.get("U15H_SPLIT")
+    os.environ["U15H_SPLIT"] = "0"
+    try:
+        o = u15h.Ops(0)
+    finally:
+        if old is None:
+            del os.environ["U15H_SPLIT"]
+        else:
+            os.environ["U15H_SPLIT"] = old
+    yield o
+    torch.cuda.synchronize()
+    o.close()
+
+
+@pytest.mark.parametrize("Mu,Mg,K,N", [(128, 4096, 4096, 4096),    # o: 272 tiles
+                                       (128, 4096, 12288, 4096),   # down
+                                       (0, 256, 4096, 6144)])      # one partial round
+def test_split_tail_matches_unsplit(ops, ops_nosplit, Mu, Mg, K, N):
+    """Split-K tail vs whole tiles on the same inputs: both within the bar
+    of the oracle on sampled rows, and of each other everywhere."""
+    M = Mu + Mg
+    g = torch.Generator(device="cuda").manual_seed(M + K + N)
+    x = torch.randn(M, K, generator=g, device="cuda").to(torch.bfloat16)
+    wu = (torch.randn(N, K, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    wg = (torch.randn(N, K, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    y1 = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    y2 = torch.empty_like(y1)
+    ops.mot_linear(x, Mu, Mg, K, [dict(w_und=wu, w_gen=wg, y=y1)])
+    ops_nosplit.mot_linear(x, Mu, Mg, K, [dict(w_und=wu, w_gen=wg, y=y2)])
+    torch.cuda.synchronize()
+    a, b = host_f32(y1), host_f32(y2)
+    assert rel_l2(a, b) < 4e-3 and max_rel(a, b) <= MAX_REL
+    xb, wub, wgb = host_bits(x), host_bits(wu), host_bits(wg)
+    rows = np.array([0, Mu // 2, M - 1, max(Mu, 1) + 7], np.int32)
+    for r in rows:
+        w = wub if r < Mu else wgb
+        ref = oracle.linear_bf16(xb, w, row_ids=np.array([r], np.int32))
+        assert max_rel(a[r:r + 1], ref) <= MAX_REL
+        assert rel_l2(a[r:r + 1], ref) < REF_BAR

@@ -194,3 +194,27 @@ def test_linear_int8_route_on_and_decline(ops):
     finally:
         ops.enable_i8_gemm(False)
         ops.release_i8_scratch()
+
+
+def test_i32_split_tail_bit_exact(ops):
+    """An int8 launch whose tiles are split into K shares (6 tiles of a
+    12288-deep K): the shares' int32 sums are exact, so the result equals
+    the exact CPU GEMM bit for bit."""
+    rng = np.random.default_rng(25)
+    Mu, Mg, K, N = 37, 263, 12288, 264
+    M = Mu + Mg
+    xq = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    wu = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    wg = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    y = torch.empty(M, N, dtype=torch.int32, device="cuda")
+    ops.mot_gemm_i8_i32(torch.from_numpy(xq).cuda(), Mu, Mg, K,
+                        [_proj(torch.from_numpy(wu).cuda(), None,
+                               torch.from_numpy(wg).cuda(), None, y)])
+    torch.cuda.synchronize()
+    out = y.cpu().numpy()
+    assert np.array_equal(out[:Mu], oracle.gemm_i8_i32(xq[:Mu], wu))
+    rows = np.array([0, 100, 262], np.int32)
+    assert np.array_equal(out[Mu:][rows], oracle.gemm_i8_i32(xq[Mu:], wg, row_ids=rows))
+    rs, cs = oracle.i8_product_sums(xq[Mu:], wg)
+    assert np.array_equal(out[Mu:].astype(np.int64).sum(axis=1), rs)
+    assert np.array_equal(out[Mu:].astype(np.int64).sum(axis=0), cs)

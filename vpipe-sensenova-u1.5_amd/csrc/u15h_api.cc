@@ -19,6 +19,11 @@
 
 struct u15h_ctx {
   int device = 0;
+  int num_cu = 256;
+  bool split_on = true;      // env U15H_SPLIT=0 turns the split-K tail off
+  // Partial-sum workspace of split tiles: at most num_cu K shares of one
+  // 256x256 tile each (allocated on first use, kept until destroy).
+  void* split_ws = nullptr;
   bool i8_on = false;
   int i8_min_m = 1024;
   // Grow-only scratch of the int8 route of u15h_linear: activation and
@@ -109,7 +114,50 @@ empty_batch(int kbytes)
   GemmBatch b;
   std::memset(&b, 0, sizeof b);
   b.kbytes = kbytes;
+  b.split = 1;
   return b;
+}
+
+// Fewest K stages a split share may have.
+constexpr int kMinStagesPerShare = 4;
+
+size_t
+split_ws_capacity(const u15h_ctx* ctx)
+{
+  return (size_t)ctx->num_cu * u15h::kBM * u15h::kBN * 4;
+}
+
+// Chooses the split-K tail of a batch once its tiles are known.  With T
+// tiles on C compute units, the last T % C tiles would run as a last,
+// partial round that leaves most units idle; instead each is cut into
+// S = C / (T % C) shares of its K stages (so the shares fill about one
+// round), at least kMinStagesPerShare stages each.
+u15h_status
+plan_split(u15h_ctx* ctx, GemmBatch& b)
+{
+  b.split = 1;
+  b.split_begin = b.total_tiles;
+  b.ws = nullptr;
+  const int T = b.total_tiles;
+  const int C = ctx->num_cu;
+  const int rem = T % C;
+  if (!ctx->split_on || T <= 0 || rem == 0) { return U15H_OK; }
+  const int nk = (b.kbytes + u15h::kKB - 1) / u15h::kKB;
+  const int S = std::min(C / rem, nk / kMinStagesPerShare);
+  if (S < 2) { return U15H_OK; }
+  if (ctx->split_ws == nullptr) {
+    if (hipMalloc(&ctx->split_ws, split_ws_capacity(ctx)) != hipSuccess) {
+      ctx->split_ws = nullptr;
+      return fail(ctx, U15H_ENOMEM, "split-K workspace of %zu bytes",
+                  split_ws_capacity(ctx));
+    }
+  }
+  b.split = S;
+  b.split_begin = T - rem;
+  b.ws = ctx->split_ws;
+  return split_ws_bytes(b) <= split_ws_capacity(ctx)
+             ? U15H_OK
+             : fail(ctx, U15H_EINVAL, "split workspace overflow");
 }
 
 // Shape limits shared by every GEMM entry point.  Byte offsets inside a
@@ -211,6 +259,8 @@ linear_i8_route(u15h_ctx* ctx, hipStream_t s, const u15h_bf16* x,
   GemmBatch b = empty_batch(K);
   add_problem(b, xqp, wqp, nullptr, y, bias, sx, sw, M, N, N,
               u15h::tile_cols(Epi::kDequantBf16));
+  u15h_status st = plan_split(ctx, b);
+  if (st != U15H_OK) { return st; }
   return launched(ctx, u15h::launch_gemm_i8(b, Epi::kDequantBf16, s),
                   "gemm_i8");
 }
@@ -266,6 +316,8 @@ u15h_create(int device, u15h_ctx** out)
   if (!ok) { return U15H_ENODEV; }
   u15h_ctx* ctx = new u15h_ctx;
   ctx->device = device;
+  ctx->num_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+  ctx->split_on = env_int("U15H_SPLIT", 1) != 0;
   ctx->i8_min_m = std::max(1, env_int("U15H_I8_MIN_M", 1024));
   *out = ctx;
   return U15H_OK;
@@ -276,6 +328,10 @@ u15h_destroy(u15h_ctx* ctx)
 {
   if (ctx == nullptr) { return; }
   u15h_release_i8_scratch(ctx);
+  if (ctx->split_ws != nullptr) {
+    (void)hipDeviceSynchronize();
+    (void)hipFree(ctx->split_ws);
+  }
   delete ctx;
 }
 
@@ -315,6 +371,7 @@ u15h_linear(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
   GemmBatch b = empty_batch(K * 2);
   add_problem(b, x, w, nullptr, y, bias, nullptr, nullptr, M, N, N,
               u15h::tile_cols(Epi::kBf16));
+  if ((st = plan_split(ctx, b)) != U15H_OK) { return st; }
   return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kBf16, s), "gemm_bf16");
 }
 
@@ -368,6 +425,7 @@ u15h_mot_linear(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
                 M_und, p.N, p.N, tc);
   }
   if ((st = check_tiles(ctx, b)) != U15H_OK) { return st; }
+  if ((st = plan_split(ctx, b)) != U15H_OK) { return st; }
   return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kBf16, as_stream(stream)),
                   "mot_gemm_bf16");
 }
@@ -426,6 +484,7 @@ u15h_mot_gate_up_swiglu(u15h_ctx* ctx, u15h_stream stream,
   add_problem(b, x, wg_und, wu_und, h, nullptr, nullptr, nullptr, M_und, I, I,
               tc);
   if ((st = check_tiles(ctx, b)) != U15H_OK) { return st; }
+  if ((st = plan_split(ctx, b)) != U15H_OK) { return st; }
   return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kSwiglu, as_stream(stream)),
                   "mot_gate_up_swiglu");
 }
@@ -537,6 +596,7 @@ mot_gemm_i8_common(u15h_ctx* ctx, u15h_stream stream, const int8_t* xq,
                 deq ? p.sw_und : nullptr, M_und, p.N, p.N, tc);
   }
   if ((st = check_tiles(ctx, b)) != U15H_OK) { return st; }
+  if ((st = plan_split(ctx, b)) != U15H_OK) { return st; }
   return launched(ctx, u15h::launch_gemm_i8(b, epi, as_stream(stream)),
                   deq ? "mot_gemm_i8" : "mot_gemm_i8_i32");
 }

@@ -42,12 +42,32 @@ struct GemmProblem {
   int tile_begin;         // first linear tile index of this problem
 };
 
+// A batch of problems run by one launch.  Tiles are numbered problem by
+// problem.  Tiles [split_begin, total_tiles) -- the ones that would
+// otherwise leave most of the GPU idle in a last, partial round -- run as
+// `split` workgroups each, every one covering a contiguous share of the K
+// stages and writing its raw accumulators to `ws`; a second, small kernel
+// sums the shares and applies the epilogue.
 struct GemmBatch {
   GemmProblem p[kMaxProb];
   int nprob;
   int kbytes;             // bytes per activation / weight row (K * elem size)
   int total_tiles;
+  int split_begin;        // == total_tiles when nothing is split
+  int split;              // K shares per split tile (1 = no split)
+  void* ws;               // [(tile - split_begin) * split + share][kBM][kBN]
 };
+
+// Workgroups a batch launches.
+inline int grid_blocks(const GemmBatch& b)
+{
+  return b.split_begin + (b.total_tiles - b.split_begin) * b.split;
+}
+// Bytes of partial-sum workspace a batch needs.
+inline size_t split_ws_bytes(const GemmBatch& b)
+{
+  return (size_t)(b.total_tiles - b.split_begin) * b.split * kBM * kBN * 4;
+}
 
 // Kernel launchers (u15h_kernels.hip).  All are asynchronous on `s`.
 hipError_t launch_gemm_bf16(const GemmBatch& b, Epi epi, hipStream_t s);

@@ -29,6 +29,8 @@
 // stage) is zero-filled by pushing the invalid chunks' offsets out of range.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "u15h_internal.h"
 
 namespace u15h {
@@ -43,11 +45,18 @@ constexpr int kStage = (kBM + kBN) * kKB;   // 64 KiB per LDS stage
 constexpr int kRsrcWord3 = 0x00020000;      // raw buffer, 32-bit data format
 constexpr int kOobOffset = 0x40000000;      // any offset past every resource
 
+// A buffer resource whose base and size are made explicitly wave-uniform,
+// so it lives in SGPRs: a resource the compiler cannot prove uniform turns
+// every buffer access into a readfirstlane loop over the lanes.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t
 make_rsrc(const void* base, int bytes)
 {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes,
-                                           kRsrcWord3);
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+  const int n = __builtin_amdgcn_readfirstlane(bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(
+      reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), 0, n, kRsrcWord3);
 }
 
 __device__ __forceinline__ uint32_t
@@ -63,6 +72,16 @@ __device__ __forceinline__ float
 bf16_round(float f)
 {
   return __builtin_bit_cast(float, bf16_bits(f) << 16);
+}
+
+// Bit reinterpretation through a by-value copy: __builtin_bit_cast applied
+// directly to an element of an ext_vector_type accumulator reads the
+// vector's first element, not the indexed one.
+template <class To, class From>
+__device__ __forceinline__ To
+bits_as(From v)
+{
+  return __builtin_bit_cast(To, v);
 }
 
 __device__ __forceinline__ float
@@ -89,6 +108,95 @@ struct MmaI8 {
   }
 };
 
+// ---- epilogue stores (shared by the GEMM and the split-K reduction) ------
+// Four consecutive output columns n..n+3 of activation row m of problem P.
+__device__ __forceinline__ void
+store_bf16x4(const GemmProblem& P, int m, int n, float v0, float v1, float v2,
+             float v3)
+{
+  if (P.bias != nullptr) {
+    const uint2 bb = *reinterpret_cast<const uint2*>(P.bias + n);
+    v0 += bf16_to_f32(bb.x & 0xffffu);
+    v1 += bf16_to_f32(bb.x >> 16);
+    v2 += bf16_to_f32(bb.y & 0xffffu);
+    v3 += bf16_to_f32(bb.y >> 16);
+  }
+  uint2 o;
+  o.x = bf16_bits(v0) | (bf16_bits(v1) << 16);
+  o.y = bf16_bits(v2) | (bf16_bits(v3) << 16);
+  *reinterpret_cast<uint2*>(static_cast<uint16_t*>(P.y) + (size_t)m * P.ldy +
+                            n) = o;
+}
+
+__device__ __forceinline__ void
+store_i32x4(const GemmProblem& P, int m, int n, int v0, int v1, int v2, int v3)
+{
+  *reinterpret_cast<int4*>(static_cast<int32_t*>(P.y) + (size_t)m * P.ldy +
+                           n) = make_int4(v0, v1, v2, v3);
+}
+
+// Fused dequant: bf16_rne((float(acc) * sa[m]) * sw[n] (+ bias)).
+__device__ __forceinline__ void
+store_dequant4(const GemmProblem& P, int m, int n, int a0, int a1, int a2,
+               int a3)
+{
+  const float sam = P.sa[m];
+  const float4 swn = *reinterpret_cast<const float4*>(P.sw + n);
+  store_bf16x4(P, m, n, ((float)a0 * sam) * swn.x, ((float)a1 * sam) * swn.y,
+               ((float)a2 * sam) * swn.z, ((float)a3 * sam) * swn.w);
+}
+
+// SwiGLU: gate and up are rounded to bf16 first (the unfused GEMMs' output
+// precision), then silu(gate) * up in fp32, rounded to bf16.
+__device__ __forceinline__ uint32_t
+swiglu1(float g, float u)
+{
+  const float gv = bf16_round(g);
+  const float uv = bf16_round(u);
+  return bf16_bits((gv / (1.0f + expf(-gv))) * uv);
+}
+
+__device__ __forceinline__ void
+store_swiglu4(const GemmProblem& P, int m, int n, const float g[4],
+              const float u[4])
+{
+  uint2 o;
+  o.x = swiglu1(g[0], u[0]) | (swiglu1(g[1], u[1]) << 16);
+  o.y = swiglu1(g[2], u[2]) | (swiglu1(g[3], u[3]) << 16);
+  *reinterpret_cast<uint2*>(static_cast<uint16_t*>(P.y) + (size_t)m * P.ldy +
+                            n) = o;
+}
+
+// Which problem a linear tile index belongs to (uniform over the block).
+__device__ __forceinline__ int
+find_problem(const GemmBatch& B, int tile)
+{
+  int p = 0;
+#pragma unroll
+  for (int q = 1; q < kMaxProb; ++q) {
+    if (q < B.nprob && tile >= B.p[q].tile_begin) { p = q; }
+  }
+  return p;
+}
+
+// Tile origin (first activation row, first output column) of a tile of P.
+// Grouped raster: bands of 4 row-tiles, walked column by column, so the
+// tiles that run together share activation and weight rows in L2.
+template <Epi E>
+__device__ __forceinline__ void
+tile_origin(const GemmProblem& P, int tile, int* row0, int* col0)
+{
+  constexpr int GM = 4;
+  const int t = tile - P.tile_begin;
+  const int per_band = GM * P.tiles_n;
+  const int band = t / per_band;
+  const int first_m = band * GM;
+  const int gm = min(P.tiles_m - first_m, GM);
+  const int tin = t - band * per_band;
+  *row0 = (first_m + tin % gm) * kBM;
+  *col0 = (tin / gm) * tile_cols(E);
+}
+
 template <class Mma, Epi E>
 __global__ __launch_bounds__(kThreads, 1) void
 mot_gemm_kernel(const GemmBatch B)
@@ -98,102 +206,103 @@ mot_gemm_kernel(const GemmBatch B)
   __shared__ __attribute__((aligned(1024))) char lds0[kStage];
   __shared__ __attribute__((aligned(1024))) char lds1[kStage];
 
-  // ---- which tile -----------------------------------------------------
-  // Consecutive workgroups are dealt round-robin to the 8 XCDs; remap so
-  // each XCD walks a contiguous run of the tile list (and so shares its
-  // operands in its own L2).
-  const int T = B.total_tiles;
+  // ---- which tile, which share of K ------------------------------------
+  // Whole tiles: consecutive workgroups are dealt round-robin to the 8
+  // XCDs; remap so each XCD walks a contiguous run of the tile list (and so
+  // shares its operands in its own L2).  Split tiles follow, `split`
+  // consecutive workgroups per tile.
   const int bid = blockIdx.x;
-  const int lin = (T % 8 == 0) ? (bid % 8) * (T / 8) + bid / 8 : bid;
-  int p = 0;
-#pragma unroll
-  for (int q = 1; q < kMaxProb; ++q) {
-    if (q < B.nprob && lin >= B.p[q].tile_begin) { p = q; }
+  const int SB = B.split_begin;
+  int tile, share = 0;
+  const bool is_split = bid >= SB;
+  if (!is_split) {
+    tile = (SB % 8 == 0) ? (bid % 8) * (SB / 8) + bid / 8 : bid;
+  } else {
+    tile = SB + (bid - SB) / B.split;
+    share = (bid - SB) % B.split;
   }
-  const GemmProblem& P = B.p[p];
-  // Grouped raster: bands of 4 row-tiles, walked column by column.
-  constexpr int GM = 4;
-  const int t = lin - P.tile_begin;
-  const int per_band = GM * P.tiles_n;
-  const int band = t / per_band;
-  const int first_m = band * GM;
-  const int gm = min(P.tiles_m - first_m, GM);
-  const int tin = t - band * per_band;
-  const int mt = first_m + tin % gm;
-  const int nt = tin / gm;
+  const GemmProblem& P = B.p[find_problem(B, tile)];
+  int row0, col0;
+  tile_origin<E>(P, tile, &row0, &col0);
   constexpr int TC = tile_cols(E);
-  const int row0 = mt * kBM;
-  const int col0 = nt * TC;
 
   const int kbytes = B.kbytes;
   const int nk = (kbytes + kKB - 1) / kKB;
+  const int kbeg = is_split ? (share * nk) / B.split : 0;
+  const int kend = is_split ? ((share + 1) * nk) / B.split : nk;
+  const int nst = kend - kbeg;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave & 1;
   const int wn = wave >> 1;
 
-  // ---- operand resources ----------------------------------------------
-  const __amdgpu_buffer_rsrc_t ra = make_rsrc(
-      static_cast<const char*>(P.a) + (size_t)row0 * kbytes,
-      min(kBM, P.rows - row0) * kbytes);
-  __amdgpu_buffer_rsrc_t rw, ru;
-  if constexpr (E == Epi::kSwiglu) {
-    const int nvalid = min(TC, P.n - col0) * kbytes;
-    rw = make_rsrc(static_cast<const char*>(P.w) + (size_t)col0 * kbytes,
-                   nvalid);
-    ru = make_rsrc(static_cast<const char*>(P.w2) + (size_t)col0 * kbytes,
-                   nvalid);
-  } else {
-    rw = make_rsrc(static_cast<const char*>(P.w) + (size_t)col0 * kbytes,
-                   min(kBN, P.n - col0) * kbytes);
-    ru = rw;
-  }
+  // ---- operand extents --------------------------------------------------
+  const char* a_base = static_cast<const char*>(P.a) + (size_t)row0 * kbytes;
+  const int a_bytes = min(kBM, P.rows - row0) * kbytes;
+  const char* w_base = static_cast<const char*>(P.w) + (size_t)col0 * kbytes;
+  const int w_bytes = min(E == Epi::kSwiglu ? TC : kBN, P.n - col0) * kbytes;
+  const char* u_base = E == Epi::kSwiglu
+                           ? static_cast<const char*>(P.w2) + (size_t)col0 * kbytes
+                           : w_base;
 
-  // ---- direct-to-LDS loads --------------------------------------------
-  // A stage is 512 rows x 128 bytes: weight rows 0..255 then activation
-  // rows.  Wave w fills rows [128w, 128w+128) in 16 blocks of 8 rows; one
-  // instruction writes a 1 KiB block, lane l landing at byte 16*l: row
-  // l/8 of the block, chunk position l%8.  The swizzle (position = chunk ^
-  // (row & 7)) is applied on the global side: lane l fetches logical chunk
-  // (l%8) ^ (l/8).
+  // ---- LDS layout -------------------------------------------------------
+  // A stage is 512 rows x 128 bytes: weight rows 0..255, then activation
+  // rows.  Row r's logical 16-byte chunk c sits at chunk position
+  // c ^ ((r >> 1) & 7).  LDS serves 16 lanes of a 16-byte read per cycle
+  // over 64 four-byte banks (16 chunk-wide bank groups); a fragment read
+  // touches 16 consecutive rows at one logical chunk, whose bank groups
+  // (r & 1) * 8 + position are then all distinct.
+  //
+  // ---- direct-to-LDS loads ----------------------------------------------
+  // Wave w fills rows [128w, 128w+128) in 16 blocks of 8 rows; one
+  // instruction writes a 1 KiB block, lane l landing at byte 16*l: row l/8
+  // of the block, chunk position l%8.  The swizzle is applied on the
+  // global side: lane l fetches logical chunk (l%8) ^ key with key =
+  // ((row >> 1) & 7) = ((b & 1) << 2) | (l >> 4) for block b.
   //
   // SwiGLU tiles: wave column wn owns 64 output columns; its 128 weight
   // rows are 64 gate rows then the 64 matching up rows, so a lane's gate
   // and up accumulators cover the same outputs.
   const int lrow8 = lane >> 3;
-  const int lchunk = (lane & 7) ^ lrow8;
-  const int lane_off = lrow8 * kbytes + lchunk * 16;
+  const int key_lo = lane >> 4;
+  const int lane_off_even =
+      lrow8 * kbytes + (((lane & 7) ^ key_lo) << 4);
+  const int lane_off_odd =
+      lrow8 * kbytes + (((lane & 7) ^ (4 | key_lo)) << 4);
   // The range check that zero-fills rows past M / N and the K tail applies
   // to the per-lane (VGPR) offset, so every row offset is carried there;
   // only the stage's K offset, common to all rows, rides in the SGPR.
-  const int tail_off =
-      ((nk - 1) * kKB + lchunk * 16 < kbytes) ? 0 : kOobOffset;
+  const int tail_even =
+      ((nk - 1) * kKB + (((lane & 7) ^ key_lo) << 4) < kbytes) ? 0 : kOobOffset;
+  const int tail_odd =
+      ((nk - 1) * kKB + (((lane & 7) ^ (4 | key_lo)) << 4) < kbytes) ? 0
+                                                                    : kOobOffset;
 
   // Per-wave load parameters (wave-uniform): the resource for blocks 0-7
-  // and 8-15, the first operand row, and the block-index mask.
-  __amdgpu_buffer_rsrc_t r_lo = ra, r_hi = ra;
-  int row_base = (wave - 2) * 128;
-  int bmask = 15;
-  if (wave < 2) {
-    if constexpr (E == Epi::kSwiglu) {
-      r_lo = rw;            // gate rows
-      r_hi = ru;            // up rows
-      row_base = wave * 64;
-      bmask = 7;
-    } else {
-      r_lo = rw;
-      r_hi = rw;
-      row_base = wave * 128;
-    }
-  }
-  // Stages past the last one (kt >= nk) load nothing: their offsets are
-  // pushed out of range, so the hardware returns zeros without a memory
-  // access.  The loop below runs an even number of stages and relies on it.
-  auto issue_loads = [&](char* stage_base, int kt) {
-    const int ko = min(kt, nk - 1) * kKB;
-    const int v = lane_off + row_base * kbytes +
-                  (kt == nk - 1 ? tail_off : 0) + (kt >= nk ? kOobOffset : 0);
+  // and 8-15, the first operand row, and the block-index mask.  Waves 0-1
+  // load weight rows (SwiGLU: gate rows in blocks 0-7, up rows in 8-15),
+  // waves 2-3 activation rows.
+  const bool loads_w = wave < 2;
+  const char* lo_base = loads_w ? w_base : a_base;
+  const char* hi_base = loads_w ? u_base : a_base;
+  const int ld_bytes = loads_w ? w_bytes : a_bytes;
+  const __amdgpu_buffer_rsrc_t r_lo = make_rsrc(lo_base, ld_bytes);
+  const __amdgpu_buffer_rsrc_t r_hi = make_rsrc(hi_base, ld_bytes);
+  const int row_base =
+      loads_w ? (E == Epi::kSwiglu ? wave * 64 : wave * 128) : (wave - 2) * 128;
+  const int bmask = (loads_w && E == Epi::kSwiglu) ? 7 : 15;
+  // Stage `ktl` of this workgroup's K range.  Stages past the range load
+  // nothing: their offsets are pushed out of range, so the hardware
+  // returns zeros without a memory access.  The loop below runs an even
+  // number of stages and relies on it.
+  auto issue_loads = [&](char* stage_base, int ktl) {
+    const int kt = kbeg + ktl;
+    const int ko = __builtin_amdgcn_readfirstlane(min(kt, nk - 1) * kKB);
+    const bool last = kt == nk - 1;
+    const int oob = ktl >= nst ? kOobOffset : 0;
+    const int ve = lane_off_even + row_base * kbytes + (last ? tail_even : 0) + oob;
+    const int vo = lane_off_odd + row_base * kbytes + (last ? tail_odd : 0) + oob;
     char* dst = stage_base + wave * (128 * kKB);
 #pragma unroll
     for (int b = 0; b < 16; ++b) {
@@ -201,7 +310,7 @@ mot_gemm_kernel(const GemmBatch B)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           b < 8 ? r_lo : r_hi,
           (__attribute__((address_space(3))) void*)(dst + b * 1024), 16,
-          v + orow8 * kbytes, ko, 0, 0);
+          ((b & 1) ? vo : ve) + orow8 * kbytes, ko, 0, 0);
     }
   };
 
@@ -211,7 +320,7 @@ mot_gemm_kernel(const GemmBatch B)
   int rd[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    rd[s] = lr * kKB + (((2 * s + lh) ^ (lr & 7)) << 4);
+    rd[s] = lr * kKB + (((2 * s + lh) ^ ((lr >> 1) & 7)) << 4);
   }
   const int wbase = wn * 128 * kKB;
   const int abase = kBN * kKB + wm * 128 * kKB;
@@ -278,7 +387,7 @@ mot_gemm_kernel(const GemmBatch B)
   // The body is branch-free (after the final stage the extra loads fetch
   // nothing and the extra fragment reads are unused), which keeps the 256
   // accumulators in AGPRs across the whole loop.
-  auto stage = [&](char* cur, const char* nxt, int kt) {
+  auto stage = [&](char* cur, const char* nxt, int ktl) {
 #pragma unroll
     for (int s = 0; s < 3; ++s) {
       read_frags(cur, s + 1, (s + 1) & 1);
@@ -287,105 +396,168 @@ mot_gemm_kernel(const GemmBatch B)
     }
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     __syncthreads();
-    issue_loads(cur, kt + 2);
+    issue_loads(cur, ktl + 2);
     read_frags(nxt, 0, 0);
     mma_step(1);
     interleave_loads_reads();
   };
 
   // ---- main loop: an even number of stages; a padding stage (K past the
-  // end) reads as zeros and adds exactly 0 to every accumulator ------------
-  const int nk_even = (nk + 1) & ~1;
+  // range) reads as zeros and adds exactly 0 to every accumulator --------
+  const int nst_even = (nst + 1) & ~1;
   issue_loads(lds0, 0);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   issue_loads(lds1, 1);
   read_frags(lds0, 0, 0);
-  for (int kt = 0; kt < nk_even; kt += 2) {
-    stage(lds0, lds1, kt);
-    stage(lds1, lds0, kt + 1);
+  for (int ktl = 0; ktl < nst_even; ktl += 2) {
+    stage(lds0, lds1, ktl);
+    stage(lds1, lds0, ktl + 1);
   }
   // No load may still be writing LDS when the workgroup retires.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // ---- epilogue ---------------------------------------------------------
-  // acc[i][j][r]: output column (within the wave's block) i*32 + (r>>2)*8 +
-  // lh*4 + (r&3), activation row j*32 + lr.
+  // acc[i][j][r]: tile column (weight row within the tile) wn*128 + i*32 +
+  // (r>>2)*8 + lh*4 + (r&3), tile row wm*128 + j*32 + lr.
+  if (is_split) {
+    // Raw accumulators of this K share -> workspace [kBM][kBN] (rows past
+    // the problem are never read back).
+    int32_t* wsb = static_cast<int32_t*>(B.ws) +
+                   (size_t)((tile - SB) * B.split + share) * (kBM * kBN);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int ml = wm * 128 + j * 32 + lr;
+      if (row0 + ml >= P.rows) { continue; }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int nl = wn * 128 + i * 32 + g * 8 + lh * 4;
+          const auto& a = acc[i][j];
+          *reinterpret_cast<int4*>(wsb + ml * kBN + nl) = make_int4(
+              bits_as<int>(a[g * 4 + 0]), bits_as<int>(a[g * 4 + 1]),
+              bits_as<int>(a[g * 4 + 2]), bits_as<int>(a[g * 4 + 3]));
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int m = row0 + wm * 128 + j * 32 + lr;
     if (m >= P.rows) { continue; }
     if constexpr (E == Epi::kSwiglu) {
-      uint16_t* yrow = static_cast<uint16_t*>(P.y) + (size_t)m * P.ldy;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int n = col0 + wn * 64 + i * 32 + g * 8 + lh * 4;
           if (n >= P.n) { continue; }
-          uint32_t h[4];
+          float gv[4], uv[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float gv = bf16_round(acc[i][j][g * 4 + e]);
-            const float uv = bf16_round(acc[i + 2][j][g * 4 + e]);
-            const float sv = gv / (1.0f + expf(-gv));
-            h[e] = bf16_bits(sv * uv);
+            gv[e] = acc[i][j][g * 4 + e];
+            uv[e] = acc[i + 2][j][g * 4 + e];
           }
-          uint2 o;
-          o.x = h[0] | (h[1] << 16);
-          o.y = h[2] | (h[3] << 16);
-          *reinterpret_cast<uint2*>(yrow + n) = o;
-        }
-      }
-    } else if constexpr (E == Epi::kI32) {
-      int32_t* yrow = static_cast<int32_t*>(P.y) + (size_t)m * P.ldy;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int n = col0 + wn * 128 + i * 32 + g * 8 + lh * 4;
-          if (n >= P.n) { continue; }
-          int4 o;
-          o.x = (int)acc[i][j][g * 4 + 0];
-          o.y = (int)acc[i][j][g * 4 + 1];
-          o.z = (int)acc[i][j][g * 4 + 2];
-          o.w = (int)acc[i][j][g * 4 + 3];
-          *reinterpret_cast<int4*>(yrow + n) = o;
+          store_swiglu4(P, m, n, gv, uv);
         }
       }
     } else {
-      uint16_t* yrow = static_cast<uint16_t*>(P.y) + (size_t)m * P.ldy;
-      float sam = 1.0f;
-      if constexpr (E == Epi::kDequantBf16) { sam = P.sa[m]; }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int n = col0 + wn * 128 + i * 32 + g * 8 + lh * 4;
           if (n >= P.n) { continue; }
-          float v[4];
-          if constexpr (E == Epi::kDequantBf16) {
-            const float4 swn = *reinterpret_cast<const float4*>(P.sw + n);
-            v[0] = ((float)acc[i][j][g * 4 + 0] * sam) * swn.x;
-            v[1] = ((float)acc[i][j][g * 4 + 1] * sam) * swn.y;
-            v[2] = ((float)acc[i][j][g * 4 + 2] * sam) * swn.z;
-            v[3] = ((float)acc[i][j][g * 4 + 3] * sam) * swn.w;
+          const auto& a = acc[i][j];
+          if constexpr (E == Epi::kI32) {
+            store_i32x4(P, m, n, a[g * 4], a[g * 4 + 1], a[g * 4 + 2],
+                        a[g * 4 + 3]);
+          } else if constexpr (E == Epi::kDequantBf16) {
+            store_dequant4(P, m, n, a[g * 4], a[g * 4 + 1], a[g * 4 + 2],
+                           a[g * 4 + 3]);
           } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) { v[e] = acc[i][j][g * 4 + e]; }
+            store_bf16x4(P, m, n, a[g * 4], a[g * 4 + 1], a[g * 4 + 2],
+                         a[g * 4 + 3]);
           }
-          if (P.bias != nullptr) {
-            const uint2 bb = *reinterpret_cast<const uint2*>(P.bias + n);
-            v[0] += bf16_to_f32(bb.x & 0xffffu);
-            v[1] += bf16_to_f32(bb.x >> 16);
-            v[2] += bf16_to_f32(bb.y & 0xffffu);
-            v[3] += bf16_to_f32(bb.y >> 16);
-          }
-          uint2 o;
-          o.x = bf16_bits(v[0]) | (bf16_bits(v[1]) << 16);
-          o.y = bf16_bits(v[2]) | (bf16_bits(v[3]) << 16);
-          *reinterpret_cast<uint2*>(yrow + n) = o;
         }
+      }
+    }
+  }
+}
+
+// ---- split-K reduction --------------------------------------------------
+// One workgroup per 16 rows of a split tile: sums the tile's K shares in
+// share order (fp32 adds for bf16 GEMMs, exact int32 adds for int8) and
+// applies the same epilogue as mot_gemm_kernel.
+template <bool kInt, Epi E>
+__global__ __launch_bounds__(256) void
+split_reduce_kernel(const GemmBatch B)
+{
+  constexpr int kRowsPerBlock = 16;
+  const int ts = blockIdx.x / (kBM / kRowsPerBlock);
+  const int tile = B.split_begin + ts;
+  const GemmProblem& P = B.p[find_problem(B, tile)];
+  int row0, col0;
+  tile_origin<E>(P, tile, &row0, &col0);
+  const int32_t* wsb =
+      static_cast<const int32_t*>(B.ws) + (size_t)ts * B.split * (kBM * kBN);
+  const int q = threadIdx.x & 63;             // column quad within the tile
+  for (int rr = threadIdx.x >> 6; rr < kRowsPerBlock; rr += 4) {
+    const int ml = (blockIdx.x % (kBM / kRowsPerBlock)) * kRowsPerBlock + rr;
+    const int m = row0 + ml;
+    if (m >= P.rows) { return; }
+    const int nl = q * 4;
+    auto sum4 = [&](int col) {
+      int4 r = make_int4(0, 0, 0, 0);
+      float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int sh = 0; sh < B.split; ++sh) {
+        const int4 v = *reinterpret_cast<const int4*>(
+            wsb + (size_t)sh * (kBM * kBN) + ml * kBN + col);
+        if constexpr (kInt) {
+          r.x += v.x; r.y += v.y; r.z += v.z; r.w += v.w;
+        } else {
+          f.x += bits_as<float>(v.x);
+          f.y += bits_as<float>(v.y);
+          f.z += bits_as<float>(v.z);
+          f.w += bits_as<float>(v.w);
+        }
+      }
+      if constexpr (kInt) {
+        return make_float4(bits_as<float>(r.x),
+                           bits_as<float>(r.y),
+                           bits_as<float>(r.z),
+                           bits_as<float>(r.w));
+      } else {
+        return f;
+      }
+    };
+    if constexpr (E == Epi::kSwiglu) {
+      // Gate columns sit at tile columns wn*128 + [0, 64), their up partners
+      // 64 further on; the output column is col0 + wn*64 + that offset.
+      if (((nl >> 6) & 1) != 0) { continue; }
+      const int n = col0 + (nl >> 7) * 64 + (nl & 63);
+      if (n >= P.n) { continue; }
+      const float4 g = sum4(nl), u = sum4(nl + 64);
+      const float gv[4] = {g.x, g.y, g.z, g.w};
+      const float uv[4] = {u.x, u.y, u.z, u.w};
+      store_swiglu4(P, m, n, gv, uv);
+    } else {
+      const int n = col0 + nl;
+      if (n >= P.n) { continue; }
+      const float4 v = sum4(nl);
+      if constexpr (E == Epi::kI32) {
+        store_i32x4(P, m, n, bits_as<int>(v.x),
+                    bits_as<int>(v.y), bits_as<int>(v.z),
+                    bits_as<int>(v.w));
+      } else if constexpr (E == Epi::kDequantBf16) {
+        store_dequant4(P, m, n, bits_as<int>(v.x),
+                       bits_as<int>(v.y),
+                       bits_as<int>(v.z),
+                       bits_as<int>(v.w));
+      } else {
+        store_bf16x4(P, m, n, v.x, v.y, v.z, v.w);
       }
     }
   }
@@ -488,8 +660,14 @@ hipError_t
 launch_gemm(const GemmBatch& b, hipStream_t s)
 {
   if (b.total_tiles <= 0) { return hipSuccess; }
-  hipLaunchKernelGGL((mot_gemm_kernel<Mma, E>), dim3(b.total_tiles),
+  hipLaunchKernelGGL((mot_gemm_kernel<Mma, E>), dim3(grid_blocks(b)),
                      dim3(kThreads), 0, s, b);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || b.split_begin >= b.total_tiles) { return e; }
+  constexpr bool kInt = std::is_same<Mma, MmaI8>::value;
+  hipLaunchKernelGGL((split_reduce_kernel<kInt, E>),
+                     dim3((b.total_tiles - b.split_begin) * (kBM / 16)),
+                     dim3(256), 0, s, b);
   return hipGetLastError();
 }
 
@@ -563,6 +741,10 @@ kernels_loadable()
       reinterpret_cast<const void*>(&mot_gemm_kernel<MmaBf16, Epi::kSwiglu>),
       reinterpret_cast<const void*>(&mot_gemm_kernel<MmaI8, Epi::kI32>),
       reinterpret_cast<const void*>(&mot_gemm_kernel<MmaI8, Epi::kDequantBf16>),
+      reinterpret_cast<const void*>(&split_reduce_kernel<false, Epi::kBf16>),
+      reinterpret_cast<const void*>(&split_reduce_kernel<false, Epi::kSwiglu>),
+      reinterpret_cast<const void*>(&split_reduce_kernel<true, Epi::kI32>),
+      reinterpret_cast<const void*>(&split_reduce_kernel<true, Epi::kDequantBf16>),
       reinterpret_cast<const void*>(&quant_rows_i8_kernel),
       reinterpret_cast<const void*>(&swiglu_kernel),
       reinterpret_cast<const void*>(&gather_rows_kernel<true>),
