@@ -314,3 +314,43 @@ def test_split_tail_matches_unsplit(ops, ops_nosplit, Mu, Mg, K, N):
         ref = oracle.linear_bf16(xb, w, row_ids=np.array([r], np.int32))
         assert max_rel(a[r:r + 1], ref) <= MAX_REL
         assert rel_l2(a[r:r + 1], ref) < REF_BAR
+
+
+@pytest.fixture(scope="module")
+def ops_4waves():
+    """A context built with the 4-wave GEMM workgroup (U15H_WAVES=4)."""
+    import os
+    old = os.environ.get("U15H_WAVES")
+    os.environ["U15H_WAVES"] = "4"
+    try:
+        o = u15h.Ops(0)
+    finally:
+        if old is None:
+            del os.environ["U15H_WAVES"]
+        else:
+            os.environ["U15H_WAVES"] = old
+    yield o
+    torch.cuda.synchronize()
+    o.close()
+
+
+@pytest.mark.parametrize("Mu,Mg,K,N", [(37, 263, 1032, 264), (128, 4096, 4096, 1024)])
+def test_workgroup_shapes_agree(ops, ops_4waves, Mu, Mg, K, N):
+    """The 8-wave and 4-wave GEMM workgroups compute the same MFMA
+    products in the same K order per element: identical bf16 output, and
+    identical fused SwiGLU output."""
+    M = Mu + Mg
+    g = torch.Generator(device="cuda").manual_seed(K + N)
+    x = torch.randn(M, K, generator=g, device="cuda").to(torch.bfloat16)
+    ws = [(torch.randn(N, K, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+          for _ in range(4)]
+    outs = []
+    for o in (ops, ops_4waves):
+        y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+        h = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+        o.mot_linear(x, Mu, Mg, K, [dict(w_und=ws[0], w_gen=ws[1], y=y)])
+        o.mot_gate_up_swiglu(x, Mu, Mg, K, ws[0], ws[1], ws[2], ws[3], h)
+        outs.append((y, h))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert torch.equal(outs[0][1], outs[1][1])

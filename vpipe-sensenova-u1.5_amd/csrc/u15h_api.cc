@@ -21,6 +21,7 @@ struct u15h_ctx {
   int device = 0;
   int num_cu = 256;
   bool split_on = true;      // env U15H_SPLIT=0 turns the split-K tail off
+  int waves = 8;             // GEMM workgroup: 8 or 4 waves (env U15H_WAVES)
   // Partial-sum workspace of split tiles: at most num_cu K shares of one
   // 256x256 tile each (allocated on first use, kept until destroy).
   void* split_ws = nullptr;
@@ -261,7 +262,7 @@ linear_i8_route(u15h_ctx* ctx, hipStream_t s, const u15h_bf16* x,
               u15h::tile_cols(Epi::kDequantBf16));
   u15h_status st = plan_split(ctx, b);
   if (st != U15H_OK) { return st; }
-  return launched(ctx, u15h::launch_gemm_i8(b, Epi::kDequantBf16, s),
+  return launched(ctx, u15h::launch_gemm_i8(b, Epi::kDequantBf16, ctx->waves, s),
                   "gemm_i8");
 }
 
@@ -318,6 +319,7 @@ u15h_create(int device, u15h_ctx** out)
   ctx->device = device;
   ctx->num_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
   ctx->split_on = env_int("U15H_SPLIT", 1) != 0;
+  ctx->waves = env_int("U15H_WAVES", 8) == 4 ? 4 : 8;
   ctx->i8_min_m = std::max(1, env_int("U15H_I8_MIN_M", 1024));
   *out = ctx;
   return U15H_OK;
@@ -372,7 +374,7 @@ u15h_linear(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
   add_problem(b, x, w, nullptr, y, bias, nullptr, nullptr, M, N, N,
               u15h::tile_cols(Epi::kBf16));
   if ((st = plan_split(ctx, b)) != U15H_OK) { return st; }
-  return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kBf16, s), "gemm_bf16");
+  return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kBf16, ctx->waves, s), "gemm_bf16");
 }
 
 u15h_status
@@ -426,7 +428,7 @@ u15h_mot_linear(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
   }
   if ((st = check_tiles(ctx, b)) != U15H_OK) { return st; }
   if ((st = plan_split(ctx, b)) != U15H_OK) { return st; }
-  return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kBf16, as_stream(stream)),
+  return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kBf16, ctx->waves, as_stream(stream)),
                   "mot_gemm_bf16");
 }
 
@@ -485,7 +487,7 @@ u15h_mot_gate_up_swiglu(u15h_ctx* ctx, u15h_stream stream,
               tc);
   if ((st = check_tiles(ctx, b)) != U15H_OK) { return st; }
   if ((st = plan_split(ctx, b)) != U15H_OK) { return st; }
-  return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kSwiglu, as_stream(stream)),
+  return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kSwiglu, ctx->waves, as_stream(stream)),
                   "mot_gate_up_swiglu");
 }
 
@@ -597,7 +599,7 @@ mot_gemm_i8_common(u15h_ctx* ctx, u15h_stream stream, const int8_t* xq,
   }
   if ((st = check_tiles(ctx, b)) != U15H_OK) { return st; }
   if ((st = plan_split(ctx, b)) != U15H_OK) { return st; }
-  return launched(ctx, u15h::launch_gemm_i8(b, epi, as_stream(stream)),
+  return launched(ctx, u15h::launch_gemm_i8(b, epi, ctx->waves, as_stream(stream)),
                   deq ? "mot_gemm_i8" : "mot_gemm_i8_i32");
 }
 

@@ -14,7 +14,6 @@ namespace u15h {
 constexpr int kBM = 256;          // activation rows per tile
 constexpr int kBN = 256;          // weight rows (output columns) per tile
 constexpr int kKB = 128;          // bytes of K per stage
-constexpr int kThreads = 256;     // 4 waves of 64
 constexpr int kMaxProb = 8;       // problems (weight sets x projections) per launch
 
 // What the epilogue does with the fp32 / int32 accumulators.
@@ -70,8 +69,12 @@ inline size_t split_ws_bytes(const GemmBatch& b)
 }
 
 // Kernel launchers (u15h_kernels.hip).  All are asynchronous on `s`.
-hipError_t launch_gemm_bf16(const GemmBatch& b, Epi epi, hipStream_t s);
-hipError_t launch_gemm_i8(const GemmBatch& b, Epi epi, hipStream_t s);
+// `waves` selects the GEMM kernel's workgroup shape: 4 (one wave per SIMD,
+// 128x128 per wave) or 8 (two per SIMD, 128x64 per wave).
+hipError_t launch_gemm_bf16(const GemmBatch& b, Epi epi, int waves,
+                            hipStream_t s);
+hipError_t launch_gemm_i8(const GemmBatch& b, Epi epi, int waves,
+                          hipStream_t s);
 hipError_t launch_quant_rows_i8(const uint16_t* x, int rows, int K,
                                 int8_t* q, float* sc, hipStream_t s);
 hipError_t launch_swiglu(const uint16_t* g, const uint16_t* u, uint16_t* o,

@@ -197,10 +197,20 @@ tile_origin(const GemmProblem& P, int tile, int* row0, int* col0)
   *col0 = (tin / gm) * tile_cols(E);
 }
 
-template <class Mma, Epi E>
-__global__ __launch_bounds__(kThreads, 1) void
+// WN = waves along the tile's N (weight-row) extent; 2 waves along M.
+//   WN = 2: 4 waves, each 128 x 128 (4 x 4 accumulators of 32 x 32)
+//   WN = 4: 8 waves, two per SIMD, each 128 x 64 (2 x 4 accumulators); a
+//           wave waiting on LDS, memory or the barrier leaves the matrix
+//           core to the other wave of its SIMD.
+template <class Mma, Epi E, int WN>
+__global__ __launch_bounds__(128 * WN, 1) void
 mot_gemm_kernel(const GemmBatch B)
 {
+  constexpr int kWaves = 2 * WN;
+  constexpr int NW = kBN / WN;            // weight rows (tile columns) per wave
+  constexpr int FI = NW / 32;             // weight fragments per sub-step
+  constexpr int FJ = 4;                   // activation fragments (128 rows)
+  constexpr int LB = 64 / kWaves;         // 1 KiB load blocks per wave per stage
   // Two LDS stages as two objects, so the compiler can tell the fragment
   // reads of one stage from the direct-to-LDS loads filling the other.
   __shared__ __attribute__((aligned(1024))) char lds0[kStage];
@@ -235,7 +245,7 @@ mot_gemm_kernel(const GemmBatch B)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave & 1;
-  const int wn = wave >> 1;
+  const int wn = wave >> 1;               // 0 .. WN-1
 
   // ---- operand extents --------------------------------------------------
   const char* a_base = static_cast<const char*>(P.a) + (size_t)row0 * kbytes;
@@ -255,15 +265,17 @@ mot_gemm_kernel(const GemmBatch B)
   // (r & 1) * 8 + position are then all distinct.
   //
   // ---- direct-to-LDS loads ----------------------------------------------
-  // Wave w fills rows [128w, 128w+128) in 16 blocks of 8 rows; one
+  // Wave w fills stage rows [8*LB*w, 8*LB*(w+1)) in LB blocks of 8 rows
+  // (waves 0..WN-1 the weight rows, which are then exactly the rows wave
+  // column w computes with; the others the activation rows).  One
   // instruction writes a 1 KiB block, lane l landing at byte 16*l: row l/8
   // of the block, chunk position l%8.  The swizzle is applied on the
   // global side: lane l fetches logical chunk (l%8) ^ key with key =
   // ((row >> 1) & 7) = ((b & 1) << 2) | (l >> 4) for block b.
   //
-  // SwiGLU tiles: wave column wn owns 64 output columns; its 128 weight
-  // rows are 64 gate rows then the 64 matching up rows, so a lane's gate
-  // and up accumulators cover the same outputs.
+  // SwiGLU tiles: wave column wn owns NW/2 output columns; its NW weight
+  // rows are NW/2 gate rows then the NW/2 matching up rows, so a lane's
+  // gate and up accumulators cover the same outputs.
   const int lrow8 = lane >> 3;
   const int key_lo = lane >> 4;
   const int lane_off_even =
@@ -279,19 +291,18 @@ mot_gemm_kernel(const GemmBatch B)
       ((nk - 1) * kKB + (((lane & 7) ^ (4 | key_lo)) << 4) < kbytes) ? 0
                                                                     : kOobOffset;
 
-  // Per-wave load parameters (wave-uniform): the resource for blocks 0-7
-  // and 8-15, the first operand row, and the block-index mask.  Waves 0-1
-  // load weight rows (SwiGLU: gate rows in blocks 0-7, up rows in 8-15),
-  // waves 2-3 activation rows.
-  const bool loads_w = wave < 2;
+  // Per-wave load parameters (wave-uniform): the resource for the first
+  // and second half of the blocks, the first operand row, and the
+  // block-index mask.
+  const bool loads_w = wave < WN;
   const char* lo_base = loads_w ? w_base : a_base;
   const char* hi_base = loads_w ? u_base : a_base;
   const int ld_bytes = loads_w ? w_bytes : a_bytes;
   const __amdgpu_buffer_rsrc_t r_lo = make_rsrc(lo_base, ld_bytes);
   const __amdgpu_buffer_rsrc_t r_hi = make_rsrc(hi_base, ld_bytes);
-  const int row_base =
-      loads_w ? (E == Epi::kSwiglu ? wave * 64 : wave * 128) : (wave - 2) * 128;
-  const int bmask = (loads_w && E == Epi::kSwiglu) ? 7 : 15;
+  const int row_base = loads_w ? (E == Epi::kSwiglu ? wave * (NW / 2) : wave * NW)
+                               : (wave - WN) * (8 * LB);
+  const int bmask = (loads_w && E == Epi::kSwiglu) ? (LB / 2 - 1) : (LB - 1);
   // Stage `ktl` of this workgroup's K range.  Stages past the range load
   // nothing: their offsets are pushed out of range, so the hardware
   // returns zeros without a memory access.  The loop below runs an even
@@ -303,12 +314,12 @@ mot_gemm_kernel(const GemmBatch B)
     const int oob = ktl >= nst ? kOobOffset : 0;
     const int ve = lane_off_even + row_base * kbytes + (last ? tail_even : 0) + oob;
     const int vo = lane_off_odd + row_base * kbytes + (last ? tail_odd : 0) + oob;
-    char* dst = stage_base + wave * (128 * kKB);
+    char* dst = stage_base + wave * (8 * LB * kKB);
 #pragma unroll
-    for (int b = 0; b < 16; ++b) {
+    for (int b = 0; b < LB; ++b) {
       const int orow8 = (b & bmask) * 8;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          b < 8 ? r_lo : r_hi,
+          b < LB / 2 ? r_lo : r_hi,
           (__attribute__((address_space(3))) void*)(dst + b * 1024), 16,
           ((b & 1) ? vo : ve) + orow8 * kbytes, ko, 0, 0);
     }
@@ -322,58 +333,68 @@ mot_gemm_kernel(const GemmBatch B)
   for (int s = 0; s < 4; ++s) {
     rd[s] = lr * kKB + (((2 * s + lh) ^ ((lr >> 1) & 7)) << 4);
   }
-  const int wbase = wn * 128 * kKB;
+  const int wbase = wn * NW * kKB;
   const int abase = kBN * kKB + wm * 128 * kKB;
 
-  typename Mma::acc_t acc[4][4];
+  typename Mma::acc_t acc[FI][FJ];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < FI; ++i) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) { acc[i][j] = typename Mma::acc_t{}; }
+    for (int j = 0; j < FJ; ++j) { acc[i][j] = typename Mma::acc_t{}; }
   }
 
-  i32x4_t fa[2][4], fb[2][4];
+  i32x4_t fa[2][FI], fb[2][FJ];
   auto read_frags = [&](const char* base, int s, int buf) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < FI; ++i) {
       fa[buf][i] = *reinterpret_cast<const i32x4_t*>(base + wbase +
                                                      i * 32 * kKB + rd[s]);
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < FJ; ++j) {
       fb[buf][j] = *reinterpret_cast<const i32x4_t*>(base + abase +
                                                      j * 32 * kKB + rd[s]);
     }
   };
   auto mma_step = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < FI; ++i) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < FJ; ++j) {
         acc[i][j] = Mma::run(fa[buf][i], fb[buf][j], acc[i][j]);
       }
     }
   };
   // Scheduling masks of __builtin_amdgcn_sched_group_barrier.
   constexpr int kSchedMfma = 0x008, kSchedVmem = 0x010, kSchedDsRead = 0x100;
-  // 8 fragment reads spread over 16 MFMAs.
+  constexpr int kMfmaPerStep = FI * FJ;
+  constexpr int kReadsPerStep = FI + FJ;
+  // The next sub-step's fragment reads spread over this sub-step's MFMAs.
   auto interleave_reads = [&]() {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < kMfmaPerStep; ++k) {
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      if (k < kReadsPerStep) {
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      }
     }
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8, 0);
   };
-  // 16 direct loads and 8 fragment reads spread over 16 MFMAs.
+  // The direct loads of stage kt+2 and the next stage's first fragment
+  // reads spread over the last sub-step's MFMAs.
   auto interleave_loads_reads = [&]() {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < kMfmaPerStep; ++k) {
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
+      constexpr int kLoadsPerMfma = (LB + kMfmaPerStep - 1) / kMfmaPerStep;
+#pragma unroll
+      for (int l = 0; l < kLoadsPerMfma; ++l) {
+        if (k * kLoadsPerMfma + l < LB) {
+          __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
+        }
+      }
+      if (k < kReadsPerStep) {
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      }
     }
   };
 
@@ -418,7 +439,7 @@ mot_gemm_kernel(const GemmBatch B)
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // ---- epilogue ---------------------------------------------------------
-  // acc[i][j][r]: tile column (weight row within the tile) wn*128 + i*32 +
+  // acc[i][j][r]: tile column (weight row within the tile) wn*NW + i*32 +
   // (r>>2)*8 + lh*4 + (r&3), tile row wm*128 + j*32 + lr.
   if (is_split) {
     // Raw accumulators of this K share -> workspace [kBM][kBN] (rows past
@@ -426,14 +447,14 @@ mot_gemm_kernel(const GemmBatch B)
     int32_t* wsb = static_cast<int32_t*>(B.ws) +
                    (size_t)((tile - SB) * B.split + share) * (kBM * kBN);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < FJ; ++j) {
       const int ml = wm * 128 + j * 32 + lr;
       if (row0 + ml >= P.rows) { continue; }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < FI; ++i) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int nl = wn * 128 + i * 32 + g * 8 + lh * 4;
+          const int nl = wn * NW + i * 32 + g * 8 + lh * 4;
           const auto& a = acc[i][j];
           *reinterpret_cast<int4*>(wsb + ml * kBN + nl) = make_int4(
               bits_as<int>(a[g * 4 + 0]), bits_as<int>(a[g * 4 + 1]),
@@ -444,31 +465,31 @@ mot_gemm_kernel(const GemmBatch B)
     return;
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < FJ; ++j) {
     const int m = row0 + wm * 128 + j * 32 + lr;
     if (m >= P.rows) { continue; }
     if constexpr (E == Epi::kSwiglu) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < FI / 2; ++i) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int n = col0 + wn * 64 + i * 32 + g * 8 + lh * 4;
+          const int n = col0 + wn * (NW / 2) + i * 32 + g * 8 + lh * 4;
           if (n >= P.n) { continue; }
           float gv[4], uv[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             gv[e] = acc[i][j][g * 4 + e];
-            uv[e] = acc[i + 2][j][g * 4 + e];
+            uv[e] = acc[i + FI / 2][j][g * 4 + e];
           }
           store_swiglu4(P, m, n, gv, uv);
         }
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < FI; ++i) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int n = col0 + wn * 128 + i * 32 + g * 8 + lh * 4;
+          const int n = col0 + wn * NW + i * 32 + g * 8 + lh * 4;
           if (n >= P.n) { continue; }
           const auto& a = acc[i][j];
           if constexpr (E == Epi::kI32) {
@@ -491,10 +512,11 @@ mot_gemm_kernel(const GemmBatch B)
 // One workgroup per 16 rows of a split tile: sums the tile's K shares in
 // share order (fp32 adds for bf16 GEMMs, exact int32 adds for int8) and
 // applies the same epilogue as mot_gemm_kernel.
-template <bool kInt, Epi E>
+template <bool kInt, Epi E, int WN>
 __global__ __launch_bounds__(256) void
 split_reduce_kernel(const GemmBatch B)
 {
+  constexpr int NW = kBN / WN;
   constexpr int kRowsPerBlock = 16;
   const int ts = blockIdx.x / (kBM / kRowsPerBlock);
   const int tile = B.split_begin + ts;
@@ -534,12 +556,13 @@ split_reduce_kernel(const GemmBatch B)
       }
     };
     if constexpr (E == Epi::kSwiglu) {
-      // Gate columns sit at tile columns wn*128 + [0, 64), their up partners
-      // 64 further on; the output column is col0 + wn*64 + that offset.
-      if (((nl >> 6) & 1) != 0) { continue; }
-      const int n = col0 + (nl >> 7) * 64 + (nl & 63);
+      // Gate columns sit at tile columns wn*NW + [0, NW/2), their up
+      // partners NW/2 further on; the output column is col0 + wn*NW/2 +
+      // that offset.
+      if ((nl % NW) >= NW / 2) { continue; }
+      const int n = col0 + (nl / NW) * (NW / 2) + (nl % NW);
       if (n >= P.n) { continue; }
-      const float4 g = sum4(nl), u = sum4(nl + 64);
+      const float4 g = sum4(nl), u = sum4(nl + NW / 2);
       const float gv[4] = {g.x, g.y, g.z, g.w};
       const float uv[4] = {u.x, u.y, u.z, u.w};
       store_swiglu4(P, m, n, gv, uv);
@@ -655,40 +678,49 @@ gather_rows_kernel(const uint16_t* __restrict__ src,
   for (int c = threadIdx.x; c < cols / 8; c += 256) { d[c] = s[c]; }
 }
 
-template <class Mma, Epi E>
+template <class Mma, Epi E, int WN>
 hipError_t
 launch_gemm(const GemmBatch& b, hipStream_t s)
 {
   if (b.total_tiles <= 0) { return hipSuccess; }
-  hipLaunchKernelGGL((mot_gemm_kernel<Mma, E>), dim3(grid_blocks(b)),
-                     dim3(kThreads), 0, s, b);
+  hipLaunchKernelGGL((mot_gemm_kernel<Mma, E, WN>), dim3(grid_blocks(b)),
+                     dim3(128 * WN), 0, s, b);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || b.split_begin >= b.total_tiles) { return e; }
   constexpr bool kInt = std::is_same<Mma, MmaI8>::value;
-  hipLaunchKernelGGL((split_reduce_kernel<kInt, E>),
+  hipLaunchKernelGGL((split_reduce_kernel<kInt, E, WN>),
                      dim3((b.total_tiles - b.split_begin) * (kBM / 16)),
                      dim3(256), 0, s, b);
   return hipGetLastError();
 }
 
+template <class Mma, Epi E>
+hipError_t
+launch_gemm_waves(const GemmBatch& b, int waves, hipStream_t s)
+{
+  return waves == 4 ? launch_gemm<Mma, E, 2>(b, s) : launch_gemm<Mma, E, 4>(b, s);
+}
+
 }  // namespace
 
 hipError_t
-launch_gemm_bf16(const GemmBatch& b, Epi epi, hipStream_t s)
+launch_gemm_bf16(const GemmBatch& b, Epi epi, int waves, hipStream_t s)
 {
   switch (epi) {
-    case Epi::kBf16: return launch_gemm<MmaBf16, Epi::kBf16>(b, s);
-    case Epi::kSwiglu: return launch_gemm<MmaBf16, Epi::kSwiglu>(b, s);
+    case Epi::kBf16: return launch_gemm_waves<MmaBf16, Epi::kBf16>(b, waves, s);
+    case Epi::kSwiglu:
+      return launch_gemm_waves<MmaBf16, Epi::kSwiglu>(b, waves, s);
     default: return hipErrorInvalidValue;
   }
 }
 
 hipError_t
-launch_gemm_i8(const GemmBatch& b, Epi epi, hipStream_t s)
+launch_gemm_i8(const GemmBatch& b, Epi epi, int waves, hipStream_t s)
 {
   switch (epi) {
-    case Epi::kI32: return launch_gemm<MmaI8, Epi::kI32>(b, s);
-    case Epi::kDequantBf16: return launch_gemm<MmaI8, Epi::kDequantBf16>(b, s);
+    case Epi::kI32: return launch_gemm_waves<MmaI8, Epi::kI32>(b, waves, s);
+    case Epi::kDequantBf16:
+      return launch_gemm_waves<MmaI8, Epi::kDequantBf16>(b, waves, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -733,18 +765,31 @@ launch_gather_rows(const uint16_t* src, const int32_t* perm, int M, int cols,
   return hipGetLastError();
 }
 
+template <int WN>
+bool
+gemm_kernels_loadable()
+{
+  const void* fns[] = {
+      reinterpret_cast<const void*>(&mot_gemm_kernel<MmaBf16, Epi::kBf16, WN>),
+      reinterpret_cast<const void*>(&mot_gemm_kernel<MmaBf16, Epi::kSwiglu, WN>),
+      reinterpret_cast<const void*>(&mot_gemm_kernel<MmaI8, Epi::kI32, WN>),
+      reinterpret_cast<const void*>(&mot_gemm_kernel<MmaI8, Epi::kDequantBf16, WN>),
+      reinterpret_cast<const void*>(&split_reduce_kernel<false, Epi::kBf16, WN>),
+      reinterpret_cast<const void*>(&split_reduce_kernel<false, Epi::kSwiglu, WN>),
+      reinterpret_cast<const void*>(&split_reduce_kernel<true, Epi::kI32, WN>),
+      reinterpret_cast<const void*>(&split_reduce_kernel<true, Epi::kDequantBf16, WN>),
+  };
+  for (const void* f : fns) {
+    hipFuncAttributes a;
+    if (hipFuncGetAttributes(&a, f) != hipSuccess) { return false; }
+  }
+  return true;
+}
+
 bool
 kernels_loadable()
 {
   const void* fns[] = {
-      reinterpret_cast<const void*>(&mot_gemm_kernel<MmaBf16, Epi::kBf16>),
-      reinterpret_cast<const void*>(&mot_gemm_kernel<MmaBf16, Epi::kSwiglu>),
-      reinterpret_cast<const void*>(&mot_gemm_kernel<MmaI8, Epi::kI32>),
-      reinterpret_cast<const void*>(&mot_gemm_kernel<MmaI8, Epi::kDequantBf16>),
-      reinterpret_cast<const void*>(&split_reduce_kernel<false, Epi::kBf16>),
-      reinterpret_cast<const void*>(&split_reduce_kernel<false, Epi::kSwiglu>),
-      reinterpret_cast<const void*>(&split_reduce_kernel<true, Epi::kI32>),
-      reinterpret_cast<const void*>(&split_reduce_kernel<true, Epi::kDequantBf16>),
       reinterpret_cast<const void*>(&quant_rows_i8_kernel),
       reinterpret_cast<const void*>(&swiglu_kernel),
       reinterpret_cast<const void*>(&gather_rows_kernel<true>),
@@ -754,7 +799,7 @@ kernels_loadable()
     hipFuncAttributes a;
     if (hipFuncGetAttributes(&a, f) != hipSuccess) { return false; }
   }
-  return true;
+  return gemm_kernels_loadable<2>() && gemm_kernels_loadable<4>();
 }
 
 }  // namespace u15h
