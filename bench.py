@@ -53,7 +53,38 @@ def parse():
     ap.add_argument("--fused-swiglu", action="store_true",
                     help="gate|up with the fused SwiGLU epilogue")
     ap.add_argument("--seed", type=int, default=2026)
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a plain 1 GiB device-to-device copy 5 times "
+                         "(calibrates rocprof FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
+
+
+COPY_PROBE_BYTES = 1 << 30
+TRAFFIC_FILE = REPO / "profiles" / "mot_gemm_bf16_c2_traffic.txt"
+
+
+def measured_traffic():
+    """HBM bytes per launch of the bf16 grouped GEMM at config 2, as the
+    committed rocprof FETCH_SIZE / WRITE_SIZE summary records them (scaled
+    by a plain copy of known size), or None if not measured."""
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            if line.startswith("hbm_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
+def copy_probe():
+    import torch
+    src = torch.empty(COPY_PROBE_BYTES // 2, dtype=torch.bfloat16, device="cuda")
+    src.fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes": COPY_PROBE_BYTES, "copies": 5}))
 
 
 class Layer:
@@ -145,37 +176,99 @@ def activations(gen, torch, mu, mg):
     return A
 
 
-def timed(torch, runs, steps, warmup, kinds=None):
-    """Runs `steps` steps of `runs`, bracketing every launch with events.
+def _call(r):
+    (r[1] if isinstance(r, tuple) else r)()
 
-    Returns (total_ms, per-kind summed launch ms, launches per kind)."""
+
+def timed_step(torch, runs, steps, warmup):
+    """`steps` steps of `runs` between two events on the launch stream
+    (after `warmup` untimed steps), nothing else inside: ms per step."""
     for _ in range(warmup):
         for r in runs:
-            (r[1] if isinstance(r, tuple) else r)()
+            _call(r)
     torch.cuda.synchronize()
-    n = len(runs)
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps * n + 1)]
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     t0.record()
-    ev[0].record()
-    k = 0
     for _ in range(steps):
         for r in runs:
-            (r[1] if isinstance(r, tuple) else r)()
-            k += 1
-            ev[k].record()
+            _call(r)
     t1.record()
     torch.cuda.synchronize()
-    total = t0.elapsed_time(t1)
-    per_kind, count = {}, {}
-    for i in range(steps * n):
-        r = runs[i % n]
-        kind = r[0] if isinstance(r, tuple) else "gemm"
-        per_kind[kind] = per_kind.get(kind, 0.0) + ev[i].elapsed_time(ev[i + 1])
-        count[kind] = count.get(kind, 0) + 1
-    return total, per_kind, count
+    return t0.elapsed_time(t1) / steps
+
+
+class HipEvents:
+    """Raw HIP events (hipEventCreate / Record / ElapsedTime) from the HIP
+    runtime the process already uses -- the library records one of them
+    itself, after the GEMM kernel, which torch's event objects do not
+    allow."""
+
+    def __init__(self):
+        import ctypes
+        self.ct = ctypes
+        self.hip = ctypes.CDLL("libamdhip64.so.7")
+        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float),
+                                                 ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.pool = []
+
+    def create(self):
+        ev = self.ct.c_void_p()
+        if self.hip.hipEventCreate(self.ct.byref(ev)) != 0:
+            raise RuntimeError("hipEventCreate failed")
+        self.pool.append(ev)
+        return ev
+
+    def record(self, ev, stream):
+        if self.hip.hipEventRecord(ev, self.ct.c_void_p(stream.cuda_stream)) != 0:
+            raise RuntimeError("hipEventRecord failed")
+
+    def elapsed(self, a, b):
+        ms = self.ct.c_float()
+        if self.hip.hipEventElapsedTime(self.ct.byref(ms), a, b) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value
+
+    def close(self):
+        for ev in self.pool:
+            self.hip.hipEventDestroy(ev)
+        self.pool = []
+
+
+def timed_kernels(torch, ops, runs, steps):
+    """Per-launch kernel times over `steps` more steps, with HIP events on
+    the launch stream: one before each launch, one the library records
+    right after the GEMM kernel (before any split-K reduction), one after
+    the launch.  Returns {kind: [summed ms of the main kernel, launches]}
+    and the summed ms of the split-K reduction kernels."""
+    hev = HipEvents()
+    stream = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    recs = []
+    for _ in range(steps):
+        for r in runs:
+            kind = r[0] if isinstance(r, tuple) else "gemm"
+            e0, e1, e2 = hev.create(), hev.create(), hev.create()
+            hev.record(e0, stream)
+            if kind == "gemm":
+                ops.profile_next_gemm(e1)
+            _call(r)
+            if kind != "gemm":
+                hev.record(e1, stream)
+            hev.record(e2, stream)
+            recs.append((kind, e0, e1, e2))
+    torch.cuda.synchronize()
+    per, red = {}, 0.0
+    for kind, e0, e1, e2 in recs:
+        acc = per.setdefault(kind, [0.0, 0])
+        acc[0] += hev.elapsed(e0, e1)
+        acc[1] += 1
+        red += hev.elapsed(e1, e2)
+    hev.close()
+    return per, red
 
 
 def cpu_baseline(target_s):
@@ -228,6 +321,9 @@ def cpu_baseline(target_s):
 
 def main():
     args = parse()
+    if args.copy_probe:
+        copy_probe()
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for "
               f"--gpus {args.gpus}); the projections shard by rows with no "
@@ -248,10 +344,10 @@ def main():
     flop = FLOP_PER_ROW * M
 
     runs = bf16_launches(ops, L, A, args.fused_swiglu)
-    total, per, cnt = timed(torch, runs, args.steps, args.warmup)
-    ms = total / args.steps
+    ms = timed_step(torch, runs, args.steps, args.warmup)
     tflops = flop / (ms * 1e-3) / 1e12
-    kern_ms = per["gemm"] / cnt["gemm"]
+    per, red_ms = timed_kernels(torch, ops, runs, args.steps)
+    kern_ms = per["gemm"][0] / per["gemm"][1]
     kern_flop = flop / len(runs)
     kern_tflops = kern_flop / (kern_ms * 1e-3) / 1e12
     # HBM bytes the kernel must move per launch (averaged over the step):
@@ -277,20 +373,22 @@ def main():
         "pct_of_peak": round(100 * tflops / PEAK_BF16, 2),
         "roofline": {"bound": "mfma", "achieved": round(kern_tflops, 2),
                      "peak": PEAK_BF16, "unit": "TFLOP/s",
-                     "frac": round(kern_tflops / PEAK_BF16, 4), "traffic": None,
-                     "kernel": "mot_gemm_kernel<MmaBf16, kBf16>",
+                     "frac": round(kern_tflops / PEAK_BF16, 4),
+                     "traffic": measured_traffic(),
+                     "kernel": "mot_gemm_kernel<MmaBf16, kBf16, 4>",
                      "avg_launch_ms": round(kern_ms, 5),
                      "flop_per_launch": kern_flop,
-                     "alg_bytes_per_launch": int(traffic_alg)},
+                     "alg_bytes_per_launch": int(traffic_alg),
+                     "split_reduce_ms_per_step": round(red_ms / args.steps, 5)},
     }
     if want_i8:
         runs8 = i8_launches(ops, L, A)
-        total8, per8, cnt8 = timed(torch, runs8, args.steps, args.warmup)
-        ms8 = total8 / args.steps
+        ms8 = timed_step(torch, runs8, args.steps, args.warmup)
         tops = flop / (ms8 * 1e-3) / 1e12
-        g_ms = per8["gemm"] / cnt8["gemm"]
+        per8, red8 = timed_kernels(torch, ops, runs8, args.steps)
+        g_ms = per8["gemm"][0] / per8["gemm"][1]
         g_tops = (flop / 4) / (g_ms * 1e-3) / 1e12
-        q_ms = per8["quant"] / cnt8["quant"]
+        q_ms = per8["quant"][0] / per8["quant"][1]
         q_bytes = 3 * M * (HIDDEN + NQ + HIDDEN + INTER) / 4 + 4 * M
         result["int8"] = {
             "value": round(tops, 2), "unit": "TOPS",
@@ -299,8 +397,9 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(g_tops, 2),
                          "peak": PEAK_I8, "unit": "TOPS",
                          "frac": round(g_tops / PEAK_I8, 4),
-                         "kernel": "mot_gemm_kernel<MmaI8, kDequantBf16>",
-                         "avg_launch_ms": round(g_ms, 5)},
+                         "kernel": "mot_gemm_kernel<MmaI8, kDequantBf16, 4>",
+                         "avg_launch_ms": round(g_ms, 5),
+                         "split_reduce_ms_per_step": round(red8 / args.steps, 5)},
             "quant_kernel": {"bound": "hbm", "avg_launch_ms": round(q_ms, 5),
                              "achieved_GBps": round(q_bytes / (q_ms * 1e-3) / 1e9, 1),
                              "peak": PEAK_HBM},

@@ -208,6 +208,18 @@ u15h_status u15h_mot_gemm_i8(u15h_ctx* ctx, u15h_stream stream,
                              int nproj);
 
 /* ------------------------------------------------------------------ */
+/* profiling                                                           */
+/* ------------------------------------------------------------------ */
+
+/* Profiling hook; no counterpart in the reference (whose perf test times
+ * whole command buffers, tests/u15-perf-test.cc:63-110).  `event` is a
+ * hipEvent_t: the next GEMM launched through this context records it on
+ * that call's stream right after the GEMM kernel and before any split-K
+ * reduction kernel, then forgets it -- so a caller brackets the GEMM
+ * kernel alone between its own event and this one.  NULL cancels. */
+u15h_status u15h_profile_next_gemm(u15h_ctx* ctx, void* event);
+
+/* ------------------------------------------------------------------ */
 /* per-token routing                                                   */
 /* ------------------------------------------------------------------ */
 

@@ -22,6 +22,8 @@ struct u15h_ctx {
   int num_cu = 256;
   bool split_on = true;      // env U15H_SPLIT=0 turns the split-K tail off
   int waves = 8;             // GEMM workgroup: 8 or 4 waves (env U15H_WAVES)
+  // One-shot profiling event: recorded after the next GEMM kernel.
+  hipEvent_t profile_event = nullptr;
   // Partial-sum workspace of split tiles: at most num_cu K shares of one
   // 256x256 tile each (allocated on first use, kept until destroy).
   void* split_ws = nullptr;
@@ -72,6 +74,15 @@ bind_device(u15h_ctx* ctx)
     return fail(ctx, U15H_ENODEV, "hipSetDevice(%d) failed", ctx->device);
   }
   return U15H_OK;
+}
+
+// The profiling event of the next GEMM launch (one-shot).
+hipEvent_t
+take_profile_event(u15h_ctx* ctx)
+{
+  hipEvent_t e = ctx->profile_event;
+  ctx->profile_event = nullptr;
+  return e;
 }
 
 u15h_status
@@ -262,7 +273,7 @@ linear_i8_route(u15h_ctx* ctx, hipStream_t s, const u15h_bf16* x,
               u15h::tile_cols(Epi::kDequantBf16));
   u15h_status st = plan_split(ctx, b);
   if (st != U15H_OK) { return st; }
-  return launched(ctx, u15h::launch_gemm_i8(b, Epi::kDequantBf16, ctx->waves, s),
+  return launched(ctx, u15h::launch_gemm_i8(b, Epi::kDequantBf16, ctx->waves, s, take_profile_event(ctx)),
                   "gemm_i8");
 }
 
@@ -374,7 +385,7 @@ u15h_linear(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
   add_problem(b, x, w, nullptr, y, bias, nullptr, nullptr, M, N, N,
               u15h::tile_cols(Epi::kBf16));
   if ((st = plan_split(ctx, b)) != U15H_OK) { return st; }
-  return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kBf16, ctx->waves, s), "gemm_bf16");
+  return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kBf16, ctx->waves, s, take_profile_event(ctx)), "gemm_bf16");
 }
 
 u15h_status
@@ -428,7 +439,7 @@ u15h_mot_linear(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
   }
   if ((st = check_tiles(ctx, b)) != U15H_OK) { return st; }
   if ((st = plan_split(ctx, b)) != U15H_OK) { return st; }
-  return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kBf16, ctx->waves, as_stream(stream)),
+  return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kBf16, ctx->waves, as_stream(stream), take_profile_event(ctx)),
                   "mot_gemm_bf16");
 }
 
@@ -487,7 +498,7 @@ u15h_mot_gate_up_swiglu(u15h_ctx* ctx, u15h_stream stream,
               tc);
   if ((st = check_tiles(ctx, b)) != U15H_OK) { return st; }
   if ((st = plan_split(ctx, b)) != U15H_OK) { return st; }
-  return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kSwiglu, ctx->waves, as_stream(stream)),
+  return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kSwiglu, ctx->waves, as_stream(stream), take_profile_event(ctx)),
                   "mot_gate_up_swiglu");
 }
 
@@ -514,6 +525,14 @@ u15h_release_i8_scratch(u15h_ctx* ctx)
   (void)hipFree(ctx->i8_scratch);
   ctx->i8_scratch = nullptr;
   ctx->i8_scratch_bytes = 0;
+}
+
+u15h_status
+u15h_profile_next_gemm(u15h_ctx* ctx, void* event)
+{
+  if (ctx == nullptr) { return U15H_EINVAL; }
+  ctx->profile_event = static_cast<hipEvent_t>(event);
+  return U15H_OK;
 }
 
 int
@@ -599,7 +618,7 @@ mot_gemm_i8_common(u15h_ctx* ctx, u15h_stream stream, const int8_t* xq,
   }
   if ((st = check_tiles(ctx, b)) != U15H_OK) { return st; }
   if ((st = plan_split(ctx, b)) != U15H_OK) { return st; }
-  return launched(ctx, u15h::launch_gemm_i8(b, epi, ctx->waves, as_stream(stream)),
+  return launched(ctx, u15h::launch_gemm_i8(b, epi, ctx->waves, as_stream(stream), take_profile_event(ctx)),
                   deq ? "mot_gemm_i8" : "mot_gemm_i8_i32");
 }
 

@@ -71,10 +71,12 @@ inline size_t split_ws_bytes(const GemmBatch& b)
 // Kernel launchers (u15h_kernels.hip).  All are asynchronous on `s`.
 // `waves` selects the GEMM kernel's workgroup shape: 4 (one wave per SIMD,
 // 128x128 per wave) or 8 (two per SIMD, 128x64 per wave).
+// `after_gemm`, when not null, is recorded on `s` right after the GEMM
+// kernel and before any split-K reduction kernel.
 hipError_t launch_gemm_bf16(const GemmBatch& b, Epi epi, int waves,
-                            hipStream_t s);
+                            hipStream_t s, hipEvent_t after_gemm);
 hipError_t launch_gemm_i8(const GemmBatch& b, Epi epi, int waves,
-                          hipStream_t s);
+                          hipStream_t s, hipEvent_t after_gemm);
 hipError_t launch_quant_rows_i8(const uint16_t* x, int rows, int K,
                                 int8_t* q, float* sc, hipStream_t s);
 hipError_t launch_swiglu(const uint16_t* g, const uint16_t* u, uint16_t* o,

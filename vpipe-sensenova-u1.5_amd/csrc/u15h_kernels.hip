@@ -589,7 +589,41 @@ split_reduce_kernel(const GemmBatch B)
 // ---- per-row symmetric int8 quantisation ------------------------------
 // One workgroup per row: absmax over the row (bf16 widened exactly), then
 // q = clamp(round_half_away(x / s), -127, 127) with s = absmax / 127
-// (fp32 division, correctly rounded).
+// (fp32 division, correctly rounded).  The row is read once: each thread
+// keeps its CPT 16-byte chunks in registers across the block reduction
+// (CPT * 8 * 256 >= K); rows longer than that take a second read.
+__device__ __forceinline__ uint2
+quant8(const uint4 v, float s)
+{
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  uint32_t packed[2] = {0u, 0u};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t h = (e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffffu);
+    int cq = 0;
+    if (s != 0.0f) {
+      const float t = bf16_to_f32(h) / s;
+      cq = (int)roundf(t);
+      cq = max(-127, min(127, cq));
+    }
+    packed[e >> 2] |= ((uint32_t)(cq & 0xff)) << ((e & 3) * 8);
+  }
+  return make_uint2(packed[0], packed[1]);
+}
+
+__device__ __forceinline__ float
+absmax8(const uint4 v, float amax)
+{
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    amax = fmaxf(amax, fabsf(bf16_to_f32(w[e] & 0xffffu)));
+    amax = fmaxf(amax, fabsf(bf16_to_f32(w[e] >> 16)));
+  }
+  return amax;
+}
+
+template <int CPT>
 __global__ __launch_bounds__(256) void
 quant_rows_i8_kernel(const uint16_t* __restrict__ x, int K,
                      int8_t* __restrict__ q, float* __restrict__ sc)
@@ -598,15 +632,16 @@ quant_rows_i8_kernel(const uint16_t* __restrict__ x, int K,
   const int r = blockIdx.x;
   const uint4* xr = reinterpret_cast<const uint4*>(x + (size_t)r * K);
   const int nchunk = K / 8;
+  uint4 v[CPT];
   float amax = 0.0f;
-  for (int c = threadIdx.x; c < nchunk; c += 256) {
-    const uint4 v = xr[c];
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      amax = fmaxf(amax, fabsf(bf16_to_f32(w[e] & 0xffffu)));
-      amax = fmaxf(amax, fabsf(bf16_to_f32(w[e] >> 16)));
-    }
+  for (int i = 0; i < CPT; ++i) {
+    const int c = threadIdx.x + i * 256;
+    v[i] = c < nchunk ? xr[c] : make_uint4(0u, 0u, 0u, 0u);
+    amax = absmax8(v[i], amax);
+  }
+  for (int c = threadIdx.x + CPT * 256; c < nchunk; c += 256) {
+    amax = absmax8(xr[c], amax);
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) { amax = fmaxf(amax, __shfl_xor(amax, o)); }
@@ -616,22 +651,13 @@ quant_rows_i8_kernel(const uint16_t* __restrict__ x, int K,
   const float s = amax / 127.0f;
   if (threadIdx.x == 0) { sc[r] = s; }
   uint2* qr = reinterpret_cast<uint2*>(q + (size_t)r * K);
-  for (int c = threadIdx.x; c < nchunk; c += 256) {
-    const uint4 v = xr[c];
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-    uint32_t packed[2] = {0u, 0u};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t h = (e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffffu);
-      int cq = 0;
-      if (s != 0.0f) {
-        const float t = bf16_to_f32(h) / s;
-        cq = (int)roundf(t);
-        cq = max(-127, min(127, cq));
-      }
-      packed[e >> 2] |= ((uint32_t)(cq & 0xff)) << ((e & 3) * 8);
-    }
-    qr[c] = make_uint2(packed[0], packed[1]);
+  for (int i = 0; i < CPT; ++i) {
+    const int c = threadIdx.x + i * 256;
+    if (c < nchunk) { qr[c] = quant8(v[i], s); }
+  }
+  for (int c = threadIdx.x + CPT * 256; c < nchunk; c += 256) {
+    qr[c] = quant8(xr[c], s);
   }
 }
 
@@ -680,12 +706,15 @@ gather_rows_kernel(const uint16_t* __restrict__ src,
 
 template <class Mma, Epi E, int WN>
 hipError_t
-launch_gemm(const GemmBatch& b, hipStream_t s)
+launch_gemm(const GemmBatch& b, hipStream_t s, hipEvent_t after_gemm)
 {
   if (b.total_tiles <= 0) { return hipSuccess; }
   hipLaunchKernelGGL((mot_gemm_kernel<Mma, E, WN>), dim3(grid_blocks(b)),
                      dim3(128 * WN), 0, s, b);
   hipError_t e = hipGetLastError();
+  if (e == hipSuccess && after_gemm != nullptr) {
+    e = hipEventRecord(after_gemm, s);
+  }
   if (e != hipSuccess || b.split_begin >= b.total_tiles) { return e; }
   constexpr bool kInt = std::is_same<Mma, MmaI8>::value;
   hipLaunchKernelGGL((split_reduce_kernel<kInt, E, WN>),
@@ -696,31 +725,37 @@ launch_gemm(const GemmBatch& b, hipStream_t s)
 
 template <class Mma, Epi E>
 hipError_t
-launch_gemm_waves(const GemmBatch& b, int waves, hipStream_t s)
+launch_gemm_waves(const GemmBatch& b, int waves, hipStream_t s, hipEvent_t ev)
 {
-  return waves == 4 ? launch_gemm<Mma, E, 2>(b, s) : launch_gemm<Mma, E, 4>(b, s);
+  return waves == 4 ? launch_gemm<Mma, E, 2>(b, s, ev)
+                    : launch_gemm<Mma, E, 4>(b, s, ev);
 }
 
 }  // namespace
 
 hipError_t
-launch_gemm_bf16(const GemmBatch& b, Epi epi, int waves, hipStream_t s)
+launch_gemm_bf16(const GemmBatch& b, Epi epi, int waves, hipStream_t s,
+                 hipEvent_t after_gemm)
 {
   switch (epi) {
-    case Epi::kBf16: return launch_gemm_waves<MmaBf16, Epi::kBf16>(b, waves, s);
+    case Epi::kBf16:
+      return launch_gemm_waves<MmaBf16, Epi::kBf16>(b, waves, s, after_gemm);
     case Epi::kSwiglu:
-      return launch_gemm_waves<MmaBf16, Epi::kSwiglu>(b, waves, s);
+      return launch_gemm_waves<MmaBf16, Epi::kSwiglu>(b, waves, s, after_gemm);
     default: return hipErrorInvalidValue;
   }
 }
 
 hipError_t
-launch_gemm_i8(const GemmBatch& b, Epi epi, int waves, hipStream_t s)
+launch_gemm_i8(const GemmBatch& b, Epi epi, int waves, hipStream_t s,
+               hipEvent_t after_gemm)
 {
   switch (epi) {
-    case Epi::kI32: return launch_gemm_waves<MmaI8, Epi::kI32>(b, waves, s);
+    case Epi::kI32:
+      return launch_gemm_waves<MmaI8, Epi::kI32>(b, waves, s, after_gemm);
     case Epi::kDequantBf16:
-      return launch_gemm_waves<MmaI8, Epi::kDequantBf16>(b, waves, s);
+      return launch_gemm_waves<MmaI8, Epi::kDequantBf16>(b, waves, s,
+                                                        after_gemm);
     default: return hipErrorInvalidValue;
   }
 }
@@ -730,8 +765,15 @@ launch_quant_rows_i8(const uint16_t* x, int rows, int K, int8_t* q,
                      float* sc, hipStream_t s)
 {
   if (rows <= 0) { return hipSuccess; }
-  hipLaunchKernelGGL(quant_rows_i8_kernel, dim3(rows), dim3(256), 0, s, x, K,
-                     q, sc);
+  // Chunks per thread held in registers: enough for K = 4096 (2) or
+  // K = 12288 (6); longer rows stream the rest twice.
+  if (K <= 2 * 8 * 256) {
+    hipLaunchKernelGGL(quant_rows_i8_kernel<2>, dim3(rows), dim3(256), 0, s, x,
+                       K, q, sc);
+  } else {
+    hipLaunchKernelGGL(quant_rows_i8_kernel<6>, dim3(rows), dim3(256), 0, s, x,
+                       K, q, sc);
+  }
   return hipGetLastError();
 }
 
@@ -790,7 +832,8 @@ bool
 kernels_loadable()
 {
   const void* fns[] = {
-      reinterpret_cast<const void*>(&quant_rows_i8_kernel),
+      reinterpret_cast<const void*>(&quant_rows_i8_kernel<2>),
+      reinterpret_cast<const void*>(&quant_rows_i8_kernel<6>),
       reinterpret_cast<const void*>(&swiglu_kernel),
       reinterpret_cast<const void*>(&gather_rows_kernel<true>),
       reinterpret_cast<const void*>(&gather_rows_kernel<false>),

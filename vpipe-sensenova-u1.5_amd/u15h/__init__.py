@@ -83,6 +83,7 @@ def load_library() -> ctypes.CDLL:
         "u15h_enable_i8_gemm": (i, [vp, i]),
         "u15h_release_i8_scratch": (None, [vp]),
         "u15h_i8_min_m": (i, [vp]),
+        "u15h_profile_next_gemm": (i, [vp, vp]),
         "u15h_quant_rows_i8": (i, [vp, vp, vp, i, i, vp, vp]),
         "u15h_mot_gemm_i8_i32": (i, [vp, vp, vp, i, i, i,
                                      ctypes.POINTER(_MotProjI8), i]),
@@ -297,6 +298,15 @@ class Ops:
                                         _ptr(sx), M_und, M_gen, K, arr,
                                         len(projs))
         self._check(st, "u15h_mot_gemm_i8")
+
+    # ---- profiling -------------------------------------------------------
+    def profile_next_gemm(self, event):
+        """Record the raw hipEvent_t `event` (a ctypes.c_void_p or int
+        handle) right after the next GEMM kernel, before any split-K
+        reduction kernel."""
+        h = event if isinstance(event, ctypes.c_void_p) else ctypes.c_void_p(event)
+        self._check(self._lib.u15h_profile_next_gemm(self._ctx, h),
+                    "u15h_profile_next_gemm")
 
     # ---- routing -------------------------------------------------------
     def gather_rows(self, src, perm, dst, stream=None):
