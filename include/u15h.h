@@ -116,6 +116,45 @@ u15h_status u15h_mot_linear(u15h_ctx* ctx, u15h_stream stream,
                             const u15h_bf16* x, int M_und, int M_gen, int K,
                             const u15h_mot_proj* proj, int nproj);
 
+/* Affine-quantized weight pack: the reference's QWeight
+ * (src/u15-metal-ops.h:39-57; shape rules src/u15-weights.cc:248-325).
+ *   codes  uint32 [N][K*bits/32], code k of a row at bits
+ *          [bits*(k % (32/bits)), +bits) of word k / (32/bits)
+ *   scales bf16 [N][K/group],  biases bf16 [N][K/group]
+ *   w[n][k] = scale * code + bias   (f32 multiply then add, then bf16 RNE)
+ * bits 4 or 8, group 32 or 64. */
+typedef struct {
+  const uint32_t*  codes;
+  const u15h_bf16* scales;
+  const u15h_bf16* biases;
+  int              bits;
+  int              group;
+} u15h_qweight;
+
+/* Expands a pack to a dense bf16 weight w_out[N][K]: the dequant-once step
+ * of MetalOps::linear_mma_q_ (src/u15-metal-ops.cc:359-400). */
+u15h_status u15h_dequant_affine(u15h_ctx* ctx, u15h_stream stream,
+                                const u15h_qweight* w, int N, int K,
+                                u15h_bf16* w_out);
+
+/* Replaces MetalOps::linear(enc, x, QWeight, bias, y, M, K, N) for a
+ * quantized pack (src/u15-metal-ops.cc:402-433): dequant once into the
+ * context's grow-only scratch, then the dense path (u15h_linear). */
+u15h_status u15h_linear_q(u15h_ctx* ctx, u15h_stream stream,
+                          const u15h_bf16* x, const u15h_qweight* w,
+                          const u15h_bf16* bias, u15h_bf16* y,
+                          int M, int K, int N);
+
+/* Replaces MetalOps::bias_add(enc, y, bias, M, N) (src/u15-metal-ops.cc:
+ * 435-446): y[m][n] = bf16(y[m][n] + bias[n]), f32 add.  N % 8 == 0. */
+u15h_status u15h_bias_add(u15h_ctx* ctx, u15h_stream stream, u15h_bf16* y,
+                          const u15h_bf16* bias, int M, int N);
+
+/* f32 -> bf16 round-to-nearest-even on the device: the weight loader's
+ * conversion (src/u15-weights.cc:51-64).  n % 4 == 0. */
+u15h_status u15h_f32_to_bf16(u15h_ctx* ctx, u15h_stream stream,
+                             const float* src, int64_t n, u15h_bf16* dst);
+
 /* ------------------------------------------------------------------ */
 /* SwiGLU                                                              */
 /* ------------------------------------------------------------------ */
@@ -127,8 +166,17 @@ u15h_status u15h_swiglu(u15h_ctx* ctx, u15h_stream stream,
                         const u15h_bf16* gate, const u15h_bf16* up,
                         u15h_bf16* out, int64_t n);
 
-/* Replaces MetalOps::swiglu_fused (src/u15-metal-ops.h:121-135,
- * src/u15-metal-ops.cc:470-491) in grouped form: one launch computes, for
+/* Replaces MetalOps::swiglu_fused(enc, x, w_fused, y, M, K, inter)
+ * (src/u15-metal-ops.h:121-135, src/u15-metal-ops.cc:470-491) with the
+ * reference's weight layout: w_fused[2*inter][K] ROW-INTERLEAVED, row 2i =
+ * gate row i, row 2i+1 = up row i.  y[M][inter] = silu(x.gate^T) *
+ * (x.up^T), gate and up rounded to bf16 before the product.
+ * Limits: K % 8 == 0, inter % 8 == 0. */
+u15h_status u15h_swiglu_fused(u15h_ctx* ctx, u15h_stream stream,
+                              const u15h_bf16* x, const u15h_bf16* w_fused,
+                              u15h_bf16* y, int M, int K, int inter);
+
+/* The same product in grouped form: one launch computes, for
  * each row group, h[M][I] = silu(x.Wg^T) * (x.Wu^T) with the gate and up
  * weights given SEPARATELY (no interleaved repack needed: each output tile
  * reads the matching gate and up rows).  Rounding follows the unfused

@@ -58,6 +58,9 @@ def lib() -> ctypes.CDLL:
             "u15o_dequant_bf16": [vp, vp, vp, sz, sz, vp],
             "u15o_dequant_f64": [vp, vp, vp, sz, sz, vp],
             "u15o_randn_mt": [ctypes.c_uint32, ctypes.c_float, sz, vp],
+            "u15o_dequant_affine": [vp, vp, vp, ctypes.c_int, ctypes.c_int, sz, sz, vp],
+            "u15o_pack_affine": [vp, ctypes.c_int, ctypes.c_int, sz, sz, vp, vp, vp, vp],
+            "u15o_bias_add_bf16": [vp, vp, sz, sz],
         }.items():
             getattr(L, n).restype = None
             getattr(L, n).argtypes = a
@@ -219,6 +222,38 @@ def dequant_f64(acc, sa, sw) -> np.ndarray:
     rows, N = acc.shape
     y = np.empty((rows, N), np.float64)
     lib().u15o_dequant_f64(pa, ps, pw, rows, N, y.ctypes.data)
+    return y
+
+
+# ---- affine-quantized packs --------------------------------------------------
+def pack_affine(w, bits, group):
+    """(codes u32 [N][K*bits/32], scales bf16, biases bf16, deq f32)."""
+    w, pw = _c(w, np.float32)
+    N, K = w.shape
+    codes = np.empty((N, K * bits // 32), np.uint32)
+    scales = np.empty((N, K // group), np.uint16)
+    biases = np.empty((N, K // group), np.uint16)
+    deq = np.empty((N, K), np.float32)
+    lib().u15o_pack_affine(pw, bits, group, N, K, codes.ctypes.data,
+                           scales.ctypes.data, biases.ctypes.data,
+                           deq.ctypes.data)
+    return codes, scales, biases, deq
+
+
+def dequant_affine(codes, scales, biases, bits, group, K):
+    codes, pc = _c(codes, np.uint32)
+    scales, ps = _c(scales, np.uint16)
+    biases, pb = _c(biases, np.uint16)
+    N = codes.shape[0]
+    out = np.empty((N, K), np.uint16)
+    lib().u15o_dequant_affine(pc, ps, pb, bits, group, N, K, out.ctypes.data)
+    return out
+
+
+def bias_add_bf16(y_bits, b_bits):
+    y = np.array(y_bits, dtype=np.uint16, copy=True)
+    b, pb = _c(b_bits, np.uint16)
+    lib().u15o_bias_add_bf16(y.ctypes.data, pb, y.shape[0], y.shape[1])
     return y
 
 

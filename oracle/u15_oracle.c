@@ -241,6 +241,76 @@ u15o_dequant_f64(const int32_t* acc, const float* sa, const float* sw,
   }
 }
 
+void
+u15o_dequant_affine(const uint32_t* codes, const uint16_t* scales,
+                     const uint16_t* biases, int bits, int group, size_t N,
+                     size_t K, uint16_t* w_out)
+{
+  const size_t per_word = 32u / (size_t)bits;
+  const uint32_t mask = (1u << bits) - 1u;
+  const size_t words = K / per_word;
+  const size_t groups = K / (size_t)group;
+  for (size_t n = 0; n < N; ++n) {
+    for (size_t k = 0; k < K; ++k) {
+      const uint32_t word = codes[n * words + k / per_word];
+      const uint32_t code = (word >> ((k % per_word) * (size_t)bits)) & mask;
+      const float sc = u15o_bf16_to_f32(scales[n * groups + k / group]);
+      const float bi = u15o_bf16_to_f32(biases[n * groups + k / group]);
+      volatile float prod = sc * (float)code;   /* no fused multiply-add */
+      w_out[n * K + k] = u15o_f32_to_bf16(prod + bi);
+    }
+  }
+}
+
+void
+u15o_pack_affine(const float* w, int bits, int group, size_t N, size_t K,
+                 uint32_t* codes, uint16_t* scales, uint16_t* biases,
+                 float* deq)
+{
+  /* tests/u15-m5-test.cc:263-310, with 255 generalised to 2^bits - 1 */
+  const long qmax = (1L << bits) - 1;
+  const size_t per_word = 32u / (size_t)bits;
+  const size_t words = K / per_word;
+  const size_t groups = K / (size_t)group;
+  for (size_t n = 0; n < N; ++n) {
+    for (size_t w_i = 0; w_i < words; ++w_i) { codes[n * words + w_i] = 0u; }
+    for (size_t g = 0; g < groups; ++g) {
+      const size_t k0 = g * (size_t)group;
+      float lo = w[n * K + k0], hi = lo;
+      for (int i = 1; i < group; ++i) {
+        const float v = w[n * K + k0 + (size_t)i];
+        if (v < lo) { lo = v; }
+        if (v > hi) { hi = v; }
+      }
+      const float sf = u15o_bf16_to_f32(u15o_f32_to_bf16((hi - lo) / (float)qmax));
+      const float bf = u15o_bf16_to_f32(u15o_f32_to_bf16(lo));
+      scales[n * groups + g] = u15o_f32_to_bf16(sf);
+      biases[n * groups + g] = u15o_f32_to_bf16(bf);
+      for (int i = 0; i < group; ++i) {
+        const size_t k = k0 + (size_t)i;
+        const float v = w[n * K + k];
+        long c = sf > 0.0f ? lroundf((v - bf) / sf) : 0;
+        if (c < 0) { c = 0; }
+        if (c > qmax) { c = qmax; }
+        codes[n * words + k / per_word] |=
+            (uint32_t)c << ((k % per_word) * (size_t)bits);
+        if (deq != NULL) { deq[n * K + k] = sf * (float)c + bf; }
+      }
+    }
+  }
+}
+
+void
+u15o_bias_add_bf16(uint16_t* y, const uint16_t* b, size_t rows, size_t N)
+{
+  for (size_t r = 0; r < rows; ++r) {
+    for (size_t n = 0; n < N; ++n) {
+      const float v = u15o_bf16_to_f32(y[r * N + n]) + u15o_bf16_to_f32(b[n]);
+      y[r * N + n] = u15o_f32_to_bf16(v);
+    }
+  }
+}
+
 double
 u15o_rel_l2(const float* a, const float* b, size_t n)
 {

@@ -85,6 +85,31 @@ void u15o_dequant_bf16(const int32_t* acc, const float* sa, const float* sw,
 void u15o_dequant_f64(const int32_t* acc, const float* sa, const float* sw,
                       size_t rows, size_t N, double* y);
 
+/* Affine-quantized weight packs (the reference's QWeight, u15-metal-ops.h:
+ * 39-57; shape rules u15-weights.cc:248-325): codes u32 [N][K*bits/32],
+ * scales and biases bf16 [N][K/group]; element k of row n is
+ *   w = scale[n][k/group] * code + bias[n][k/group]
+ * in f32 (a multiply, then an add), code k sitting at bits
+ * [bits*(k % (32/bits)), +bits) of word k / (32/bits) -- the w8 order of the
+ * reference's own pack fixture (tests/u15-m5-test.cc:300-306), w4 by the
+ * same low-bits-first rule.  dequant writes bf16 (RNE), the expansion the
+ * reference's dequant-once route feeds to the dense GEMM
+ * (u15-metal-ops.cc:359-400). */
+void u15o_dequant_affine(const uint32_t* codes, const uint16_t* scales,
+                         const uint16_t* biases, int bits, int group,
+                         size_t N, size_t K, uint16_t* w_out);
+/* Builds a pack from f32 weights the way the reference's fixture does
+ * (tests/u15-m5-test.cc:263-310): per group, scale = bf16((hi-lo)/(2^bits-1)),
+ * bias = bf16(lo), code = clamp(lround((w - bias)/scale), 0, 2^bits-1)
+ * (0 when scale is 0); `deq` (optional) receives scale*code+bias in f32. */
+void u15o_pack_affine(const float* w, int bits, int group, size_t N, size_t K,
+                      uint32_t* codes, uint16_t* scales, uint16_t* biases,
+                      float* deq);
+
+/* y[r][n] = bf16(y[r][n] + b[n]) (f32 add), the reference's bias_add
+ * (u15-metal-ops.cc:435-446). */
+void u15o_bias_add_bf16(uint16_t* y, const uint16_t* b, size_t rows, size_t N);
+
 /* rel-L2 = sqrt(sum (a-b)^2 / sum b^2), tests/u15-kernels-test.cc:95-105;
  * max-rel = max|a-b| / max|b|. */
 double u15o_rel_l2(const float* a, const float* b, size_t n);

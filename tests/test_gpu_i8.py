@@ -218,3 +218,36 @@ def test_i32_split_tail_bit_exact(ops):
     rs, cs = oracle.i8_product_sums(xq[Mu:], wg)
     assert np.array_equal(out[Mu:].astype(np.int64).sum(axis=1), rs)
     assert np.array_equal(out[Mu:].astype(np.int64).sum(axis=0), cs)
+
+
+def test_i32_ring_pipeline_bit_exact():
+    """The four-stage ring pipeline on the int8 path: exact accumulators,
+    split shares included."""
+    import os
+    old = os.environ.get("U15H_RING")
+    os.environ["U15H_RING"] = "1"
+    try:
+        import u15h
+        ops_ring = u15h.Ops(0)
+    finally:
+        if old is None:
+            del os.environ["U15H_RING"]
+        else:
+            os.environ["U15H_RING"] = old
+    rng = np.random.default_rng(26)
+    Mu, Mg, K, N = 37, 263, 12288, 264
+    M = Mu + Mg
+    xq = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    wu = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    wg = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    y = torch.empty(M, N, dtype=torch.int32, device="cuda")
+    ops_ring.mot_gemm_i8_i32(torch.from_numpy(xq).cuda(), Mu, Mg, K,
+                             [_proj(torch.from_numpy(wu).cuda(), None,
+                                    torch.from_numpy(wg).cuda(), None, y)])
+    torch.cuda.synchronize()
+    out = y.cpu().numpy()
+    assert np.array_equal(out[:Mu], oracle.gemm_i8_i32(xq[:Mu], wu))
+    rs, cs = oracle.i8_product_sums(xq[Mu:], wg)
+    assert np.array_equal(out[Mu:].astype(np.int64).sum(axis=1), rs)
+    assert np.array_equal(out[Mu:].astype(np.int64).sum(axis=0), cs)
+    ops_ring.close()

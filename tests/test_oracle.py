@@ -252,3 +252,127 @@ def test_quantised_gemm_tracks_bf16_linear():
     y = oracle.dequant_f64(oracle.gemm_i8_i32(xq, wq), sx, sw)
     ref = oracle.linear_bf16(x, w)
     assert oracle.rel_l2(y.astype(np.float32), ref) < 0.03
+
+
+# ---- affine-quantized packs ------------------------------------------------
+def _np_unpack(codes, bits, K):
+    """Independent unpack: code k at bits [bits*(k%per), +bits) of word k/per."""
+    per = 32 // bits
+    N = codes.shape[0]
+    sh = (np.arange(K) % per) * bits
+    words = codes[:, np.arange(K) // per].astype(np.uint64)
+    return ((words >> sh.astype(np.uint64)) & ((1 << bits) - 1)).astype(np.int64)
+
+
+def _np_dequant_bits(codes, scales, biases, bits, group, K):
+    q = _np_unpack(codes, bits, K).astype(np.float32)
+    s = oracle.bf16_to_f32(scales).repeat(group, axis=1)
+    b = oracle.bf16_to_f32(biases).repeat(group, axis=1)
+    with np.errstate(all="ignore"):
+        w = (s * q).astype(np.float32) + b           # f32 multiply, then add
+    return torch_bf16_bits(w.astype(np.float32))
+
+
+def test_pack_w8g64_round_trips_on_reference_fixture():
+    """tests/u15-m5-test.cc:316-329: K=4096, N=6144, G=64, seed 77, stddev
+    0.05; the pack's meaning is within 1.5e-2 rel-L2 of the weights."""
+    K, N, G = 4096, 6144, 64
+    w = oracle.randn_mt(77, N * K, 0.05).reshape(N, K)
+    codes, sc, bi, deq = oracle.pack_affine(w, 8, G)
+    e = oracle.rel_l2(deq, w)
+    assert e < 1.5e-2
+    # A uniform residual of step/sqrt(12), step = range/255: far below the
+    # bar, so a packing error (wrong group, wrong byte) cannot hide under it.
+    assert e < 8e-3
+
+
+def test_pack_w4g32_round_trips():
+    # 4 bits over 32 normals: step ~ 4.1 sigma / 15, residual ~ step/sqrt(12)
+    # ~ 0.08 sigma.  A byte-order or group mix-up gives O(1).
+    w = oracle.randn_mt(5, 512 * 256, 1.0).reshape(512, 256)
+    codes, sc, bi, deq = oracle.pack_affine(w, 4, 32)
+    e = oracle.rel_l2(deq, w)
+    assert 0.03 < e < 0.12
+
+
+@pytest.mark.parametrize("bits,group", [(8, 64), (8, 32), (4, 64), (4, 32)])
+def test_pack_codes_follow_the_fixture_rule(bits, group):
+    """Recompute every code with numpy from the stored scale/bias
+    (tests/u15-m5-test.cc:280-306 generalised to 2^bits-1 levels) and check
+    the packed words and the f32 meaning."""
+    N, K = 24, 256
+    w = oracle.randn_mt(11 + bits + group, N * K, 0.05).reshape(N, K)
+    w[3, :group] = 0.25                            # a flat group: scale 0
+    codes, sc, bi, deq = oracle.pack_affine(w, bits, group)
+    lv = (1 << bits) - 1
+    sf = oracle.bf16_to_f32(sc).repeat(group, axis=1)
+    bf = oracle.bf16_to_f32(bi).repeat(group, axis=1)
+    lo = w.reshape(N, K // group, group).min(axis=2).repeat(group, axis=1)
+    hi = w.reshape(N, K // group, group).max(axis=2).repeat(group, axis=1)
+    assert np.array_equal(sc.repeat(group, axis=1),
+                          torch_bf16_bits((hi - lo) / np.float32(lv)))
+    assert np.array_equal(bi.repeat(group, axis=1), torch_bf16_bits(lo))
+    with np.errstate(all="ignore"):
+        r = np.where(sf > 0, (w - bf) / np.where(sf > 0, sf, 1), 0)
+    # lround: half away from zero
+    q = np.clip(np.sign(r) * np.floor(np.abs(r).astype(np.float64) + 0.5),
+                0, lv).astype(np.int64)
+    assert np.array_equal(_np_unpack(codes, bits, K), q)
+    assert np.array_equal(deq, (sf * q.astype(np.float32)) + bf)
+    assert np.all(q[3, :group] == 0)
+
+
+@pytest.mark.parametrize("bits,group", [(8, 64), (4, 32), (4, 64), (8, 32)])
+def test_dequant_affine_matches_numpy_unpack(bits, group):
+    N, K = 40, 512
+    rng = np.random.default_rng(bits * 100 + group)
+    codes = rng.integers(0, 2**32, size=(N, K * bits // 32),
+                         dtype=np.uint64).astype(np.uint32)
+    sc = torch_bf16_bits(rng.uniform(-0.02, 0.02, (N, K // group)))
+    bi = torch_bf16_bits(rng.normal(0, 0.5, (N, K // group)))
+    got = oracle.dequant_affine(codes, sc, bi, bits, group, K)
+    assert np.array_equal(got, _np_dequant_bits(codes, sc, bi, bits, group, K))
+
+
+def test_dequant_affine_closed_forms():
+    N, K, G = 2, 64, 32
+    # scale 1, bias 0: w = code exactly (codes <= 255 are bf16-exact).
+    codes = np.array([[0x03020100 + 0x04040404 * i for i in range(16)]] * N,
+                     np.uint32)
+    one = torch_bf16_bits(np.ones((N, K // G)))
+    zero = np.zeros((N, K // G), np.uint16)
+    w = oracle.bf16_to_f32(oracle.dequant_affine(codes, one, zero, 8, G, K))
+    assert np.array_equal(w, np.tile(np.arange(64, dtype=np.float32), (N, 1)))
+    # all codes 0: w = bias; code 15 (w4 max) with scale 2, bias -1 -> 29.
+    b = torch_bf16_bits(np.full((N, K // G), 0.375))
+    w = oracle.bf16_to_f32(oracle.dequant_affine(
+        np.zeros((N, K // 8), np.uint32), one, b, 4, G, K))
+    assert np.all(w == 0.375)
+    w = oracle.bf16_to_f32(oracle.dequant_affine(
+        np.full((N, K // 8), 0xFFFFFFFF, np.uint32),
+        torch_bf16_bits(np.full((N, K // G), 2.0)),
+        torch_bf16_bits(np.full((N, K // G), -1.0)), 4, G, K))
+    assert np.all(w == 29.0)
+
+
+def test_dequant_affine_inverts_pack():
+    """The pack and the dequant are two readers of one convention: the bf16
+    expansion is the RNE of the pack's own f32 meaning."""
+    w = oracle.randn_mt(3, 64 * 512, 0.05).reshape(64, 512)
+    for bits, group in ((8, 64), (4, 32)):
+        codes, sc, bi, deq = oracle.pack_affine(w, bits, group)
+        got = oracle.dequant_affine(codes, sc, bi, bits, group, 512)
+        assert np.array_equal(got, torch_bf16_bits(deq))
+
+
+def test_bias_add_matches_f32_add_then_rne():
+    rng = np.random.default_rng(9)
+    y = torch_bf16_bits(rng.normal(0, 3, (33, 64)))
+    b = torch_bf16_bits(rng.normal(0, 1, 64))
+    got = oracle.bias_add_bf16(y, b)
+    want = torch_bf16_bits(oracle.bf16_to_f32(y) + oracle.bf16_to_f32(b))
+    assert np.array_equal(got, want)
+    # bias 0 is the identity; y = -bias gives +0.
+    assert np.array_equal(oracle.bias_add_bf16(y, np.zeros(64, np.uint16)), y)
+    z = oracle.bias_add_bf16(np.tile(b ^ 0x8000, (2, 1)), b)
+    assert np.all(oracle.bf16_to_f32(z) == 0)

@@ -21,7 +21,9 @@ struct u15h_ctx {
   int device = 0;
   int num_cu = 256;
   bool split_on = true;      // env U15H_SPLIT=0 turns the split-K tail off
-  int waves = 8;             // GEMM workgroup: 8 or 4 waves (env U15H_WAVES)
+  // GEMM kernel build: 8 or 4 waves (env U15H_WAVES), four-stage LDS ring
+  // or two-stage pipeline (env U15H_RING=1/0).
+  u15h::GemmShape gemm = {8, false};
   // One-shot profiling event: recorded after the next GEMM kernel.
   hipEvent_t profile_event = nullptr;
   // Partial-sum workspace of split tiles: at most num_cu K shares of one
@@ -33,6 +35,10 @@ struct u15h_ctx {
   // weight codes + scales.
   void* i8_scratch = nullptr;
   size_t i8_scratch_bytes = 0;
+  // Grow-only bf16 expansion of an affine-quantized weight (the
+  // reference's `_w_deq`, u15-metal-ops.h:461-469).
+  void* w_deq = nullptr;
+  size_t w_deq_bytes = 0;
   std::string err;
 };
 
@@ -100,7 +106,7 @@ launched(u15h_ctx* ctx, hipError_t e, const char* what)
 void
 add_problem(GemmBatch& b, const void* a, const void* w, const void* w2,
             void* y, const uint16_t* bias, const float* sa, const float* sw,
-            int rows, int n, int ldy, int tile_cols)
+            int rows, int n, int ldy, int tile_cols, int wld = 0)
 {
   if (rows <= 0) { return; }
   GemmProblem& p = b.p[b.nprob++];
@@ -113,6 +119,7 @@ add_problem(GemmBatch& b, const void* a, const void* w, const void* w2,
   p.sw = sw;
   p.rows = rows;
   p.n = n;
+  p.wld = wld > 0 ? wld : b.kbytes;
   p.ldy = ldy;
   p.tiles_m = (rows + u15h::kBM - 1) / u15h::kBM;
   p.tiles_n = (n + tile_cols - 1) / tile_cols;
@@ -273,7 +280,7 @@ linear_i8_route(u15h_ctx* ctx, hipStream_t s, const u15h_bf16* x,
               u15h::tile_cols(Epi::kDequantBf16));
   u15h_status st = plan_split(ctx, b);
   if (st != U15H_OK) { return st; }
-  return launched(ctx, u15h::launch_gemm_i8(b, Epi::kDequantBf16, ctx->waves, s, take_profile_event(ctx)),
+  return launched(ctx, u15h::launch_gemm_i8(b, Epi::kDequantBf16, ctx->gemm, s, take_profile_event(ctx)),
                   "gemm_i8");
 }
 
@@ -330,7 +337,8 @@ u15h_create(int device, u15h_ctx** out)
   ctx->device = device;
   ctx->num_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
   ctx->split_on = env_int("U15H_SPLIT", 1) != 0;
-  ctx->waves = env_int("U15H_WAVES", 8) == 4 ? 4 : 8;
+  ctx->gemm.waves = env_int("U15H_WAVES", 8) == 4 ? 4 : 8;
+  ctx->gemm.ring = env_int("U15H_RING", 0) != 0;
   ctx->i8_min_m = std::max(1, env_int("U15H_I8_MIN_M", 1024));
   *out = ctx;
   return U15H_OK;
@@ -341,6 +349,10 @@ u15h_destroy(u15h_ctx* ctx)
 {
   if (ctx == nullptr) { return; }
   u15h_release_i8_scratch(ctx);
+  if (ctx->w_deq != nullptr) {
+    (void)hipDeviceSynchronize();
+    (void)hipFree(ctx->w_deq);
+  }
   if (ctx->split_ws != nullptr) {
     (void)hipDeviceSynchronize();
     (void)hipFree(ctx->split_ws);
@@ -352,6 +364,20 @@ const char*
 u15h_last_error(const u15h_ctx* ctx)
 {
   return ctx != nullptr ? ctx->err.c_str() : "null context";
+}
+
+// The dense bf16 GEMM on checked, bound arguments.
+static u15h_status
+dense_bf16(u15h_ctx* ctx, hipStream_t s, const u15h_bf16* x,
+           const u15h_bf16* w, const u15h_bf16* bias, u15h_bf16* y, int M,
+           int K, int N)
+{
+  GemmBatch b = empty_batch(K * 2);
+  add_problem(b, x, w, nullptr, y, bias, nullptr, nullptr, M, N, N,
+              u15h::tile_cols(Epi::kBf16));
+  u15h_status st = plan_split(ctx, b);
+  if (st != U15H_OK) { return st; }
+  return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kBf16, ctx->gemm, s, take_profile_event(ctx)), "gemm_bf16");
 }
 
 u15h_status
@@ -381,11 +407,7 @@ u15h_linear(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
   if (ctx->i8_on && M >= ctx->i8_min_m && K % 128 == 0) {
     return linear_i8_route(ctx, s, x, w, bias, y, M, K, N);
   }
-  GemmBatch b = empty_batch(K * 2);
-  add_problem(b, x, w, nullptr, y, bias, nullptr, nullptr, M, N, N,
-              u15h::tile_cols(Epi::kBf16));
-  if ((st = plan_split(ctx, b)) != U15H_OK) { return st; }
-  return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kBf16, ctx->waves, s, take_profile_event(ctx)), "gemm_bf16");
+  return dense_bf16(ctx, s, x, w, bias, y, M, K, N);
 }
 
 u15h_status
@@ -439,7 +461,7 @@ u15h_mot_linear(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
   }
   if ((st = check_tiles(ctx, b)) != U15H_OK) { return st; }
   if ((st = plan_split(ctx, b)) != U15H_OK) { return st; }
-  return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kBf16, ctx->waves, as_stream(stream), take_profile_event(ctx)),
+  return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kBf16, ctx->gemm, as_stream(stream), take_profile_event(ctx)),
                   "mot_gemm_bf16");
 }
 
@@ -498,7 +520,7 @@ u15h_mot_gate_up_swiglu(u15h_ctx* ctx, u15h_stream stream,
               tc);
   if ((st = check_tiles(ctx, b)) != U15H_OK) { return st; }
   if ((st = plan_split(ctx, b)) != U15H_OK) { return st; }
-  return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kSwiglu, ctx->waves, as_stream(stream), take_profile_event(ctx)),
+  return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kSwiglu, ctx->gemm, as_stream(stream), take_profile_event(ctx)),
                   "mot_gate_up_swiglu");
 }
 
@@ -618,7 +640,7 @@ mot_gemm_i8_common(u15h_ctx* ctx, u15h_stream stream, const int8_t* xq,
   }
   if ((st = check_tiles(ctx, b)) != U15H_OK) { return st; }
   if ((st = plan_split(ctx, b)) != U15H_OK) { return st; }
-  return launched(ctx, u15h::launch_gemm_i8(b, epi, ctx->waves, as_stream(stream), take_profile_event(ctx)),
+  return launched(ctx, u15h::launch_gemm_i8(b, epi, ctx->gemm, as_stream(stream), take_profile_event(ctx)),
                   deq ? "mot_gemm_i8" : "mot_gemm_i8_i32");
 }
 
@@ -638,6 +660,161 @@ u15h_mot_gemm_i8(u15h_ctx* ctx, u15h_stream stream, const int8_t* xq,
 {
   return mot_gemm_i8_common(ctx, stream, xq, sx, M_und, M_gen, K, proj, nproj,
                             Epi::kDequantBf16);
+}
+
+static u15h_status
+check_qweight(u15h_ctx* ctx, const u15h_qweight* w, int N, int K)
+{
+  if (w == nullptr || w->codes == nullptr || w->scales == nullptr ||
+      w->biases == nullptr) {
+    return fail(ctx, U15H_EINVAL, "null quantized weight pack");
+  }
+  if ((w->bits != 4 && w->bits != 8) || (w->group != 32 && w->group != 64)) {
+    return fail(ctx, U15H_EINVAL, "pack w%dg%d: bits must be 4 or 8, group "
+                "32 or 64", w->bits, w->group);
+  }
+  if (N <= 0 || K <= 0 || K % w->group != 0 || K % 8 != 0) {
+    return fail(ctx, U15H_EINVAL, "N=%d K=%d do not close with group %d", N,
+                K, w->group);
+  }
+  if ((long long)N * K > (1LL << 31)) {
+    return fail(ctx, U15H_EINVAL, "pack too large");
+  }
+  if (!aligned16(w->codes)) {
+    return fail(ctx, U15H_EINVAL, "codes must be 16-byte aligned");
+  }
+  return U15H_OK;
+}
+
+u15h_status
+u15h_dequant_affine(u15h_ctx* ctx, u15h_stream stream, const u15h_qweight* w,
+                    int N, int K, u15h_bf16* w_out)
+{
+  if (ctx == nullptr) { return U15H_EINVAL; }
+  u15h_status st = check_qweight(ctx, w, N, K);
+  if (st != U15H_OK) { return st; }
+  if (w_out == nullptr || !aligned16(w_out)) {
+    return fail(ctx, U15H_EINVAL, "w_out null or misaligned");
+  }
+  if ((st = bind_device(ctx)) != U15H_OK) { return st; }
+  return launched(ctx,
+                  u15h::launch_dequant_affine(w->codes, w->scales, w->biases,
+                                              w->bits, w->group, N, K, w_out,
+                                              as_stream(stream)),
+                  "dequant_affine");
+}
+
+u15h_status
+u15h_linear_q(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
+              const u15h_qweight* w, const u15h_bf16* bias, u15h_bf16* y,
+              int M, int K, int N)
+{
+  if (ctx == nullptr) { return U15H_EINVAL; }
+  u15h_status st = check_qweight(ctx, w, N, K);
+  if (st == U15H_OK) { st = check_n(ctx, N); }
+  if (st == U15H_OK) { st = check_k(ctx, K, 2, 8); }
+  if (st == U15H_OK) { st = check_rows(ctx, M, 0); }
+  if (st != U15H_OK) { return st; }
+  if (M == 0) { ctx->err.clear(); return U15H_OK; }
+  if (x == nullptr || y == nullptr || !aligned16(x) || !aligned16(y) ||
+      (bias != nullptr && !aligned16(bias))) {
+    return fail(ctx, U15H_EINVAL, "x/y null, or x/y/bias misaligned");
+  }
+  const size_t need = (size_t)N * K * 2;
+  if (ctx->w_deq_bytes < need) {
+    if (ctx->w_deq != nullptr) {
+      (void)hipStreamSynchronize(as_stream(stream));
+      (void)hipFree(ctx->w_deq);
+      ctx->w_deq = nullptr;
+      ctx->w_deq_bytes = 0;
+    }
+    if ((st = bind_device(ctx)) != U15H_OK) { return st; }
+    if (hipMalloc(&ctx->w_deq, need) != hipSuccess) {
+      ctx->w_deq = nullptr;
+      return fail(ctx, U15H_ENOMEM, "dequant scratch of %zu bytes", need);
+    }
+    ctx->w_deq_bytes = need;
+  }
+  u15h_bf16* wd = static_cast<u15h_bf16*>(ctx->w_deq);
+  if ((st = u15h_dequant_affine(ctx, stream, w, N, K, wd)) != U15H_OK) {
+    return st;
+  }
+  // From here it is the dense bf16 path, never the int8 tier: the
+  // reference re-enters linear_mma_'s matmul the same way
+  // (u15-metal-ops.cc:393-399).
+  return dense_bf16(ctx, as_stream(stream), x, wd, bias, y, M, K, N);
+}
+
+u15h_status
+u15h_swiglu_fused(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
+                  const u15h_bf16* w_fused, u15h_bf16* y, int M, int K,
+                  int inter)
+{
+  if (ctx == nullptr) { return U15H_EINVAL; }
+  // Weight rows are 2K apart here, so K is held to half the plain limit.
+  u15h_status st = check_k(ctx, K, 4, 8);
+  if (st == U15H_OK) { st = check_n(ctx, inter); }
+  if (st == U15H_OK) { st = check_rows(ctx, M, 0); }
+  if (st != U15H_OK) { return st; }
+  if (M == 0) { ctx->err.clear(); return U15H_OK; }
+  if (x == nullptr || w_fused == nullptr || y == nullptr || !aligned16(x) ||
+      !aligned16(w_fused) || !aligned16(y)) {
+    return fail(ctx, U15H_EINVAL, "null or misaligned swiglu_fused operand");
+  }
+  if ((st = bind_device(ctx)) != U15H_OK) { return st; }
+  // Row 2i of w_fused is gate row i and row 2i+1 up row i: two [inter][K]
+  // weights 2K bytes apart per row, the second starting one row in.
+  const size_t kb = (size_t)K * 2;
+  GemmBatch b = empty_batch(K * 2);
+  add_problem(b, x, w_fused, reinterpret_cast<const char*>(w_fused) + kb, y,
+              nullptr, nullptr, nullptr, M, inter, inter,
+              u15h::tile_cols(Epi::kSwiglu), (int)(2 * kb));
+  if ((st = check_tiles(ctx, b)) != U15H_OK) { return st; }
+  if ((st = plan_split(ctx, b)) != U15H_OK) { return st; }
+  return launched(ctx,
+                  u15h::launch_gemm_bf16(b, Epi::kSwiglu, ctx->gemm,
+                                         as_stream(stream),
+                                         take_profile_event(ctx)),
+                  "swiglu_fused");
+}
+
+u15h_status
+u15h_bias_add(u15h_ctx* ctx, u15h_stream stream, u15h_bf16* y,
+              const u15h_bf16* bias, int M, int N)
+{
+  if (ctx == nullptr) { return U15H_EINVAL; }
+  if (M < 0 || N <= 0 || N % 8 != 0) {
+    return fail(ctx, U15H_EINVAL, "M=%d N=%d (N must be a multiple of 8)", M,
+                N);
+  }
+  if (M == 0) { ctx->err.clear(); return U15H_OK; }
+  if (y == nullptr || bias == nullptr || !aligned16(y) || !aligned16(bias)) {
+    return fail(ctx, U15H_EINVAL, "y/bias null or misaligned");
+  }
+  u15h_status st = bind_device(ctx);
+  if (st != U15H_OK) { return st; }
+  return launched(ctx, u15h::launch_bias_add(y, bias, M, N, as_stream(stream)),
+                  "bias_add");
+}
+
+u15h_status
+u15h_f32_to_bf16(u15h_ctx* ctx, u15h_stream stream, const float* src,
+                 int64_t n, u15h_bf16* dst)
+{
+  if (ctx == nullptr) { return U15H_EINVAL; }
+  if (n < 0 || n % 4 != 0) {
+    return fail(ctx, U15H_EINVAL, "n=%lld must be a multiple of 4",
+                (long long)n);
+  }
+  if (n == 0) { ctx->err.clear(); return U15H_OK; }
+  if (src == nullptr || dst == nullptr || !aligned16(src) || !aligned16(dst)) {
+    return fail(ctx, U15H_EINVAL, "src/dst null or misaligned");
+  }
+  u15h_status st = bind_device(ctx);
+  if (st != U15H_OK) { return st; }
+  return launched(ctx,
+                  u15h::launch_f32_to_bf16(src, n, dst, as_stream(stream)),
+                  "f32_to_bf16");
 }
 
 u15h_status

@@ -35,6 +35,7 @@ struct GemmProblem {
   const float*    sw;     // per-column scale [n] (kDequantBf16)
   int rows;               // activation rows of this problem
   int n;                  // output columns of this problem
+  int wld;                // bytes between consecutive weight rows
   int ldy;                // output row pitch in elements
   int tiles_m;            // ceil(rows / kBM)
   int tiles_n;            // ceil(n / tile columns)
@@ -69,18 +70,32 @@ inline size_t split_ws_bytes(const GemmBatch& b)
 }
 
 // Kernel launchers (u15h_kernels.hip).  All are asynchronous on `s`.
-// `waves` selects the GEMM kernel's workgroup shape: 4 (one wave per SIMD,
-// 128x128 per wave) or 8 (two per SIMD, 128x64 per wave).
+// How the GEMM kernel is built: `waves` is the workgroup shape, 4 (one
+// wave per SIMD, 128x128 per wave) or 8 (two per SIMD, 128x64 per wave);
+// `ring` selects the four-stage LDS ring (64 bytes of K per stage) over the
+// two-stage pipeline (128 bytes).
+struct GemmShape {
+  int waves;
+  bool ring;
+};
+
 // `after_gemm`, when not null, is recorded on `s` right after the GEMM
 // kernel and before any split-K reduction kernel.
-hipError_t launch_gemm_bf16(const GemmBatch& b, Epi epi, int waves,
+hipError_t launch_gemm_bf16(const GemmBatch& b, Epi epi, const GemmShape& g,
                             hipStream_t s, hipEvent_t after_gemm);
-hipError_t launch_gemm_i8(const GemmBatch& b, Epi epi, int waves,
+hipError_t launch_gemm_i8(const GemmBatch& b, Epi epi, const GemmShape& g,
                           hipStream_t s, hipEvent_t after_gemm);
 hipError_t launch_quant_rows_i8(const uint16_t* x, int rows, int K,
                                 int8_t* q, float* sc, hipStream_t s);
 hipError_t launch_swiglu(const uint16_t* g, const uint16_t* u, uint16_t* o,
                          int64_t n, hipStream_t s);
+hipError_t launch_dequant_affine(const uint32_t* codes, const uint16_t* sc,
+                                 const uint16_t* bi, int bits, int group, int N,
+                                 int K, uint16_t* w, hipStream_t s);
+hipError_t launch_bias_add(uint16_t* y, const uint16_t* b, int M, int N,
+                           hipStream_t s);
+hipError_t launch_f32_to_bf16(const float* src, int64_t n, uint16_t* dst,
+                              hipStream_t s);
 hipError_t launch_gather_rows(const uint16_t* src, const int32_t* perm,
                               int M, int cols, uint16_t* dst, bool scatter,
                               hipStream_t s);

@@ -197,259 +197,103 @@ tile_origin(const GemmProblem& P, int tile, int* row0, int* col0)
   *col0 = (tin / gm) * tile_cols(E);
 }
 
-// WN = waves along the tile's N (weight-row) extent; 2 waves along M.
-//   WN = 2: 4 waves, each 128 x 128 (4 x 4 accumulators of 32 x 32)
-//   WN = 4: 8 waves, two per SIMD, each 128 x 64 (2 x 4 accumulators); a
-//           wave waiting on LDS, memory or the barrier leaves the matrix
-//           core to the other wave of its SIMD.
-template <class Mma, Epi E, int WN>
-__global__ __launch_bounds__(128 * WN, 1) void
-mot_gemm_kernel(const GemmBatch B)
-{
-  constexpr int kWaves = 2 * WN;
-  constexpr int NW = kBN / WN;            // weight rows (tile columns) per wave
-  constexpr int FI = NW / 32;             // weight fragments per sub-step
-  constexpr int FJ = 4;                   // activation fragments (128 rows)
-  constexpr int LB = 64 / kWaves;         // 1 KiB load blocks per wave per stage
-  // Two LDS stages as two objects, so the compiler can tell the fragment
-  // reads of one stage from the direct-to-LDS loads filling the other.
-  __shared__ __attribute__((aligned(1024))) char lds0[kStage];
-  __shared__ __attribute__((aligned(1024))) char lds1[kStage];
+// Which tile and which share of K a workgroup computes.
+struct TileWork {
+  int tile;
+  int share;
+  bool is_split;
+  int prob;     // problem index in the batch
+  int row0;     // first activation row of the tile (within the problem)
+  int col0;     // first output column of the tile
+  int kbeg;     // first K stage of this workgroup
+  int nst;      // K stages of this workgroup
+};
 
-  // ---- which tile, which share of K ------------------------------------
-  // Whole tiles: consecutive workgroups are dealt round-robin to the 8
-  // XCDs; remap so each XCD walks a contiguous run of the tile list (and so
-  // shares its operands in its own L2).  Split tiles follow, `split`
-  // consecutive workgroups per tile.
+// Whole tiles: consecutive workgroups are dealt round-robin to the 8 XCDs;
+// remap so each XCD walks a contiguous run of the tile list (and so shares
+// its operands in its own L2).  Split tiles follow, `split` consecutive
+// workgroups per tile, each a contiguous share of the `nk` K stages.
+template <Epi E>
+__device__ __forceinline__ TileWork
+tile_work(const GemmBatch& B, int nk)
+{
+  TileWork t;
   const int bid = blockIdx.x;
   const int SB = B.split_begin;
-  int tile, share = 0;
-  const bool is_split = bid >= SB;
-  if (!is_split) {
-    tile = (SB % 8 == 0) ? (bid % 8) * (SB / 8) + bid / 8 : bid;
+  t.is_split = bid >= SB;
+  t.share = 0;
+  if (!t.is_split) {
+    t.tile = (SB % 8 == 0) ? (bid % 8) * (SB / 8) + bid / 8 : bid;
   } else {
-    tile = SB + (bid - SB) / B.split;
-    share = (bid - SB) % B.split;
+    t.tile = SB + (bid - SB) / B.split;
+    t.share = (bid - SB) % B.split;
   }
-  const GemmProblem& P = B.p[find_problem(B, tile)];
-  int row0, col0;
-  tile_origin<E>(P, tile, &row0, &col0);
-  constexpr int TC = tile_cols(E);
+  t.prob = find_problem(B, t.tile);
+  tile_origin<E>(B.p[t.prob], t.tile, &t.row0, &t.col0);
+  t.kbeg = t.is_split ? (t.share * nk) / B.split : 0;
+  const int kend = t.is_split ? ((t.share + 1) * nk) / B.split : nk;
+  t.nst = kend - t.kbeg;
+  return t;
+}
 
-  const int kbytes = B.kbytes;
-  const int nk = (kbytes + kKB - 1) / kKB;
-  const int kbeg = is_split ? (share * nk) / B.split : 0;
-  const int kend = is_split ? ((share + 1) * nk) / B.split : nk;
-  const int nst = kend - kbeg;
+// Scheduling masks of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedMfma = 0x008, kSchedVmem = 0x010, kSchedDsRead = 0x100;
 
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave & 1;
-  const int wn = wave >> 1;               // 0 .. WN-1
-
-  // ---- operand extents --------------------------------------------------
-  const char* a_base = static_cast<const char*>(P.a) + (size_t)row0 * kbytes;
-  const int a_bytes = min(kBM, P.rows - row0) * kbytes;
-  const char* w_base = static_cast<const char*>(P.w) + (size_t)col0 * kbytes;
-  const int w_bytes = min(E == Epi::kSwiglu ? TC : kBN, P.n - col0) * kbytes;
-  const char* u_base = E == Epi::kSwiglu
-                           ? static_cast<const char*>(P.w2) + (size_t)col0 * kbytes
-                           : w_base;
-
-  // ---- LDS layout -------------------------------------------------------
-  // A stage is 512 rows x 128 bytes: weight rows 0..255, then activation
-  // rows.  Row r's logical 16-byte chunk c sits at chunk position
-  // c ^ ((r >> 1) & 7).  LDS serves 16 lanes of a 16-byte read per cycle
-  // over 64 four-byte banks (16 chunk-wide bank groups); a fragment read
-  // touches 16 consecutive rows at one logical chunk, whose bank groups
-  // (r & 1) * 8 + position are then all distinct.
-  //
-  // ---- direct-to-LDS loads ----------------------------------------------
-  // Wave w fills stage rows [8*LB*w, 8*LB*(w+1)) in LB blocks of 8 rows
-  // (waves 0..WN-1 the weight rows, which are then exactly the rows wave
-  // column w computes with; the others the activation rows).  One
-  // instruction writes a 1 KiB block, lane l landing at byte 16*l: row l/8
-  // of the block, chunk position l%8.  The swizzle is applied on the
-  // global side: lane l fetches logical chunk (l%8) ^ key with key =
-  // ((row >> 1) & 7) = ((b & 1) << 2) | (l >> 4) for block b.
-  //
-  // SwiGLU tiles: wave column wn owns NW/2 output columns; its NW weight
-  // rows are NW/2 gate rows then the NW/2 matching up rows, so a lane's
-  // gate and up accumulators cover the same outputs.
-  const int lrow8 = lane >> 3;
-  const int key_lo = lane >> 4;
-  const int lane_off_even =
-      lrow8 * kbytes + (((lane & 7) ^ key_lo) << 4);
-  const int lane_off_odd =
-      lrow8 * kbytes + (((lane & 7) ^ (4 | key_lo)) << 4);
-  // The range check that zero-fills rows past M / N and the K tail applies
-  // to the per-lane (VGPR) offset, so every row offset is carried there;
-  // only the stage's K offset, common to all rows, rides in the SGPR.
-  const int tail_even =
-      ((nk - 1) * kKB + (((lane & 7) ^ key_lo) << 4) < kbytes) ? 0 : kOobOffset;
-  const int tail_odd =
-      ((nk - 1) * kKB + (((lane & 7) ^ (4 | key_lo)) << 4) < kbytes) ? 0
-                                                                    : kOobOffset;
-
-  // Per-wave load parameters (wave-uniform): the resource for the first
-  // and second half of the blocks, the first operand row, and the
-  // block-index mask.
-  const bool loads_w = wave < WN;
-  const char* lo_base = loads_w ? w_base : a_base;
-  const char* hi_base = loads_w ? u_base : a_base;
-  const int ld_bytes = loads_w ? w_bytes : a_bytes;
-  const __amdgpu_buffer_rsrc_t r_lo = make_rsrc(lo_base, ld_bytes);
-  const __amdgpu_buffer_rsrc_t r_hi = make_rsrc(hi_base, ld_bytes);
-  const int row_base = loads_w ? (E == Epi::kSwiglu ? wave * (NW / 2) : wave * NW)
-                               : (wave - WN) * (8 * LB);
-  const int bmask = (loads_w && E == Epi::kSwiglu) ? (LB / 2 - 1) : (LB - 1);
-  // Stage `ktl` of this workgroup's K range.  Stages past the range load
-  // nothing: their offsets are pushed out of range, so the hardware
-  // returns zeros without a memory access.  The loop below runs an even
-  // number of stages and relies on it.
-  auto issue_loads = [&](char* stage_base, int ktl) {
-    const int kt = kbeg + ktl;
-    const int ko = __builtin_amdgcn_readfirstlane(min(kt, nk - 1) * kKB);
-    const bool last = kt == nk - 1;
-    const int oob = ktl >= nst ? kOobOffset : 0;
-    const int ve = lane_off_even + row_base * kbytes + (last ? tail_even : 0) + oob;
-    const int vo = lane_off_odd + row_base * kbytes + (last ? tail_odd : 0) + oob;
-    char* dst = stage_base + wave * (8 * LB * kKB);
+// `reads` fragment reads spread over `mfmas` MFMAs.
+template <int kMfmas, int kReads>
+__device__ __forceinline__ void
+interleave_reads()
+{
 #pragma unroll
-    for (int b = 0; b < LB; ++b) {
-      const int orow8 = (b & bmask) * 8;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          b < LB / 2 ? r_lo : r_hi,
-          (__attribute__((address_space(3))) void*)(dst + b * 1024), 16,
-          ((b & 1) ? vo : ve) + orow8 * kbytes, ko, 0, 0);
-    }
-  };
+  for (int k = 0; k < kMfmas; ++k) {
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+    if (k < kReads) { __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0); }
+  }
+}
 
-  // ---- MFMA fragments ---------------------------------------------------
+// `loads` direct loads and `reads` fragment reads spread over `mfmas` MFMAs.
+template <int kMfmas, int kLoads, int kReads>
+__device__ __forceinline__ void
+interleave_loads_reads()
+{
+  constexpr int kLoadsPerMfma = (kLoads + kMfmas - 1) / kMfmas;
+#pragma unroll
+  for (int k = 0; k < kMfmas; ++k) {
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+#pragma unroll
+    for (int l = 0; l < kLoadsPerMfma; ++l) {
+      if (k * kLoadsPerMfma + l < kLoads) {
+        __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
+      }
+    }
+    if (k < kReads) { __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0); }
+  }
+}
+
+// Epilogue of a tile.  acc[i][j][r] holds tile column (weight row within
+// the tile) wn*NW + i*32 + (r>>2)*8 + lh*4 + (r&3) and tile row wm*128 +
+// j*32 + lr.  A K share writes its raw accumulators to the workspace
+// [kBM][kBN] (rows past the problem are never read back); a whole tile
+// applies the epilogue E.
+template <class Mma, Epi E, int WN>
+__device__ __forceinline__ void
+gemm_epilogue(const GemmBatch& B, const GemmProblem& P, const TileWork& t,
+              int wm, int wn, int lane,
+              const typename Mma::acc_t (&acc)[kBN / WN / 32][4])
+{
+  constexpr int NW = kBN / WN;
+  constexpr int FI = NW / 32;
+  constexpr int FJ = 4;
   const int lr = lane & 31;
   const int lh = lane >> 5;
-  int rd[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    rd[s] = lr * kKB + (((2 * s + lh) ^ ((lr >> 1) & 7)) << 4);
-  }
-  const int wbase = wn * NW * kKB;
-  const int abase = kBN * kKB + wm * 128 * kKB;
-
-  typename Mma::acc_t acc[FI][FJ];
-#pragma unroll
-  for (int i = 0; i < FI; ++i) {
-#pragma unroll
-    for (int j = 0; j < FJ; ++j) { acc[i][j] = typename Mma::acc_t{}; }
-  }
-
-  i32x4_t fa[2][FI], fb[2][FJ];
-  auto read_frags = [&](const char* base, int s, int buf) {
-#pragma unroll
-    for (int i = 0; i < FI; ++i) {
-      fa[buf][i] = *reinterpret_cast<const i32x4_t*>(base + wbase +
-                                                     i * 32 * kKB + rd[s]);
-    }
-#pragma unroll
-    for (int j = 0; j < FJ; ++j) {
-      fb[buf][j] = *reinterpret_cast<const i32x4_t*>(base + abase +
-                                                     j * 32 * kKB + rd[s]);
-    }
-  };
-  auto mma_step = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < FI; ++i) {
-#pragma unroll
-      for (int j = 0; j < FJ; ++j) {
-        acc[i][j] = Mma::run(fa[buf][i], fb[buf][j], acc[i][j]);
-      }
-    }
-  };
-  // Scheduling masks of __builtin_amdgcn_sched_group_barrier.
-  constexpr int kSchedMfma = 0x008, kSchedVmem = 0x010, kSchedDsRead = 0x100;
-  constexpr int kMfmaPerStep = FI * FJ;
-  constexpr int kReadsPerStep = FI + FJ;
-  // The next sub-step's fragment reads spread over this sub-step's MFMAs.
-  auto interleave_reads = [&]() {
-#pragma unroll
-    for (int k = 0; k < kMfmaPerStep; ++k) {
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-      if (k < kReadsPerStep) {
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-      }
-    }
-  };
-  // The direct loads of stage kt+2 and the next stage's first fragment
-  // reads spread over the last sub-step's MFMAs.
-  auto interleave_loads_reads = [&]() {
-#pragma unroll
-    for (int k = 0; k < kMfmaPerStep; ++k) {
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-      constexpr int kLoadsPerMfma = (LB + kMfmaPerStep - 1) / kMfmaPerStep;
-#pragma unroll
-      for (int l = 0; l < kLoadsPerMfma; ++l) {
-        if (k * kLoadsPerMfma + l < LB) {
-          __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
-        }
-      }
-      if (k < kReadsPerStep) {
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-      }
-    }
-  };
-
-  // One K stage held in LDS buffer `cur`; `nxt` is the other buffer.  On
-  // entry fragments of sub-step 0 are in fa/fb[0]; fragments of sub-step
-  // s+1 are read while the 16 MFMAs of sub-step s run.  Before the last
-  // sub-step the stage's LDS is handed back: once every wave has its last
-  // fragments in registers and its direct loads of the next stage have
-  // landed, one barrier lets the loads of stage kt+2 refill `cur` and the
-  // first fragments of stage kt+1 be read while the last 16 MFMAs run.
-  // The body is branch-free (after the final stage the extra loads fetch
-  // nothing and the extra fragment reads are unused), which keeps the 256
-  // accumulators in AGPRs across the whole loop.
-  auto stage = [&](char* cur, const char* nxt, int ktl) {
-#pragma unroll
-    for (int s = 0; s < 3; ++s) {
-      read_frags(cur, s + 1, (s + 1) & 1);
-      mma_step(s & 1);
-      interleave_reads();
-    }
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-    __syncthreads();
-    issue_loads(cur, ktl + 2);
-    read_frags(nxt, 0, 0);
-    mma_step(1);
-    interleave_loads_reads();
-  };
-
-  // ---- main loop: an even number of stages; a padding stage (K past the
-  // range) reads as zeros and adds exactly 0 to every accumulator --------
-  const int nst_even = (nst + 1) & ~1;
-  issue_loads(lds0, 0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  issue_loads(lds1, 1);
-  read_frags(lds0, 0, 0);
-  for (int ktl = 0; ktl < nst_even; ktl += 2) {
-    stage(lds0, lds1, ktl);
-    stage(lds1, lds0, ktl + 1);
-  }
-  // No load may still be writing LDS when the workgroup retires.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-
-  // ---- epilogue ---------------------------------------------------------
-  // acc[i][j][r]: tile column (weight row within the tile) wn*NW + i*32 +
-  // (r>>2)*8 + lh*4 + (r&3), tile row wm*128 + j*32 + lr.
-  if (is_split) {
-    // Raw accumulators of this K share -> workspace [kBM][kBN] (rows past
-    // the problem are never read back).
+  if (t.is_split) {
     int32_t* wsb = static_cast<int32_t*>(B.ws) +
-                   (size_t)((tile - SB) * B.split + share) * (kBM * kBN);
+                   (size_t)((t.tile - B.split_begin) * B.split + t.share) *
+                       (kBM * kBN);
 #pragma unroll
     for (int j = 0; j < FJ; ++j) {
       const int ml = wm * 128 + j * 32 + lr;
-      if (row0 + ml >= P.rows) { continue; }
+      if (t.row0 + ml >= P.rows) { continue; }
 #pragma unroll
       for (int i = 0; i < FI; ++i) {
 #pragma unroll
@@ -466,14 +310,14 @@ mot_gemm_kernel(const GemmBatch B)
   }
 #pragma unroll
   for (int j = 0; j < FJ; ++j) {
-    const int m = row0 + wm * 128 + j * 32 + lr;
+    const int m = t.row0 + wm * 128 + j * 32 + lr;
     if (m >= P.rows) { continue; }
     if constexpr (E == Epi::kSwiglu) {
 #pragma unroll
       for (int i = 0; i < FI / 2; ++i) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int n = col0 + wn * (NW / 2) + i * 32 + g * 8 + lh * 4;
+          const int n = t.col0 + wn * (NW / 2) + i * 32 + g * 8 + lh * 4;
           if (n >= P.n) { continue; }
           float gv[4], uv[4];
 #pragma unroll
@@ -489,7 +333,7 @@ mot_gemm_kernel(const GemmBatch B)
       for (int i = 0; i < FI; ++i) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int n = col0 + wn * NW + i * 32 + g * 8 + lh * 4;
+          const int n = t.col0 + wn * NW + i * 32 + g * 8 + lh * 4;
           if (n >= P.n) { continue; }
           const auto& a = acc[i][j];
           if constexpr (E == Epi::kI32) {
@@ -506,6 +350,257 @@ mot_gemm_kernel(const GemmBatch B)
       }
     }
   }
+}
+
+// The GEMM main loop, parametrised by the LDS pipeline:
+//   KB     bytes of K per stage per row (128: 64 bf16 / 128 int8; or 64)
+//   RING   LDS stages in the ring (2 with KB=128, 4 with KB=64: 128 KiB)
+// A ring stage is (kBM + kBN) rows x KB bytes: weight rows 0..255, then
+// activation rows.  Loads for stage k+RING are issued once stage k's
+// buffer is free, so a load has RING-1 stages to land.
+//
+// WN = waves along the tile's N (weight-row) extent; 2 waves along M.
+//   WN = 2: 4 waves, each 128 x 128 (4 x 4 accumulators of 32 x 32)
+//   WN = 4: 8 waves, two per SIMD, each 128 x 64 (2 x 4 accumulators); a
+//           wave waiting on LDS, memory or the barrier leaves the matrix
+//           core to the other wave of its SIMD.
+//
+// LDS layout.  Row r's logical 16-byte chunk c sits at position
+// c ^ key(r).  LDS serves 16 lanes of a 16-byte read per cycle over 64
+// four-byte banks (16 bank groups of 16 bytes); a fragment read touches 16
+// consecutive rows at one logical chunk, so key(r) is chosen to put those
+// 16 reads in 16 different bank groups:
+//   KB = 128 (8 chunks/row, 2 rows per 256 B): key(r) = (r >> 1) & 7
+//   KB =  64 (4 chunks/row, 4 rows per 256 B): key(r) = (r >> 2) & 3
+//
+// Direct-to-LDS loads.  One buffer_load ... lds instruction writes a 1 KiB
+// block, lane l landing at byte 16*l (KB/16 chunks per row, 1024/KB rows
+// per block).  The swizzle is applied on the global side: lane l fetches
+// the logical chunk that belongs at its landing position.  Wave w fills
+// stage rows [w * R, (w+1) * R) with R = 512 / waves (waves 0..WN-1 the
+// weight rows, exactly the rows wave column w computes with; the others
+// the activation rows).  SwiGLU tiles: wave column wn owns NW/2 output
+// columns; its NW weight rows are NW/2 gate rows then the NW/2 matching up
+// rows, so a lane's gate and up accumulators cover the same outputs.
+//
+// Buffer resources span only the tile's valid rows, so rows past M or N
+// read as zero in hardware; the K tail and the stages past this
+// workgroup's K range are zero-filled by pushing their offsets out of
+// range.  The range check applies to the per-lane (VGPR) offset, so every
+// row offset is carried there; only the stage's K offset, common to all
+// rows, rides in the SGPR.
+template <class Mma, Epi E, int WN, int KB, int RING>
+__device__ __forceinline__ void
+gemm_tile(const GemmBatch& B, char* const (&ring)[RING])
+{
+  constexpr int kWaves = 2 * WN;
+  constexpr int NW = kBN / WN;               // weight rows per wave
+  constexpr int FI = NW / 32;                // weight fragments per sub-step
+  constexpr int FJ = 4;                      // activation fragments
+  constexpr int kStageBytes = (kBM + kBN) * KB;
+  constexpr int kRowsPerBlock = 1024 / KB;   // rows one load instruction fills
+  constexpr int kChunks = KB / 16;           // 16-byte chunks per row
+  constexpr int LB = kStageBytes / 1024 / kWaves;   // load blocks per wave
+  constexpr int kSub = KB / 32;              // MFMA sub-steps per stage
+  constexpr int kRowsPerWave = (kBM + kBN) / kWaves;
+
+  const int kbytes = B.kbytes;
+  const int nk = (kbytes + KB - 1) / KB;
+  const TileWork t = tile_work<E>(B, nk);
+  const GemmProblem& P = B.p[t.prob];
+  constexpr int TC = tile_cols(E);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave & 1;
+  const int wn = wave >> 1;
+
+  // ---- operand extents and per-wave load parameters (wave-uniform) ------
+  // Weight rows are wld bytes apart (kbytes for a plain [N][K] matrix, 2K
+  // for the reference's row-interleaved gate/up weight).
+  const int wld = P.wld;
+  const char* a_base = static_cast<const char*>(P.a) + (size_t)t.row0 * kbytes;
+  const int a_bytes = min(kBM, P.rows - t.row0) * kbytes;
+  const char* w_base = static_cast<const char*>(P.w) + (size_t)t.col0 * wld;
+  const int w_bytes = min(E == Epi::kSwiglu ? TC : kBN, P.n - t.col0) * wld;
+  const char* u_base = E == Epi::kSwiglu
+                           ? static_cast<const char*>(P.w2) + (size_t)t.col0 * wld
+                           : w_base;
+  const bool loads_w = wave < WN;
+  const int pitch = loads_w ? wld : kbytes;
+  const __amdgpu_buffer_rsrc_t r_lo =
+      make_rsrc(loads_w ? w_base : a_base, loads_w ? w_bytes : a_bytes);
+  const __amdgpu_buffer_rsrc_t r_hi =
+      make_rsrc(loads_w ? u_base : a_base, loads_w ? w_bytes : a_bytes);
+  // First operand row and block mask: blocks [0, LB/2) use r_lo and
+  // [LB/2, LB) r_hi (SwiGLU weights: gate then up).
+  const int row_base =
+      loads_w ? (E == Epi::kSwiglu ? wave * (kRowsPerWave / 2) : wave * kRowsPerWave)
+              : (wave - WN) * kRowsPerWave;
+  const int bmask = (loads_w && E == Epi::kSwiglu) ? (LB / 2 - 1) : (LB - 1);
+
+  // Lane landing position -> logical chunk.  Blocks start at rows that are
+  // multiples of kRowsPerBlock, so the key depends on the block only through
+  // its parity when KB = 128 (8 rows per block) and not at all when KB = 64.
+  const int lrow = lane / kChunks;                  // row within the block
+  const int lpos = lane % kChunks;                  // landing position
+  auto key_of = [&](int blk_row) {
+    if constexpr (KB == 128) { return ((blk_row + lrow) >> 1) & 7; }
+    else { return ((blk_row + lrow) >> 2) & 3; }
+  };
+  const int chunk_even = lpos ^ key_of(0);
+  const int chunk_odd = lpos ^ key_of(kRowsPerBlock);
+  const int lane_even = lrow * pitch + (chunk_even << 4);
+  const int lane_odd = lrow * pitch + (chunk_odd << 4);
+  const int tail_even =
+      ((nk - 1) * KB + (chunk_even << 4) < kbytes) ? 0 : kOobOffset;
+  const int tail_odd =
+      ((nk - 1) * KB + (chunk_odd << 4) < kbytes) ? 0 : kOobOffset;
+
+  auto issue_loads = [&](char* stage_base, int ktl) {
+    const int kt = t.kbeg + ktl;
+    const int ko = __builtin_amdgcn_readfirstlane(min(kt, nk - 1) * KB);
+    const bool last = kt == nk - 1;
+    const int oob = ktl >= t.nst ? kOobOffset : 0;
+    const int ve = lane_even + row_base * pitch + (last ? tail_even : 0) + oob;
+    const int vo = lane_odd + row_base * pitch + (last ? tail_odd : 0) + oob;
+    char* dst = stage_base + wave * (kRowsPerWave * KB);
+#pragma unroll
+    for (int b = 0; b < LB; ++b) {
+      const int orow = (b & bmask) * kRowsPerBlock;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          b < LB / 2 ? r_lo : r_hi,
+          (__attribute__((address_space(3))) void*)(dst + b * 1024), 16,
+          ((b & 1) ? vo : ve) + orow * pitch, ko, 0, 0);
+    }
+  };
+
+  // ---- MFMA fragments ---------------------------------------------------
+  const int lr = lane & 31;
+  const int lh = lane >> 5;
+  int rd[kSub];
+#pragma unroll
+  for (int s = 0; s < kSub; ++s) {
+    const int key = KB == 128 ? ((lr >> 1) & 7) : ((lr >> 2) & 3);
+    rd[s] = lr * KB + (((2 * s + lh) ^ key) << 4);
+  }
+  const int wbase = wn * NW * KB;
+  const int abase = kBN * KB + wm * 128 * KB;
+
+  typename Mma::acc_t acc[FI][FJ];
+#pragma unroll
+  for (int i = 0; i < FI; ++i) {
+#pragma unroll
+    for (int j = 0; j < FJ; ++j) { acc[i][j] = typename Mma::acc_t{}; }
+  }
+
+  i32x4_t fa[2][FI], fb[2][FJ];
+  auto read_frags = [&](const char* base, int s, int buf) {
+#pragma unroll
+    for (int i = 0; i < FI; ++i) {
+      fa[buf][i] = *reinterpret_cast<const i32x4_t*>(base + wbase + i * 32 * KB +
+                                                     rd[s]);
+    }
+#pragma unroll
+    for (int j = 0; j < FJ; ++j) {
+      fb[buf][j] = *reinterpret_cast<const i32x4_t*>(base + abase + j * 32 * KB +
+                                                     rd[s]);
+    }
+  };
+  auto mma_step = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < FI; ++i) {
+#pragma unroll
+      for (int j = 0; j < FJ; ++j) {
+        acc[i][j] = Mma::run(fa[buf][i], fb[buf][j], acc[i][j]);
+      }
+    }
+  };
+  constexpr int kMfmaPerStep = FI * FJ;
+  constexpr int kReadsPerStep = FI + FJ;
+
+  // One K stage in ring buffer `cur`; `nxt` holds the next stage.  On entry
+  // the fragments of sub-step 0 are in fa/fb[0]; the fragments of sub-step
+  // s+1 are read while the MFMAs of sub-step s run.  Before the last
+  // sub-step the stage's buffer is handed back: once every wave has its
+  // last fragments in registers and its loads of the next stage have
+  // landed (at most the loads of the RING-2 stages after it may still be
+  // in flight; loads complete in issue order), one barrier lets the loads
+  // of stage k+RING refill `cur` and the first fragments of the next stage
+  // be read while the last MFMAs run.  The body is branch-free, which keeps
+  // the accumulators in registers across the whole loop; past the last
+  // stage the extra loads fetch nothing and the extra reads are unused.
+  auto stage = [&](char* cur, const char* nxt, int ktl) {
+#pragma unroll
+    for (int s = 0; s + 1 < kSub; ++s) {
+      read_frags(cur, s + 1, (s + 1) & 1);
+      mma_step(s & 1);
+      interleave_reads<kMfmaPerStep, kReadsPerStep>();
+    }
+    if constexpr (RING == 2) {
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    } else if constexpr (LB == 4) {
+      asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)" ::: "memory");
+    }
+    __syncthreads();
+    issue_loads(cur, ktl + RING);
+    read_frags(nxt, 0, 0);
+    mma_step((kSub - 1) & 1);
+    interleave_loads_reads<kMfmaPerStep, LB, kReadsPerStep>();
+  };
+
+  // ---- main loop: a multiple of RING stages; a padding stage (K past the
+  // range) reads as zeros and adds exactly 0 to every accumulator --------
+  const int nst_pad = (t.nst + RING - 1) / RING * RING;
+#pragma unroll
+  for (int r = 0; r < RING; ++r) { issue_loads(ring[r], r); }
+  if constexpr (RING == 2) {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LB) : "memory");
+  } else {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * LB) : "memory");
+  }
+  __syncthreads();
+  read_frags(ring[0], 0, 0);
+  for (int ktl = 0; ktl < nst_pad; ktl += RING) {
+#pragma unroll
+    for (int r = 0; r < RING; ++r) {
+      stage(ring[r], ring[(r + 1) % RING], ktl + r);
+    }
+  }
+  // No load may still be writing LDS when the workgroup retires.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  gemm_epilogue<Mma, E, WN>(B, P, t, wm, wn, lane, acc);
+}
+
+// Two 64 KiB stages of 128 bytes of K per row.
+template <class Mma, Epi E, int WN>
+__global__ __launch_bounds__(128 * WN, 1) void
+mot_gemm_kernel(const GemmBatch B)
+{
+  // Stages as separate objects, so the compiler can tell the fragment
+  // reads of one stage from the direct-to-LDS loads filling another.
+  __shared__ __attribute__((aligned(1024))) char lds0[kStage];
+  __shared__ __attribute__((aligned(1024))) char lds1[kStage];
+  char* const ring[2] = {lds0, lds1};
+  gemm_tile<Mma, E, WN, kKB, 2>(B, ring);
+}
+
+// A ring of four 32 KiB stages of 64 bytes of K per row: loads have three
+// stages to land instead of one.
+template <class Mma, Epi E, int WN>
+__global__ __launch_bounds__(128 * WN, 1) void
+mot_gemm_ring_kernel(const GemmBatch B)
+{
+  constexpr int kRingStage = (kBM + kBN) * 64;
+  __shared__ __attribute__((aligned(1024))) char lds0[kRingStage];
+  __shared__ __attribute__((aligned(1024))) char lds1[kRingStage];
+  __shared__ __attribute__((aligned(1024))) char lds2[kRingStage];
+  __shared__ __attribute__((aligned(1024))) char lds3[kRingStage];
+  char* const ring[4] = {lds0, lds1, lds2, lds3};
+  gemm_tile<Mma, E, WN, 64, 4>(B, ring);
 }
 
 // ---- split-K reduction --------------------------------------------------
@@ -685,6 +780,83 @@ swiglu_kernel(const uint4* __restrict__ g, const uint4* __restrict__ u,
   }
 }
 
+// ---- affine-quantized weights: dequant once to bf16 ----------------------
+// One thread per u32 code word (32/BITS codes of one row): w = scale * code
+// + bias of the code's group, a multiply then an add in f32 (no fused
+// multiply-add, so the rounding is the pack fixture's), rounded to bf16.
+template <int BITS>
+__global__ __launch_bounds__(256) void
+dequant_affine_kernel(const uint32_t* __restrict__ codes,
+                      const uint16_t* __restrict__ sc,
+                      const uint16_t* __restrict__ bi, int group, int N, int K,
+                      uint16_t* __restrict__ w)
+{
+  constexpr int kPer = 32 / BITS;
+  constexpr uint32_t kMask = (1u << BITS) - 1u;
+  const int words = K / kPer;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)N * words) { return; }
+  const int n = (int)(idx / words);
+  const int wi = (int)(idx % words);
+  const int k0 = wi * kPer;
+  const int gidx = n * (K / group) + k0 / group;   // kPer divides group
+  const float s = bf16_to_f32(sc[gidx]);
+  const float b = bf16_to_f32(bi[gidx]);
+  const uint32_t word = codes[idx];
+  uint32_t out[kPer / 2];
+#pragma unroll
+  for (int e = 0; e < kPer; e += 2) {
+    const float v0 = __fadd_rn(__fmul_rn(s, (float)((word >> (e * BITS)) & kMask)), b);
+    const float v1 = __fadd_rn(__fmul_rn(s, (float)((word >> ((e + 1) * BITS)) & kMask)), b);
+    out[e / 2] = bf16_bits(v0) | (bf16_bits(v1) << 16);
+  }
+  uint16_t* dst = w + (size_t)n * K + k0;
+  if constexpr (BITS == 8) {
+    *reinterpret_cast<uint2*>(dst) = make_uint2(out[0], out[1]);
+  } else {
+    *reinterpret_cast<uint4*>(dst) = make_uint4(out[0], out[1], out[2], out[3]);
+  }
+}
+
+// ---- y += bias, broadcast over rows (bf16, f32 add) ---------------------
+__global__ __launch_bounds__(256) void
+bias_add_kernel(uint16_t* __restrict__ y, const uint16_t* __restrict__ b,
+                int N, int64_t nvec)
+{
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nvec;
+       i += stride) {
+    const int64_t e0 = i * 8;
+    const int n0 = (int)(e0 % N);
+    uint4 v = reinterpret_cast<uint4*>(y)[i];
+    const uint4 bb = *reinterpret_cast<const uint4*>(b + n0);
+    const uint32_t yw[4] = {v.x, v.y, v.z, v.w};
+    const uint32_t bw[4] = {bb.x, bb.y, bb.z, bb.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = bf16_to_f32(yw[e] & 0xffffu) + bf16_to_f32(bw[e] & 0xffffu);
+      const float hi = bf16_to_f32(yw[e] >> 16) + bf16_to_f32(bw[e] >> 16);
+      o[e] = bf16_bits(lo) | (bf16_bits(hi) << 16);
+    }
+    reinterpret_cast<uint4*>(y)[i] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+// ---- f32 -> bf16, round to nearest even ----------------------------------
+__global__ __launch_bounds__(256) void
+f32_to_bf16_kernel(const float4* __restrict__ src, uint2* __restrict__ dst,
+                   int64_t nvec)
+{
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nvec;
+       i += stride) {
+    const float4 v = src[i];
+    dst[i] = make_uint2(bf16_bits(v.x) | (bf16_bits(v.y) << 16),
+                        bf16_bits(v.z) | (bf16_bits(v.w) << 16));
+  }
+}
+
 // ---- row gather / scatter for per-token routing ------------------------
 template <bool kScatter>
 __global__ __launch_bounds__(256) void
@@ -706,11 +878,16 @@ gather_rows_kernel(const uint16_t* __restrict__ src,
 
 template <class Mma, Epi E, int WN>
 hipError_t
-launch_gemm(const GemmBatch& b, hipStream_t s, hipEvent_t after_gemm)
+launch_gemm(const GemmBatch& b, bool ring, hipStream_t s, hipEvent_t after_gemm)
 {
   if (b.total_tiles <= 0) { return hipSuccess; }
-  hipLaunchKernelGGL((mot_gemm_kernel<Mma, E, WN>), dim3(grid_blocks(b)),
-                     dim3(128 * WN), 0, s, b);
+  if (ring) {
+    hipLaunchKernelGGL((mot_gemm_ring_kernel<Mma, E, WN>), dim3(grid_blocks(b)),
+                       dim3(128 * WN), 0, s, b);
+  } else {
+    hipLaunchKernelGGL((mot_gemm_kernel<Mma, E, WN>), dim3(grid_blocks(b)),
+                       dim3(128 * WN), 0, s, b);
+  }
   hipError_t e = hipGetLastError();
   if (e == hipSuccess && after_gemm != nullptr) {
     e = hipEventRecord(after_gemm, s);
@@ -725,37 +902,37 @@ launch_gemm(const GemmBatch& b, hipStream_t s, hipEvent_t after_gemm)
 
 template <class Mma, Epi E>
 hipError_t
-launch_gemm_waves(const GemmBatch& b, int waves, hipStream_t s, hipEvent_t ev)
+launch_gemm_waves(const GemmBatch& b, const GemmShape& g, hipStream_t s,
+                  hipEvent_t ev)
 {
-  return waves == 4 ? launch_gemm<Mma, E, 2>(b, s, ev)
-                    : launch_gemm<Mma, E, 4>(b, s, ev);
+  return g.waves == 4 ? launch_gemm<Mma, E, 2>(b, g.ring, s, ev)
+                      : launch_gemm<Mma, E, 4>(b, g.ring, s, ev);
 }
 
 }  // namespace
 
 hipError_t
-launch_gemm_bf16(const GemmBatch& b, Epi epi, int waves, hipStream_t s,
-                 hipEvent_t after_gemm)
+launch_gemm_bf16(const GemmBatch& b, Epi epi, const GemmShape& g,
+                 hipStream_t s, hipEvent_t after_gemm)
 {
   switch (epi) {
     case Epi::kBf16:
-      return launch_gemm_waves<MmaBf16, Epi::kBf16>(b, waves, s, after_gemm);
+      return launch_gemm_waves<MmaBf16, Epi::kBf16>(b, g, s, after_gemm);
     case Epi::kSwiglu:
-      return launch_gemm_waves<MmaBf16, Epi::kSwiglu>(b, waves, s, after_gemm);
+      return launch_gemm_waves<MmaBf16, Epi::kSwiglu>(b, g, s, after_gemm);
     default: return hipErrorInvalidValue;
   }
 }
 
 hipError_t
-launch_gemm_i8(const GemmBatch& b, Epi epi, int waves, hipStream_t s,
+launch_gemm_i8(const GemmBatch& b, Epi epi, const GemmShape& g, hipStream_t s,
                hipEvent_t after_gemm)
 {
   switch (epi) {
     case Epi::kI32:
-      return launch_gemm_waves<MmaI8, Epi::kI32>(b, waves, s, after_gemm);
+      return launch_gemm_waves<MmaI8, Epi::kI32>(b, g, s, after_gemm);
     case Epi::kDequantBf16:
-      return launch_gemm_waves<MmaI8, Epi::kDequantBf16>(b, waves, s,
-                                                        after_gemm);
+      return launch_gemm_waves<MmaI8, Epi::kDequantBf16>(b, g, s, after_gemm);
     default: return hipErrorInvalidValue;
   }
 }
@@ -793,6 +970,48 @@ launch_swiglu(const uint16_t* g, const uint16_t* u, uint16_t* o, int64_t n,
 }
 
 hipError_t
+launch_dequant_affine(const uint32_t* codes, const uint16_t* sc,
+                      const uint16_t* bi, int bits, int group, int N, int K,
+                      uint16_t* w, hipStream_t s)
+{
+  const int64_t words = (int64_t)N * (K * bits / 32);
+  if (words <= 0) { return hipSuccess; }
+  const dim3 grid((unsigned)((words + 255) / 256));
+  if (bits == 8) {
+    hipLaunchKernelGGL(dequant_affine_kernel<8>, grid, dim3(256), 0, s, codes,
+                       sc, bi, group, N, K, w);
+  } else {
+    hipLaunchKernelGGL(dequant_affine_kernel<4>, grid, dim3(256), 0, s, codes,
+                       sc, bi, group, N, K, w);
+  }
+  return hipGetLastError();
+}
+
+hipError_t
+launch_bias_add(uint16_t* y, const uint16_t* b, int M, int N, hipStream_t s)
+{
+  const int64_t nvec = (int64_t)M * N / 8;
+  if (nvec <= 0) { return hipSuccess; }
+  const int64_t want = (nvec + 255) / 256;
+  hipLaunchKernelGGL(bias_add_kernel, dim3((unsigned)(want < 8192 ? want : 8192)),
+                     dim3(256), 0, s, y, b, N, nvec);
+  return hipGetLastError();
+}
+
+hipError_t
+launch_f32_to_bf16(const float* src, int64_t n, uint16_t* dst, hipStream_t s)
+{
+  const int64_t nvec = n / 4;
+  if (nvec <= 0) { return hipSuccess; }
+  const int64_t want = (nvec + 255) / 256;
+  hipLaunchKernelGGL(f32_to_bf16_kernel,
+                     dim3((unsigned)(want < 8192 ? want : 8192)), dim3(256), 0,
+                     s, reinterpret_cast<const float4*>(src),
+                     reinterpret_cast<uint2*>(dst), nvec);
+  return hipGetLastError();
+}
+
+hipError_t
 launch_gather_rows(const uint16_t* src, const int32_t* perm, int M, int cols,
                    uint16_t* dst, bool scatter, hipStream_t s)
 {
@@ -812,6 +1031,10 @@ bool
 gemm_kernels_loadable()
 {
   const void* fns[] = {
+      reinterpret_cast<const void*>(&mot_gemm_ring_kernel<MmaBf16, Epi::kBf16, WN>),
+      reinterpret_cast<const void*>(&mot_gemm_ring_kernel<MmaBf16, Epi::kSwiglu, WN>),
+      reinterpret_cast<const void*>(&mot_gemm_ring_kernel<MmaI8, Epi::kI32, WN>),
+      reinterpret_cast<const void*>(&mot_gemm_ring_kernel<MmaI8, Epi::kDequantBf16, WN>),
       reinterpret_cast<const void*>(&mot_gemm_kernel<MmaBf16, Epi::kBf16, WN>),
       reinterpret_cast<const void*>(&mot_gemm_kernel<MmaBf16, Epi::kSwiglu, WN>),
       reinterpret_cast<const void*>(&mot_gemm_kernel<MmaI8, Epi::kI32, WN>),
@@ -835,6 +1058,10 @@ kernels_loadable()
       reinterpret_cast<const void*>(&quant_rows_i8_kernel<2>),
       reinterpret_cast<const void*>(&quant_rows_i8_kernel<6>),
       reinterpret_cast<const void*>(&swiglu_kernel),
+      reinterpret_cast<const void*>(&dequant_affine_kernel<8>),
+      reinterpret_cast<const void*>(&dequant_affine_kernel<4>),
+      reinterpret_cast<const void*>(&bias_add_kernel),
+      reinterpret_cast<const void*>(&f32_to_bf16_kernel),
       reinterpret_cast<const void*>(&gather_rows_kernel<true>),
       reinterpret_cast<const void*>(&gather_rows_kernel<false>),
   };

@@ -52,6 +52,12 @@ class _MotProjI8(ctypes.Structure):
                 ("y", ctypes.c_void_p), ("N", ctypes.c_int)]
 
 
+class _QWeight(ctypes.Structure):
+    _fields_ = [("codes", ctypes.c_void_p), ("scales", ctypes.c_void_p),
+                ("biases", ctypes.c_void_p), ("bits", ctypes.c_int),
+                ("group", ctypes.c_int)]
+
+
 def declared_symbols() -> list[str]:
     """Every function include/u15h.h declares."""
     text = HEADER_PATH.read_text()
@@ -91,6 +97,13 @@ def load_library() -> ctypes.CDLL:
                                  ctypes.POINTER(_MotProjI8), i]),
         "u15h_route_rows": (i, [vp, i, vp, ctypes.POINTER(i),
                                 ctypes.POINTER(i)]),
+        "u15h_dequant_affine": (i, [vp, vp, ctypes.POINTER(_QWeight), i, i,
+                                    vp]),
+        "u15h_linear_q": (i, [vp, vp, vp, ctypes.POINTER(_QWeight), vp, vp,
+                              i, i, i]),
+        "u15h_swiglu_fused": (i, [vp, vp, vp, vp, vp, i, i, i]),
+        "u15h_bias_add": (i, [vp, vp, vp, vp, i, i]),
+        "u15h_f32_to_bf16": (i, [vp, vp, vp, i64, vp]),
         "u15h_gather_rows": (i, [vp, vp, vp, vp, i, i, vp]),
         "u15h_scatter_rows": (i, [vp, vp, vp, vp, i, i, vp]),
     }
@@ -214,7 +227,63 @@ class Ops:
                                        M_und, M_gen, K, arr, len(projs))
         self._check(st, "u15h_mot_linear")
 
+    # ---- affine-quantized weights ---------------------------------------
+    @staticmethod
+    def _qweight(qw, N, K):
+        codes, scales, biases, bits, group = qw
+        _need(codes, torch.int32, (N, K * bits // 32), "codes")
+        _need(scales, torch.bfloat16, (N, K // group), "scales")
+        _need(biases, torch.bfloat16, (N, K // group), "biases")
+        return _QWeight(codes.data_ptr(), scales.data_ptr(),
+                        biases.data_ptr(), bits, group)
+
+    def dequant_affine(self, qw, N, K, w_out, stream=None):
+        """Expand qw = (codes int32 [N][K*bits/32], scales bf16, biases bf16,
+        bits, group) into w_out bf16 [N][K]."""
+        _need(w_out, torch.bfloat16, (N, K), "w_out")
+        q = self._qweight(qw, N, K)
+        st = self._lib.u15h_dequant_affine(self._ctx, _stream(stream),
+                                           ctypes.byref(q), N, K, _ptr(w_out))
+        self._check(st, "u15h_dequant_affine")
+
+    def linear_q(self, x, qw, bias, y, M, K, N, stream=None):
+        """MetalOps::linear on a QWeight: dequant once, then the dense GEMM."""
+        _need(x, torch.bfloat16, (M, K), "x")
+        _need(y, torch.bfloat16, (M, N), "y")
+        if bias is not None:
+            _need(bias, torch.bfloat16, (N,), "bias")
+        q = self._qweight(qw, N, K)
+        st = self._lib.u15h_linear_q(self._ctx, _stream(stream), _ptr(x),
+                                     ctypes.byref(q), _ptr(bias), _ptr(y),
+                                     M, K, N)
+        self._check(st, "u15h_linear_q")
+
+    def bias_add(self, y, bias, stream=None):
+        M, N = y.shape
+        _need(y, torch.bfloat16, (M, N), "y")
+        _need(bias, torch.bfloat16, (N,), "bias")
+        st = self._lib.u15h_bias_add(self._ctx, _stream(stream), _ptr(y),
+                                     _ptr(bias), M, N)
+        self._check(st, "u15h_bias_add")
+
+    def f32_to_bf16(self, src, dst, stream=None):
+        _need(src, torch.float32, tuple(src.shape), "src")
+        _need(dst, torch.bfloat16, tuple(src.shape), "dst")
+        st = self._lib.u15h_f32_to_bf16(self._ctx, _stream(stream), _ptr(src),
+                                        src.numel(), _ptr(dst))
+        self._check(st, "u15h_f32_to_bf16")
+
     # ---- swiglu --------------------------------------------------------
+    def swiglu_fused(self, x, w_fused, y, M, K, inter, stream=None):
+        """MetalOps::swiglu_fused: w_fused [2*inter][K] row-interleaved
+        (row 2i gate i, row 2i+1 up i)."""
+        _need(x, torch.bfloat16, (M, K), "x")
+        _need(w_fused, torch.bfloat16, (2 * inter, K), "w_fused")
+        _need(y, torch.bfloat16, (M, inter), "y")
+        st = self._lib.u15h_swiglu_fused(self._ctx, _stream(stream), _ptr(x),
+                                         _ptr(w_fused), _ptr(y), M, K, inter)
+        self._check(st, "u15h_swiglu_fused")
+
     def swiglu(self, gate, up, out, stream=None):
         n = gate.numel()
         for t, nm in ((gate, "gate"), (up, "up"), (out, "out")):
