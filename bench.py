@@ -39,13 +39,30 @@ FLOP_PER_ROW = 2 * (HIDDEN * NQ + 2 * HIDDEN * NKV + NQ * HIDDEN
                     + 2 * HIDDEN * INTER + INTER * HIDDEN)   # 385,875,968
 
 
+# name -> (m_und, m_gen, layers, description)
+WORKLOADS = {
+    "c2": (128, 4096, 1, "BASELINE config 2: one MoT layer's 7 projections x "
+                         "2 weight sets"),
+    "c4": (4352, 12288, 1, "BASELINE config 4 (edit + CFG): one MoT layer's 7 "
+                           "projections x 2 weight sets, unequal groups"),
+    "c5": (128, 4096, 42, "BASELINE config 5: the 42-layer stack, 84 weight "
+                          "sets resident in HBM, each layer's 7 projections"),
+}
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--m-und", type=int, default=128)
-    ap.add_argument("--m-gen", type=int, default=4096)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c2",
+                    help="c2: one layer, 128 und + 4096 gen tokens (the "
+                         "headline); c4: one layer, edit + CFG, 4352 und + "
+                         "12288 gen; c5: the 42-layer stack, every layer's "
+                         "weights resident, 128 und + 4096 gen (or --m-gen "
+                         "1024)")
+    ap.add_argument("--m-und", type=int, default=None)
+    ap.add_argument("--m-gen", type=int, default=None)
     ap.add_argument("--no-int8", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
@@ -56,7 +73,12 @@ def parse():
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy 5 times "
                          "(calibrates rocprof FETCH_SIZE / WRITE_SIZE)")
-    return ap.parse_args()
+    a = ap.parse_args()
+    mu, mg, layers, _ = WORKLOADS[a.workload]
+    a.m_und = mu if a.m_und is None else a.m_und
+    a.m_gen = mg if a.m_gen is None else a.m_gen
+    a.layers = layers
+    return a
 
 
 COPY_PROBE_BYTES = 1 << 30
@@ -110,8 +132,16 @@ class Layer:
                     self.q[(e, n)] = (wq, sw)
 
 
-def bf16_launches(ops, L, A, fused):
-    """The step's launches as closures (so events can bracket each)."""
+def bf16_launches(ops, layers, A, fused):
+    """The step's launches as closures (so events can bracket each), layer
+    after layer."""
+    runs = []
+    for L in layers:
+        runs += _bf16_layer(ops, L, A, fused)
+    return runs
+
+
+def _bf16_layer(ops, L, A, fused):
     mu, mg = A["mu"], A["mg"]
 
     def P(names, outs):
@@ -134,9 +164,16 @@ def bf16_launches(ops, L, A, fused):
     return runs
 
 
-def i8_launches(ops, L, A):
-    """int8 step: quantise each distinct input per token, then the grouped
-    int8 GEMM with fused dequant."""
+def i8_launches(ops, layers, A):
+    """int8 step: per layer, quantise each distinct input per token, then
+    the grouped int8 GEMM with fused dequant."""
+    runs = []
+    for L in layers:
+        runs += _i8_layer(ops, L, A)
+    return runs
+
+
+def _i8_layer(ops, L, A):
     mu, mg = A["mu"], A["mg"]
 
     def P(names, outs):
@@ -338,12 +375,12 @@ def main():
     ops = u15h.Ops(0)
     gen = torch.Generator(device="cuda").manual_seed(args.seed)
     want_i8 = not args.no_int8
-    L = Layer(gen, torch, want_i8, ops)
+    layers = [Layer(gen, torch, want_i8, ops) for _ in range(args.layers)]
     A = activations(gen, torch, args.m_und, args.m_gen)
     M = args.m_und + args.m_gen
-    flop = FLOP_PER_ROW * M
+    flop = FLOP_PER_ROW * M * args.layers
 
-    runs = bf16_launches(ops, L, A, args.fused_swiglu)
+    runs = bf16_launches(ops, layers, A, args.fused_swiglu)
     ms = timed_step(torch, runs, args.steps, args.warmup)
     tflops = flop / (ms * 1e-3) / 1e12
     per, red_ms = timed_kernels(torch, ops, runs, args.steps)
@@ -355,7 +392,8 @@ def main():
     wbytes = 2 * 2 * FLOP_PER_ROW // 2
     abytes = 2 * M * (HIDDEN + NQ + HIDDEN + INTER)
     obytes = 2 * M * (NQ + 2 * NKV + HIDDEN + 2 * INTER + HIDDEN)
-    traffic_alg = (wbytes + abytes + obytes) / len(runs)
+    traffic_alg = (wbytes + abytes + obytes) * args.layers / len(runs)
+    _, _, _, wdesc = WORKLOADS[args.workload]
 
     result = {
         "metric": "MoT proj GEMM bf16 TFLOP/s + int8 TOPS at 4096 tok; % of MFMA peak",
@@ -364,8 +402,9 @@ def main():
         "ms_per_step": round(ms, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights, random init, on device)",
-        "config": {"workload": "BASELINE config 2: one MoT layer's 7 projections x 2 weight sets, "
-                               f"{args.m_und} und + {args.m_gen} gen tokens, two-group grouped GEMM",
+        "config": {"workload": f"{wdesc}, {args.m_und} und + {args.m_gen} gen "
+                               "tokens, two-group grouped GEMM",
+                   "name": args.workload, "layers": args.layers,
                    "m_und": args.m_und, "m_gen": args.m_gen, "hidden": HIDDEN,
                    "intermediate": INTER, "q_out": NQ, "kv_out": NKV,
                    "launches_per_step": len(runs),
@@ -382,14 +421,14 @@ def main():
                      "split_reduce_ms_per_step": round(red_ms / args.steps, 5)},
     }
     if want_i8:
-        runs8 = i8_launches(ops, L, A)
+        runs8 = i8_launches(ops, layers, A)
         ms8 = timed_step(torch, runs8, args.steps, args.warmup)
         tops = flop / (ms8 * 1e-3) / 1e12
         per8, red8 = timed_kernels(torch, ops, runs8, args.steps)
         g_ms = per8["gemm"][0] / per8["gemm"][1]
         g_tops = (flop / 4) / (g_ms * 1e-3) / 1e12
         q_ms = per8["quant"][0] / per8["quant"][1]
-        q_bytes = 3 * M * (HIDDEN + NQ + HIDDEN + INTER) / 4 + 4 * M
+        q_bytes = (3 * M * (HIDDEN + NQ + HIDDEN + INTER) + 4 * 4 * M) / 4
         result["int8"] = {
             "value": round(tops, 2), "unit": "TOPS",
             "pct_of_peak": round(100 * tops / PEAK_I8, 2),
