@@ -220,20 +220,20 @@ def test_i32_split_tail_bit_exact(ops):
     assert np.array_equal(out[Mu:].astype(np.int64).sum(axis=0), cs)
 
 
-def test_i32_ring_pipeline_bit_exact():
-    """The four-stage ring pipeline on the int8 path: exact accumulators,
-    split shares included."""
+def test_i32_per_item_launch_bit_exact():
+    """One workgroup per work item (U15H_PERSIST=0) on the int8 path: exact
+    accumulators, split shares included, equal to the persistent launch."""
     import os
-    old = os.environ.get("U15H_RING")
-    os.environ["U15H_RING"] = "1"
+    old = os.environ.get("U15H_PERSIST")
+    os.environ["U15H_PERSIST"] = "0"
     try:
         import u15h
-        ops_ring = u15h.Ops(0)
+        ops_pi = u15h.Ops(0)
     finally:
         if old is None:
-            del os.environ["U15H_RING"]
+            del os.environ["U15H_PERSIST"]
         else:
-            os.environ["U15H_RING"] = old
+            os.environ["U15H_PERSIST"] = old
     rng = np.random.default_rng(26)
     Mu, Mg, K, N = 37, 263, 12288, 264
     M = Mu + Mg
@@ -241,13 +241,13 @@ def test_i32_ring_pipeline_bit_exact():
     wu = rng.integers(-127, 128, (N, K), dtype=np.int8)
     wg = rng.integers(-127, 128, (N, K), dtype=np.int8)
     y = torch.empty(M, N, dtype=torch.int32, device="cuda")
-    ops_ring.mot_gemm_i8_i32(torch.from_numpy(xq).cuda(), Mu, Mg, K,
-                             [_proj(torch.from_numpy(wu).cuda(), None,
-                                    torch.from_numpy(wg).cuda(), None, y)])
+    ops_pi.mot_gemm_i8_i32(torch.from_numpy(xq).cuda(), Mu, Mg, K,
+                           [_proj(torch.from_numpy(wu).cuda(), None,
+                                  torch.from_numpy(wg).cuda(), None, y)])
     torch.cuda.synchronize()
     out = y.cpu().numpy()
     assert np.array_equal(out[:Mu], oracle.gemm_i8_i32(xq[:Mu], wu))
     rs, cs = oracle.i8_product_sums(xq[Mu:], wg)
     assert np.array_equal(out[Mu:].astype(np.int64).sum(axis=1), rs)
     assert np.array_equal(out[Mu:].astype(np.int64).sum(axis=0), cs)
-    ops_ring.close()
+    ops_pi.close()

@@ -59,7 +59,7 @@ struct GemmBatch {
 };
 
 // Workgroups a batch launches.
-inline int grid_blocks(const GemmBatch& b)
+__host__ __device__ inline int grid_blocks(const GemmBatch& b)
 {
   return b.split_begin + (b.total_tiles - b.split_begin) * b.split;
 }
@@ -70,13 +70,13 @@ inline size_t split_ws_bytes(const GemmBatch& b)
 }
 
 // Kernel launchers (u15h_kernels.hip).  All are asynchronous on `s`.
-// How the GEMM kernel is built: `waves` is the workgroup shape, 4 (one
+// How the GEMM kernel is launched: `waves` is the workgroup shape, 4 (one
 // wave per SIMD, 128x128 per wave) or 8 (two per SIMD, 128x64 per wave);
-// `ring` selects the four-stage LDS ring (64 bytes of K per stage) over the
-// two-stage pipeline (128 bytes).
+// `cus` > 0 caps the grid at that many workgroups (persistent: one per CU),
+// 0 launches one workgroup per work item.
 struct GemmShape {
   int waves;
-  bool ring;
+  int cus;
 };
 
 // `after_gemm`, when not null, is recorded on `s` right after the GEMM

@@ -39,6 +39,7 @@ namespace {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 typedef int i32x16_t __attribute__((ext_vector_type(16)));
 
 constexpr int kStage = (kBM + kBN) * kKB;   // 64 KiB per LDS stage
@@ -167,6 +168,16 @@ store_swiglu4(const GemmProblem& P, int m, int n, const float g[4],
                             n) = o;
 }
 
+// One 16-byte chunk of an output row, written non-temporally: the staged
+// epilogue writes whole 128-byte lines with such stores, so the output
+// bypasses allocation in L2 instead of evicting the activation and weight
+// rows that the tiles still running on the XCD stream through it.
+__device__ __forceinline__ void
+store_line16(void* p, const i32x4_t& v)
+{
+  __builtin_nontemporal_store(v, static_cast<i32x4_t*>(p));
+}
+
 // Which problem a linear tile index belongs to (uniform over the block).
 __device__ __forceinline__ int
 find_problem(const GemmBatch& B, int tile)
@@ -209,24 +220,21 @@ struct TileWork {
   int nst;      // K stages of this workgroup
 };
 
-// Whole tiles: consecutive workgroups are dealt round-robin to the 8 XCDs;
-// remap so each XCD walks a contiguous run of the tile list (and so shares
-// its operands in its own L2).  Split tiles follow, `split` consecutive
-// workgroups per tile, each a contiguous share of the `nk` K stages.
+// Work item w: whole tiles first, then the split tiles, `split`
+// consecutive items per tile, each a contiguous share of the `nk` K stages.
 template <Epi E>
 __device__ __forceinline__ TileWork
-tile_work(const GemmBatch& B, int nk)
+tile_work(const GemmBatch& B, int nk, int w)
 {
   TileWork t;
-  const int bid = blockIdx.x;
   const int SB = B.split_begin;
-  t.is_split = bid >= SB;
+  t.is_split = w >= SB;
   t.share = 0;
   if (!t.is_split) {
-    t.tile = (SB % 8 == 0) ? (bid % 8) * (SB / 8) + bid / 8 : bid;
+    t.tile = w;
   } else {
-    t.tile = SB + (bid - SB) / B.split;
-    t.share = (bid - SB) % B.split;
+    t.tile = SB + (w - SB) / B.split;
+    t.share = (w - SB) % B.split;
   }
   t.prob = find_problem(B, t.tile);
   tile_origin<E>(B.p[t.prob], t.tile, &t.row0, &t.col0);
@@ -270,6 +278,123 @@ interleave_loads_reads()
   }
 }
 
+// bf16 epilogue of a whole tile through LDS.  The MFMA layout gives each
+// lane 4 consecutive output columns of one row per store, so direct stores
+// write every 128-byte output line in 16-byte pieces from 8 instructions.
+// Instead each wave writes its bf16 results (bias, dequant or SwiGLU
+// applied) into a [256][TC] tile in the two stage buffers (rows 0..127 in
+// ring[0], 128..255 in ring[1]; the main loop is done with them), then the
+// tile is read back row-wise and 32 (or 16) lanes store one row's
+// 512 (256) contiguous bytes.  Row r's 16-byte chunk c sits at chunk
+// c ^ (r % CH) of its staged row, which spreads both the column writes (32
+// rows, one chunk) and the row reads over the bank groups.
+template <class Mma, Epi E, int WN>
+__device__ __forceinline__ void
+gemm_epilogue_staged(const GemmProblem& P, const TileWork& t, int wm, int wn,
+                     int lane, const typename Mma::acc_t (&acc)[kBN / WN / 32][4],
+                     char* const (&ring)[2])
+{
+  constexpr int NW = kBN / WN;
+  constexpr int FI = NW / 32;
+  constexpr int FJ = 4;
+  constexpr int TC = tile_cols(E);            // output columns per tile
+  constexpr int RB = TC * 2;                  // staged bytes per row
+  constexpr int CH = RB / 16;                 // 16-byte chunks per row
+  const int lr = lane & 31;
+  const int lh = lane >> 5;
+  // Every wave is past its last fragment read of the main loop.
+  __syncthreads();
+  char* const half = wm ? ring[1] : ring[0];
+  auto put = [&](int row, int col, uint32_t lo, uint32_t hi) {
+    // row within the half (0..127), col = first of 4 output columns
+    const int c = col >> 3;
+    char* p = half + row * RB + ((c ^ (row % CH)) << 4) + ((col & 7) << 1);
+    *reinterpret_cast<u32x2_t*>(p) = u32x2_t{lo, hi};
+  };
+#pragma unroll
+  for (int j = 0; j < FJ; ++j) {
+    const int row = j * 32 + lr;
+    const int m = t.row0 + wm * 128 + row;
+    if constexpr (E == Epi::kSwiglu) {
+#pragma unroll
+      for (int i = 0; i < FI / 2; ++i) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int col = wn * (NW / 2) + i * 32 + g * 8 + lh * 4;
+          put(row, col,
+              swiglu1(acc[i][j][g * 4 + 0], acc[i + FI / 2][j][g * 4 + 0]) |
+                  (swiglu1(acc[i][j][g * 4 + 1], acc[i + FI / 2][j][g * 4 + 1]) << 16),
+              swiglu1(acc[i][j][g * 4 + 2], acc[i + FI / 2][j][g * 4 + 2]) |
+                  (swiglu1(acc[i][j][g * 4 + 3], acc[i + FI / 2][j][g * 4 + 3]) << 16));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < FI; ++i) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int col = wn * NW + i * 32 + g * 8 + lh * 4;
+          const int n = t.col0 + col;
+          const auto& a = acc[i][j];
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if constexpr (E == Epi::kDequantBf16) {
+              v[e] = (float)bits_as<int>(a[g * 4 + e]);
+            } else {
+              v[e] = a[g * 4 + e];
+            }
+          }
+          // Columns and rows past the problem are staged but never stored;
+          // their scale and bias reads stay inside the problem.
+          if (n < P.n && m < P.rows) {
+            if constexpr (E == Epi::kDequantBf16) {
+              const float sam = P.sa[m];
+              const float4 swn = *reinterpret_cast<const float4*>(P.sw + n);
+              v[0] = (v[0] * sam) * swn.x;
+              v[1] = (v[1] * sam) * swn.y;
+              v[2] = (v[2] * sam) * swn.z;
+              v[3] = (v[3] * sam) * swn.w;
+            }
+            if (P.bias != nullptr) {
+              const uint2 bb = *reinterpret_cast<const uint2*>(P.bias + n);
+              v[0] += bf16_to_f32(bb.x & 0xffffu);
+              v[1] += bf16_to_f32(bb.x >> 16);
+              v[2] += bf16_to_f32(bb.y & 0xffffu);
+              v[3] += bf16_to_f32(bb.y >> 16);
+            }
+          }
+          put(row, col, bf16_bits(v[0]) | (bf16_bits(v[1]) << 16),
+              bf16_bits(v[2]) | (bf16_bits(v[3]) << 16));
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // Read back: wave w stores tile rows [RW w, RW w + RW) (RW = 256 / waves);
+  // 64 / CH rows per instruction, CH lanes per row.
+  constexpr int RW = kBM / (2 * WN);
+  const int wave = (int)(threadIdx.x >> 6);
+  constexpr int kRowsPerRead = 64 / CH;
+  const int first = wave * RW;                          // first tile row
+  const char* const src = first >= 128 ? ring[1] : ring[0];
+#pragma unroll
+  for (int r = 0; r < RW; r += kRowsPerRead) {
+    const int hrow = first % 128 + r + lane / CH;       // row within the half
+    const int trow = first + r + lane / CH;             // row within the tile
+    const int c = lane % CH;
+    const i32x4_t v = *reinterpret_cast<const i32x4_t*>(
+        src + hrow * RB + ((c ^ (hrow % CH)) << 4));
+    const int m = t.row0 + trow;
+    const int n = t.col0 + c * 8;
+    if (m < P.rows && n < P.n) {
+      store_line16(static_cast<uint16_t*>(P.y) + (size_t)m * P.ldy + n, v);
+    }
+  }
+  // The next tile's loads refill these buffers.
+  __syncthreads();
+}
+
 // Epilogue of a tile.  acc[i][j][r] holds tile column (weight row within
 // the tile) wn*NW + i*32 + (r>>2)*8 + lh*4 + (r&3) and tile row wm*128 +
 // j*32 + lr.  A K share writes its raw accumulators to the workspace
@@ -279,7 +404,8 @@ template <class Mma, Epi E, int WN>
 __device__ __forceinline__ void
 gemm_epilogue(const GemmBatch& B, const GemmProblem& P, const TileWork& t,
               int wm, int wn, int lane,
-              const typename Mma::acc_t (&acc)[kBN / WN / 32][4])
+              const typename Mma::acc_t (&acc)[kBN / WN / 32][4],
+              char* const (&ring)[2])
 {
   constexpr int NW = kBN / WN;
   constexpr int FI = NW / 32;
@@ -306,6 +432,10 @@ gemm_epilogue(const GemmBatch& B, const GemmProblem& P, const TileWork& t,
         }
       }
     }
+    return;
+  }
+  if constexpr (E != Epi::kI32) {
+    gemm_epilogue_staged<Mma, E, WN>(P, t, wm, wn, lane, acc, ring);
     return;
   }
 #pragma unroll
@@ -391,7 +521,7 @@ gemm_epilogue(const GemmBatch& B, const GemmProblem& P, const TileWork& t,
 // rows, rides in the SGPR.
 template <class Mma, Epi E, int WN, int KB, int RING>
 __device__ __forceinline__ void
-gemm_tile(const GemmBatch& B, char* const (&ring)[RING])
+gemm_tile(const GemmBatch& B, char* const (&ring)[RING], int item)
 {
   constexpr int kWaves = 2 * WN;
   constexpr int NW = kBN / WN;               // weight rows per wave
@@ -406,7 +536,7 @@ gemm_tile(const GemmBatch& B, char* const (&ring)[RING])
 
   const int kbytes = B.kbytes;
   const int nk = (kbytes + KB - 1) / KB;
-  const TileWork t = tile_work<E>(B, nk);
+  const TileWork t = tile_work<E>(B, nk, item);
   const GemmProblem& P = B.p[t.prob];
   constexpr int TC = tile_cols(E);
 
@@ -572,10 +702,17 @@ gemm_tile(const GemmBatch& B, char* const (&ring)[RING])
   // No load may still be writing LDS when the workgroup retires.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  gemm_epilogue<Mma, E, WN>(B, P, t, wm, wn, lane, acc);
+  gemm_epilogue<Mma, E, WN>(B, P, t, wm, wn, lane, acc, ring);
 }
 
 // Two 64 KiB stages of 128 bytes of K per row.
+//
+// Work items are dealt in rounds of gridDim.x: workgroup b takes item
+// round * gridDim.x + slot(b).  Launched with one workgroup per CU the
+// kernel is persistent; launched with one workgroup per item it is a single
+// round.  Workgroups b, b+8, ... run on XCD b % 8, and slot() gives each
+// XCD a contiguous run of the round's items, so the tiles that run
+// together on an XCD share operand rows in its L2.
 template <class Mma, Epi E, int WN>
 __global__ __launch_bounds__(128 * WN, 1) void
 mot_gemm_kernel(const GemmBatch B)
@@ -585,22 +722,15 @@ mot_gemm_kernel(const GemmBatch B)
   __shared__ __attribute__((aligned(1024))) char lds0[kStage];
   __shared__ __attribute__((aligned(1024))) char lds1[kStage];
   char* const ring[2] = {lds0, lds1};
-  gemm_tile<Mma, E, WN, kKB, 2>(B, ring);
-}
-
-// A ring of four 32 KiB stages of 64 bytes of K per row: loads have three
-// stages to land instead of one.
-template <class Mma, Epi E, int WN>
-__global__ __launch_bounds__(128 * WN, 1) void
-mot_gemm_ring_kernel(const GemmBatch B)
-{
-  constexpr int kRingStage = (kBM + kBN) * 64;
-  __shared__ __attribute__((aligned(1024))) char lds0[kRingStage];
-  __shared__ __attribute__((aligned(1024))) char lds1[kRingStage];
-  __shared__ __attribute__((aligned(1024))) char lds2[kRingStage];
-  __shared__ __attribute__((aligned(1024))) char lds3[kRingStage];
-  char* const ring[4] = {lds0, lds1, lds2, lds3};
-  gemm_tile<Mma, E, WN, 64, 4>(B, ring);
+  const int items = grid_blocks(B);
+  const int G = gridDim.x;
+  const int b = blockIdx.x;
+  const int slot = (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
+  for (int base = 0; base < items; base += G) {
+    const int w = base + slot;
+    if (w >= items) { break; }
+    gemm_tile<Mma, E, WN, kKB, 2>(B, ring, w);
+  }
 }
 
 // ---- split-K reduction --------------------------------------------------
@@ -878,16 +1008,13 @@ gather_rows_kernel(const uint16_t* __restrict__ src,
 
 template <class Mma, Epi E, int WN>
 hipError_t
-launch_gemm(const GemmBatch& b, bool ring, hipStream_t s, hipEvent_t after_gemm)
+launch_gemm(const GemmBatch& b, int cus, hipStream_t s, hipEvent_t after_gemm)
 {
   if (b.total_tiles <= 0) { return hipSuccess; }
-  if (ring) {
-    hipLaunchKernelGGL((mot_gemm_ring_kernel<Mma, E, WN>), dim3(grid_blocks(b)),
-                       dim3(128 * WN), 0, s, b);
-  } else {
-    hipLaunchKernelGGL((mot_gemm_kernel<Mma, E, WN>), dim3(grid_blocks(b)),
-                       dim3(128 * WN), 0, s, b);
-  }
+  const int items = grid_blocks(b);
+  const int grid = (cus > 0 && cus < items) ? cus : items;
+  hipLaunchKernelGGL((mot_gemm_kernel<Mma, E, WN>), dim3(grid), dim3(128 * WN),
+                     0, s, b);
   hipError_t e = hipGetLastError();
   if (e == hipSuccess && after_gemm != nullptr) {
     e = hipEventRecord(after_gemm, s);
@@ -905,8 +1032,8 @@ hipError_t
 launch_gemm_waves(const GemmBatch& b, const GemmShape& g, hipStream_t s,
                   hipEvent_t ev)
 {
-  return g.waves == 4 ? launch_gemm<Mma, E, 2>(b, g.ring, s, ev)
-                      : launch_gemm<Mma, E, 4>(b, g.ring, s, ev);
+  return g.waves == 4 ? launch_gemm<Mma, E, 2>(b, g.cus, s, ev)
+                      : launch_gemm<Mma, E, 4>(b, g.cus, s, ev);
 }
 
 }  // namespace
@@ -1031,10 +1158,6 @@ bool
 gemm_kernels_loadable()
 {
   const void* fns[] = {
-      reinterpret_cast<const void*>(&mot_gemm_ring_kernel<MmaBf16, Epi::kBf16, WN>),
-      reinterpret_cast<const void*>(&mot_gemm_ring_kernel<MmaBf16, Epi::kSwiglu, WN>),
-      reinterpret_cast<const void*>(&mot_gemm_ring_kernel<MmaI8, Epi::kI32, WN>),
-      reinterpret_cast<const void*>(&mot_gemm_ring_kernel<MmaI8, Epi::kDequantBf16, WN>),
       reinterpret_cast<const void*>(&mot_gemm_kernel<MmaBf16, Epi::kBf16, WN>),
       reinterpret_cast<const void*>(&mot_gemm_kernel<MmaBf16, Epi::kSwiglu, WN>),
       reinterpret_cast<const void*>(&mot_gemm_kernel<MmaI8, Epi::kI32, WN>),
