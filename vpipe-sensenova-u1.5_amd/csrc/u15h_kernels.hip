@@ -707,12 +707,12 @@ gemm_tile(const GemmBatch& B, char* const (&ring)[RING], int item)
 
 // Two 64 KiB stages of 128 bytes of K per row.
 //
-// Work items are dealt in rounds of gridDim.x: workgroup b takes item
-// round * gridDim.x + slot(b).  Launched with one workgroup per CU the
-// kernel is persistent; launched with one workgroup per item it is a single
-// round.  Workgroups b, b+8, ... run on XCD b % 8, and slot() gives each
-// XCD a contiguous run of the round's items, so the tiles that run
-// together on an XCD share operand rows in its L2.
+// Work items are dealt in rounds of gridDim.x.  Launched with one workgroup
+// per CU the kernel is persistent; launched with one workgroup per item it
+// is a single round.  Workgroups b, b+8, ... run on XCD b % 8; each round's
+// R items are cut into 8 contiguous runs of R/8, one per XCD, so the tiles
+// that run together on an XCD share operand rows in its L2 and a partial
+// last round still spreads over all eight XCDs.
 template <class Mma, Epi E, int WN>
 __global__ __launch_bounds__(128 * WN, 1) void
 mot_gemm_kernel(const GemmBatch B)
@@ -725,10 +725,17 @@ mot_gemm_kernel(const GemmBatch B)
   const int items = grid_blocks(B);
   const int G = gridDim.x;
   const int b = blockIdx.x;
-  const int slot = (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
   for (int base = 0; base < items; base += G) {
-    const int w = base + slot;
-    if (w >= items) { break; }
+    const int R = min(G, items - base);
+    int w = base + b;
+    if (G % 8 == 0) {
+      const int x = b % 8, i = b / 8;
+      const int lo = x * R / 8, hi = (x + 1) * R / 8;
+      if (i >= hi - lo) { break; }
+      w = base + lo + i;
+    } else if (b >= R) {
+      break;
+    }
     gemm_tile<Mma, E, WN, kKB, 2>(B, ring, w);
   }
 }
