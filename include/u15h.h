@@ -156,6 +156,56 @@ u15h_status u15h_f32_to_bf16(u15h_ctx* ctx, u15h_stream stream,
                              const float* src, int64_t n, u15h_bf16* dst);
 
 /* ------------------------------------------------------------------ */
+/* The step after the q/k projections: split norm and split RoPE       */
+/* ------------------------------------------------------------------ */
+
+/* Replaces MetalOps::split_qk_norm(enc, x, w_t, w_hw, heads, tokens,
+ * head_dim, eps) (src/u15-metal-ops.h:169-173, .cc:508-524;
+ * kernel u15_split_qk_norm, src/u15-kernels.metal:50-90).  x [tokens]
+ * [heads*head_dim] bf16 in place; per (token, head) the halves [0, D/2)
+ * and [D/2, D) are normalised separately:
+ *   y = x * rsqrt(mean(half^2) + eps) * w   (w_t / w_hw bf16 [D/2], f32)
+ * head_dim even, <= 512. */
+u15h_status u15h_split_qk_norm(u15h_ctx* ctx, u15h_stream stream,
+                               u15h_bf16* x, const u15h_bf16* w_t,
+                               const u15h_bf16* w_hw, int heads, int tokens,
+                               int head_dim, float eps);
+
+/* Replaces MetalOps::split_rope(enc, x, cos, sin, heads, tokens, head_dim,
+ * d_t, d_h) (src/u15-metal-ops.h:177-181, .cc:526-545; kernel
+ * u15_split_rope, src/u15-kernels.metal:92-157): rotate_half on the ranges
+ * [0,d_t) t, [d_t,d_t+d_h) h, [d_t+d_h,head_dim) w of every head, with the
+ * f32 tables cos/sin [tokens][head_dim] from u15h_build_rope_tables (device
+ * memory).  d_t + 2*d_h == head_dim, both even. */
+u15h_status u15h_split_rope(u15h_ctx* ctx, u15h_stream stream, u15h_bf16* x,
+                            const float* cos_tab, const float* sin_tab,
+                            int heads, int tokens, int head_dim, int d_t,
+                            int d_h);
+
+/* Both in one pass over x (no reference counterpart; the backbone issues
+ * them back to back, src/u15-backbone.cc:203-206): the normalised row
+ * stays in f32 between the norm and the rotation. */
+u15h_status u15h_split_qk_norm_rope(u15h_ctx* ctx, u15h_stream stream,
+                                    u15h_bf16* x, const u15h_bf16* w_t,
+                                    const u15h_bf16* w_hw,
+                                    const float* cos_tab,
+                                    const float* sin_tab, int heads,
+                                    int tokens, int head_dim, int d_t,
+                                    int d_h, float eps);
+
+/* Replaces MetalOps::build_rope_tables(pos_t, pos_h, pos_w, head_dim, d_t,
+ * d_h, theta_t, theta_hw) (src/u15-metal-ops.h:186-195, .cc:547-600).  HOST
+ * function, no context: fills host arrays cos_tab/sin_tab [tokens]
+ * [head_dim]; per range the ladder 1/theta^(2i/width) and the angle
+ * pos*inv are formed in double and narrowed once, each range's second half
+ * repeating its first.  The caller copies the tables to the device. */
+u15h_status u15h_build_rope_tables(const int32_t* pos_t, const int32_t* pos_h,
+                                   const int32_t* pos_w, int tokens,
+                                   int head_dim, int d_t, int d_h,
+                                   double theta_t, double theta_hw,
+                                   float* cos_tab, float* sin_tab);
+
+/* ------------------------------------------------------------------ */
 /* SwiGLU                                                              */
 /* ------------------------------------------------------------------ */
 

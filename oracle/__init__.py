@@ -61,6 +61,17 @@ def lib() -> ctypes.CDLL:
             "u15o_dequant_affine": [vp, vp, vp, ctypes.c_int, ctypes.c_int, sz, sz, vp],
             "u15o_pack_affine": [vp, ctypes.c_int, ctypes.c_int, sz, sz, vp, vp, vp, vp],
             "u15o_bias_add_bf16": [vp, vp, sz, sz],
+            "u15o_rms_norm": [vp, vp, ctypes.c_float, sz, sz, vp],
+            "u15o_rope_inv_freq": [ctypes.c_int, ctypes.c_double, vp],
+            "u15o_rope_half": [vp, vp, ctypes.c_int, ctypes.c_double],
+            "u15o_rope_tables": [vp, vp, vp, sz, ctypes.c_int, ctypes.c_int,
+                                 ctypes.c_int, ctypes.c_double, ctypes.c_double,
+                                 vp, vp],
+            "u15o_split_qk_norm_rope": [vp, vp, vp, vp, vp, vp, sz, sz,
+                                        ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_double, ctypes.c_double,
+                                        ctypes.c_float, ctypes.c_int,
+                                        ctypes.c_int],
         }.items():
             getattr(L, n).restype = None
             getattr(L, n).argtypes = a
@@ -83,6 +94,17 @@ def ref_lib():
         R.u15ref_linear.argtypes = [vp, vp, vp, sz, sz, sz, vp]
         R.u15ref_silu.restype = None
         R.u15ref_silu.argtypes = [vp, sz]
+        for n, a in {
+            "u15ref_rms_norm": [vp, vp, ctypes.c_float, sz, sz, vp],
+            "u15ref_rope_inv_freq": [ctypes.c_int, ctypes.c_double, vp],
+            "u15ref_rope_half": [vp, vp, ctypes.c_int, ctypes.c_double],
+            "u15ref_split_rope_project": [vp, vp, vp, vp, vp, vp, vp, sz, sz,
+                                          ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_double, ctypes.c_double,
+                                          ctypes.c_double, vp],
+        }.items():
+            getattr(R, n).restype = None
+            getattr(R, n).argtypes = a
         _ref = R
     return _ref
 
@@ -255,6 +277,112 @@ def bias_add_bf16(y_bits, b_bits):
     b, pb = _c(b_bits, np.uint16)
     lib().u15o_bias_add_bf16(y.ctypes.data, pb, y.shape[0], y.shape[1])
     return y
+
+
+# ---- split q/k norm + three-way RoPE ---------------------------------------------
+def rms_norm(x, w, eps=1e-6):
+    x, px = _c(x, np.float32)
+    w, pw = _c(w, np.float32)
+    rows, dim = x.shape
+    out = np.empty_like(x)
+    lib().u15o_rms_norm(px, pw, eps, rows, dim, out.ctypes.data)
+    return out
+
+
+def rope_inv_freq(dim, theta):
+    out = np.empty(dim // 2, np.float32)
+    lib().u15o_rope_inv_freq(dim, theta, out.ctypes.data)
+    return out
+
+
+def rope_half(x, inv, dim, pos):
+    x = np.array(x, dtype=np.float32, copy=True)
+    inv, pi = _c(inv, np.float32)
+    lib().u15o_rope_half(x.ctypes.data, pi, dim, float(pos))
+    return x
+
+
+def rope_tables(pos_t, pos_h, pos_w, D, d_t, d_h, theta_t=5e6, theta_hw=1e4):
+    pt, a = _c(pos_t, np.int32)
+    ph, b = _c(pos_h, np.int32)
+    pw, c = _c(pos_w, np.int32)
+    T = pt.size
+    cs = np.empty((T, D), np.float32)
+    sn = np.empty((T, D), np.float32)
+    lib().u15o_rope_tables(a, b, c, T, D, d_t, d_h, theta_t, theta_hw,
+                           cs.ctypes.data, sn.ctypes.data)
+    return cs, sn
+
+
+def split_qk_norm_rope(x, w_t, w_hw, pos_t, pos_h, pos_w, H, D, d_t, d_h,
+                       theta_t=5e6, theta_hw=1e4, eps=1e-6, norm=True,
+                       rope=True):
+    """x [T][H*D] f32 (returned as a new array)."""
+    x = np.array(x, dtype=np.float32, copy=True)
+    T = x.shape[0]
+    wt, pwt = _c(w_t, np.float32)
+    wh, pwh = _c(w_hw, np.float32)
+    pt, a = _c(pos_t, np.int32)
+    ph, b = _c(pos_h, np.int32)
+    pw, c = _c(pos_w, np.int32)
+    lib().u15o_split_qk_norm_rope(x.ctypes.data, pwt, pwh, a, b, c, T, H, D,
+                                  d_t, d_h, theta_t, theta_hw, eps,
+                                  int(norm), int(rope))
+    return x
+
+
+def ref_rms_norm(x, w, eps=1e-6):
+    R = ref_lib()
+    if R is None:
+        return None
+    x, px = _c(x, np.float32)
+    w, pw = _c(w, np.float32)
+    rows, dim = x.shape
+    out = np.empty_like(x)
+    R.u15ref_rms_norm(px, pw, eps, rows, dim, out.ctypes.data)
+    return out
+
+
+def ref_rope_inv_freq(dim, theta):
+    R = ref_lib()
+    if R is None:
+        return None
+    out = np.empty(dim // 2, np.float32)
+    R.u15ref_rope_inv_freq(dim, theta, out.ctypes.data)
+    return out
+
+
+def ref_rope_half(x, inv, dim, pos):
+    R = ref_lib()
+    if R is None:
+        return None
+    x = np.array(x, dtype=np.float32, copy=True)
+    inv, pi = _c(inv, np.float32)
+    R.u15ref_rope_half(x.ctypes.data, pi, dim, float(pos))
+    return x
+
+
+def ref_split_rope_project(x, w_proj, w_norm, w_norm_hw, pos_t, pos_h, pos_w,
+                           heads, head_dim, theta_t=5e6, theta_hw=1e4,
+                           eps=1e-6):
+    """The reference's projection + split norm + split RoPE; head-major
+    [heads][tokens][head_dim] out."""
+    R = ref_lib()
+    if R is None:
+        return None
+    x, px = _c(x, np.float32)
+    w_proj, pwp = _c(w_proj, np.float32)
+    w_norm, pwn = _c(w_norm, np.float32)
+    w_norm_hw, pwh = _c(w_norm_hw, np.float32)
+    pt, a = _c(pos_t, np.int32)
+    ph, b = _c(pos_h, np.int32)
+    pw, c = _c(pos_w, np.int32)
+    T, hidden = x.shape
+    out = np.empty((heads, T, head_dim), np.float32)
+    R.u15ref_split_rope_project(px, pwp, pwn, pwh, a, b, c, T, hidden, heads,
+                                head_dim, theta_t, theta_hw, eps,
+                                out.ctypes.data)
+    return out
 
 
 # ---- metrics / generator ------------------------------------------------------

@@ -5,6 +5,8 @@
 // names so the oracle tests can call them through ctypes:
 //   u15ref_linear -> u15::ref::linear   (src/u15-ref.h:33-36, u15-ref.cc:33-49)
 //   u15ref_silu   -> u15::ref::silu     (src/u15-ref.h:38, u15-ref.cc:51-58)
+//   u15ref_rms_norm, u15ref_rope_inv_freq, u15ref_rope_half,
+//   u15ref_split_rope_project -> the RoPE/norm helpers (src/u15-ref.h:25-95)
 #include "u15-ref.h"
 
 extern "C" void
@@ -19,4 +21,46 @@ extern "C" void
 u15ref_silu(float* x, std::size_t n)
 {
   u15::ref::silu(x, n);
+}
+
+extern "C" void
+u15ref_rms_norm(const float* x, const float* w, float eps, std::size_t rows,
+                std::size_t dim, float* out)
+{
+  u15::ref::rms_norm(x, w, eps, rows, dim, out);
+}
+
+extern "C" void
+u15ref_rope_inv_freq(int dim, double theta, float* out)
+{
+  const std::vector<float> f = u15::ref::rope_inv_freq(dim, theta);
+  for (std::size_t i = 0; i < f.size(); ++i) { out[i] = f[i]; }
+}
+
+extern "C" void
+u15ref_rope_half(float* x, const float* inv, int dim, double pos)
+{
+  const std::vector<float> f(inv, inv + dim / 2);
+  u15::ref::rope_half_inplace(x, f, dim, pos);
+}
+
+extern "C" void
+u15ref_split_rope_project(const float* x, const float* w_proj,
+                          const float* w_norm, const float* w_norm_hw,
+                          const int* pos_t, const int* pos_h,
+                          const int* pos_w, std::size_t tokens,
+                          std::size_t hidden, int heads, int head_dim,
+                          double theta_t, double theta_hw, double eps,
+                          float* out)
+{
+  u15::ref::SplitRopeParams p;
+  p.heads = heads;
+  p.head_dim = head_dim;
+  p.theta_t = theta_t;
+  p.theta_hw = theta_hw;
+  p.rms_eps = eps;
+  const std::vector<int> t(pos_t, pos_t + tokens), h(pos_h, pos_h + tokens),
+      w(pos_w, pos_w + tokens);
+  u15::ref::split_rope_project(x, w_proj, w_norm, w_norm_hw, t, h, w, tokens,
+                               hidden, p, out);
 }

@@ -25,6 +25,21 @@
  *   u15o_gemm_i8_i32      brute-force Python integer sums; the exact
  *                         row/column-sum identity; +-127 extremes.
  *   u15o_dequant_*        float32 numpy evaluation of the same expression.
+ *   u15o_rms_norm, u15o_rope_inv_freq, u15o_rope_half
+ *                         bit-equal to the compiled reference's
+ *                         u15::ref::rms_norm / rope_inv_freq /
+ *                         rope_half_inplace on random inputs.
+ *   u15o_rope_tables      closed forms (position 0: cos 1, sin 0; the
+ *                         first pair of every range has frequency 1),
+ *                         the doubled halves, and ref::rope_half on the
+ *                         table's angles.
+ *   u15o_split_qk_norm_rope
+ *                         its projection composition equals the compiled
+ *                         reference's split_rope_project (u15-ref.cc:
+ *                         121-175) after re-layout; the reference test's
+ *                         negative controls (h/w swapped, one whole-head
+ *                         norm) differ by > 1e-2; rotation preserves each
+ *                         pair's norm.
  */
 #include "u15_oracle.h"
 
@@ -307,6 +322,119 @@ u15o_bias_add_bf16(uint16_t* y, const uint16_t* b, size_t rows, size_t N)
     for (size_t n = 0; n < N; ++n) {
       const float v = u15o_bf16_to_f32(y[r * N + n]) + u15o_bf16_to_f32(b[n]);
       y[r * N + n] = u15o_f32_to_bf16(v);
+    }
+  }
+}
+
+/* ---- the step after the q/k projections: split norm + split RoPE ---- */
+
+void
+u15o_rms_norm(const float* x, const float* w, float eps, size_t rows,
+              size_t dim, float* out)
+{
+  /* src/u15-ref.cc:12-31: double sum of squares, double inverse root,
+   * each output x * inv * w narrowed once. */
+  for (size_t r = 0; r < rows; ++r) {
+    const float* xr = x + r * dim;
+    float* o = out + r * dim;
+    double acc = 0.0;
+    for (size_t c = 0; c < dim; ++c) { acc += (double)xr[c] * xr[c]; }
+    const double inv = 1.0 / sqrt(acc / (double)dim + (double)eps);
+    for (size_t c = 0; c < dim; ++c) {
+      o[c] = (float)((double)xr[c] * inv * (double)w[c]);
+    }
+  }
+}
+
+void
+u15o_rope_inv_freq(int dim, double theta, float* inv)
+{
+  /* src/u15-ref.cc:77-86: inv[i] = 1 / theta^(2i/dim), narrowed to f32. */
+  for (int i = 0; i < dim / 2; ++i) {
+    inv[i] = (float)(1.0 / pow(theta, (double)(2 * i) / (double)dim));
+  }
+}
+
+void
+u15o_rope_half(float* x, const float* inv, int dim, double pos)
+{
+  /* src/u15-ref.cc:88-101: rotate_half over dim/2 pairs (j, j + dim/2),
+   * the angle and the rotation in double. */
+  const int half = dim / 2;
+  for (int j = 0; j < half; ++j) {
+    const double ang = pos * (double)inv[j];
+    const double c = cos(ang), s = sin(ang);
+    const double a = (double)x[j], b = (double)x[j + half];
+    x[j] = (float)(a * c - b * s);
+    x[j + half] = (float)(b * c + a * s);
+  }
+}
+
+void
+u15o_rope_tables(const int32_t* pos_t, const int32_t* pos_h,
+                 const int32_t* pos_w, size_t T, int D, int d_t, int d_h,
+                 double theta_t, double theta_hw, float* cosf, float* sinf)
+{
+  /* src/u15-metal-ops.cc:547-600 (build_rope_tables): per token, the three
+   * ranges [0,d_t) t, [d_t,d_t+d_h) h, [d_t+d_h,D) w, each filled with its
+   * own ladder inv = 1/theta^(2i/width) formed in double, the angle
+   * pos*inv in double, cos/sin narrowed once, doubled cat(f, f) across the
+   * range's two halves. */
+  const int off[3] = {0, d_t, d_t + d_h};
+  const int width[3] = {d_t, d_h, d_h};
+  const double theta[3] = {theta_t, theta_hw, theta_hw};
+  const int32_t* pos[3] = {pos_t, pos_h, pos_w};
+  for (int r = 0; r < 3; ++r) {
+    const int half = width[r] / 2;
+    for (size_t t = 0; t < T; ++t) {
+      for (int i = 0; i < half; ++i) {
+        const double inv =
+            1.0 / pow(theta[r], (double)(2 * i) / (double)width[r]);
+        const double a = (double)pos[r][t] * inv;
+        const float cv = (float)cos(a), sv = (float)sin(a);
+        const size_t b = t * (size_t)D + (size_t)off[r];
+        cosf[b + i] = cv;
+        sinf[b + i] = sv;
+        cosf[b + i + half] = cv;
+        sinf[b + i + half] = sv;
+      }
+    }
+  }
+}
+
+void
+u15o_split_qk_norm_rope(float* x, const float* w_t, const float* w_hw,
+                        const int32_t* pos_t, const int32_t* pos_h,
+                        const int32_t* pos_w, size_t T, size_t H, int D,
+                        int d_t, int d_h, double theta_t, double theta_hw,
+                        float eps, int do_norm, int do_rope)
+{
+  /* The reference test's CPU path (tests/u15-kernels-test.cc:156-181),
+   * the same two steps split_qk_norm and split_rope take: on each
+   * (token, head) row of x [T][H*D], rms_norm of the two halves
+   * [0, D/2) and [D/2, D) with their own weights, then rotate_half on the
+   * three ranges with ladders 1/theta_t^(2i/d_t) and 1/theta_hw^(2i/d_h)
+   * (u15-ref.cc:121-175 uses the same split). */
+  const int half = D / 2;
+  float inv_t[256], inv_h[256], a[512], na[512];
+  u15o_rope_inv_freq(d_t, theta_t, inv_t);
+  u15o_rope_inv_freq(d_h, theta_hw, inv_h);
+  for (size_t t = 0; t < T; ++t) {
+    for (size_t h = 0; h < H; ++h) {
+      float* row = x + (t * H + h) * (size_t)D;
+      if (do_norm) {
+        for (int c = 0; c < half; ++c) { a[c] = row[c]; }
+        u15o_rms_norm(a, w_t, eps, 1, (size_t)half, na);
+        for (int c = 0; c < half; ++c) { row[c] = na[c]; }
+        for (int c = 0; c < half; ++c) { a[c] = row[half + c]; }
+        u15o_rms_norm(a, w_hw, eps, 1, (size_t)half, na);
+        for (int c = 0; c < half; ++c) { row[half + c] = na[c]; }
+      }
+      if (do_rope) {
+        u15o_rope_half(row, inv_t, d_t, (double)pos_t[t]);
+        u15o_rope_half(row + d_t, inv_h, d_h, (double)pos_h[t]);
+        u15o_rope_half(row + d_t + d_h, inv_h, d_h, (double)pos_w[t]);
+      }
     }
   }
 }

@@ -110,6 +110,29 @@ void u15o_pack_affine(const float* w, int bits, int group, size_t N, size_t K,
  * (u15-metal-ops.cc:435-446). */
 void u15o_bias_add_bf16(uint16_t* y, const uint16_t* b, size_t rows, size_t N);
 
+/* The step after the q/k projections (src/u15-ref.h:25-95):
+ *   rms_norm      y = x * 1/sqrt(mean(x^2) + eps) * w, double arithmetic
+ *   rope_inv_freq inv[i] = 1/theta^(2i/dim), i < dim/2
+ *   rope_half     rotate_half on pairs (j, j + dim/2) at one position
+ *   rope_tables   the packed [T][D] f32 cos/sin of build_rope_tables
+ *                 (src/u15-metal-ops.cc:547-600)
+ *   split_qk_norm_rope  on x [T][H*D] in place: the two half norms, then
+ *                 the three-way rope [t | h | w] (D/2, D/4, D/4). */
+void u15o_rms_norm(const float* x, const float* w, float eps, size_t rows,
+                   size_t dim, float* out);
+void u15o_rope_inv_freq(int dim, double theta, float* inv);
+void u15o_rope_half(float* x, const float* inv, int dim, double pos);
+void u15o_rope_tables(const int32_t* pos_t, const int32_t* pos_h,
+                      const int32_t* pos_w, size_t T, int D, int d_t, int d_h,
+                      double theta_t, double theta_hw, float* cosf,
+                      float* sinf);
+void u15o_split_qk_norm_rope(float* x, const float* w_t, const float* w_hw,
+                             const int32_t* pos_t, const int32_t* pos_h,
+                             const int32_t* pos_w, size_t T, size_t H, int D,
+                             int d_t, int d_h, double theta_t,
+                             double theta_hw, float eps, int do_norm,
+                             int do_rope);
+
 /* rel-L2 = sqrt(sum (a-b)^2 / sum b^2), tests/u15-kernels-test.cc:95-105;
  * max-rel = max|a-b| / max|b|. */
 double u15o_rel_l2(const float* a, const float* b, size_t n);

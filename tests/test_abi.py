@@ -60,3 +60,22 @@ def test_route_rows_edge_cases():
     assert (list(perm), mu, mg) == ([0, 1, 2], 0, 3)
     with pytest.raises(u15h.U15hError):
         u15h.route_rows([0, 2])
+
+
+def test_build_rope_tables_matches_oracle():
+    """u15h_build_rope_tables is host code (no device): bit-equal to the
+    oracle's restatement of build_rope_tables, including long positions."""
+    import numpy as np
+    import oracle
+    rng = np.random.default_rng(4)
+    T, D = 50, 128
+    pt = rng.integers(0, 20000, T)
+    ph = rng.integers(0, 64, T)
+    pw = rng.integers(0, 64, T)
+    c, s = u15h.build_rope_tables(pt, ph, pw, D, 64, 32)
+    oc, osn = oracle.rope_tables(pt, ph, pw, D, 64, 32)
+    assert np.array_equal(c, oc) and np.array_equal(s, osn)
+    with pytest.raises(u15h.U15hError):
+        u15h.build_rope_tables(pt, ph, pw, D, 64, 30)   # 64 + 60 != 128
+    c0, s0 = u15h.build_rope_tables([], [], [], D, 64, 32)
+    assert c0.shape == (0, D)

@@ -376,3 +376,130 @@ def test_bias_add_matches_f32_add_then_rne():
     assert np.array_equal(oracle.bias_add_bf16(y, np.zeros(64, np.uint16)), y)
     z = oracle.bias_add_bf16(np.tile(b ^ 0x8000, (2, 1)), b)
     assert np.all(oracle.bf16_to_f32(z) == 0)
+
+
+# ---- split q/k norm + three-way RoPE ------------------------------------------
+def _ref_test_case():
+    """test_split_head's inputs (tests/u15-kernels-test.cc:124-153):
+    H=4, T=12, D=32, x = randn(seed 7), w_t, w_hw ~ N(1, 0.2) from seed 8,
+    positions: 5 text tokens then an image block (t = 5, h = i/7, w = i%7)."""
+    H, T, D = 4, 12, 32
+    x = oracle.randn_mt(7, T * H * D).reshape(T, H * D)
+    w = oracle.randn_mt(8, D, 0.2) + np.float32(1.0)
+    w_t, w_hw = w[: D // 2], w[D // 2:]
+    pt = [i for i in range(5)] + [5] * (T - 5)
+    ph = [0] * 5 + [i // 7 for i in range(T - 5)]
+    pw = [0] * 5 + [i % 7 for i in range(T - 5)]
+    return H, T, D, x, w_t, w_hw, np.array(pt), np.array(ph), np.array(pw)
+
+
+@pytest.mark.skipif(not REF, reason="reference CPU path not built")
+def test_norm_and_rope_pieces_equal_reference():
+    rng = np.random.default_rng(3)
+    for dim in (16, 32, 64, 128):
+        x = rng.standard_normal((7, dim)).astype(np.float32) * 3
+        w = rng.normal(1, 0.2, dim).astype(np.float32)
+        assert np.array_equal(oracle.rms_norm(x, w, 1e-6),
+                              oracle.ref_rms_norm(x, w, 1e-6))
+        for theta in (1e4, 5e6):
+            inv = oracle.rope_inv_freq(dim, theta)
+            assert np.array_equal(inv, oracle.ref_rope_inv_freq(dim, theta))
+            for pos in (0, 1, 37, 4095, 100000):
+                assert np.array_equal(oracle.rope_half(x[0], inv, dim, pos),
+                                      oracle.ref_rope_half(x[0], inv, dim, pos))
+
+
+@pytest.mark.skipif(not REF, reason="reference CPU path not built")
+def test_split_composition_equals_reference_split_rope_project():
+    """u15::ref::split_rope_project (u15-ref.cc:121-175): projection, the two
+    half norms, the three-way rope, emitted head-major.  The oracle's
+    linear + split_qk_norm_rope, re-laid out, is bit-equal."""
+    T, hidden, H, D = 9, 64, 3, 32
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((T, hidden)).astype(np.float32)
+    wp = (rng.standard_normal((H * D, hidden)) * 0.1).astype(np.float32)
+    wn = rng.normal(1, 0.2, D // 2).astype(np.float32)
+    wh = rng.normal(1, 0.2, D // 2).astype(np.float32)
+    pt, ph, pw = np.arange(T), np.arange(T) % 3, np.arange(T) // 3
+    ref = oracle.ref_split_rope_project(x, wp, wn, wh, pt, ph, pw, H, D)
+    proj = oracle.linear(x, wp)
+    ours = oracle.split_qk_norm_rope(proj, wn, wh, pt, ph, pw, H, D, D // 2,
+                                     D // 4)
+    ours = ours.reshape(T, H, D).transpose(1, 0, 2)
+    assert np.array_equal(ours, ref)
+
+
+def test_split_head_negative_controls():
+    """The reference test's two controls (tests/u15-kernels-test.cc:
+    208-257): h and w exchanged, and one whole-head norm instead of two
+    half norms, must both be more than 1e-2 away."""
+    H, T, D, x, w_t, w_hw, pt, ph, pw = _ref_test_case()
+    d_t, d_h = D // 2, D // 4
+    ref = oracle.split_qk_norm_rope(x, w_t, w_hw, pt, ph, pw, H, D, d_t, d_h)
+    swapped = oracle.split_qk_norm_rope(x, w_t, w_hw, pt, pw, ph, H, D, d_t, d_h)
+    assert oracle.rel_l2(swapped, ref) > 1e-2
+    whole = oracle.rms_norm(x.reshape(T * H, D),
+                            np.concatenate([w_t, w_hw]), 1e-6).reshape(T, H * D)
+    whole = oracle.split_qk_norm_rope(whole, w_t, w_hw, pt, ph, pw, H, D, d_t,
+                                      d_h, norm=False)
+    assert oracle.rel_l2(whole, ref) > 1e-2
+
+
+def test_rope_rotation_closed_forms():
+    H, T, D, x, w_t, w_hw, pt, ph, pw = _ref_test_case()
+    d_t, d_h = D // 2, D // 4
+    normed = oracle.split_qk_norm_rope(x, w_t, w_hw, pt, ph, pw, H, D, d_t,
+                                       d_h, rope=False)
+    roped = oracle.split_qk_norm_rope(x, w_t, w_hw, pt, ph, pw, H, D, d_t, d_h)
+    n3 = normed.reshape(T, H, D).astype(np.float64)
+    r3 = roped.reshape(T, H, D).astype(np.float64)
+    # each rotated pair keeps its length
+    for off, width in ((0, d_t), (d_t, d_h), (d_t + d_h, d_h)):
+        h = width // 2
+        a = n3[..., off:off + h] ** 2 + n3[..., off + h:off + width] ** 2
+        b = r3[..., off:off + h] ** 2 + r3[..., off + h:off + width] ** 2
+        assert np.allclose(a, b, rtol=1e-5, atol=1e-6)
+    # all positions 0: the rotation is the identity
+    z = np.zeros(T, np.int32)
+    r0 = oracle.split_qk_norm_rope(x, w_t, w_hw, z, z, z, H, D, d_t, d_h)
+    assert np.array_equal(r0, normed)
+    # the half norms: unit weights give each half a mean square of 1
+    ones = np.ones(D // 2, np.float32)
+    u = oracle.split_qk_norm_rope(x, ones, ones, pt, ph, pw, H, D, d_t, d_h,
+                                  rope=False).reshape(T * H, D).astype(np.float64)
+    assert np.allclose((u[:, : D // 2] ** 2).mean(1), 1, rtol=1e-5)
+    assert np.allclose((u[:, D // 2:] ** 2).mean(1), 1, rtol=1e-5)
+
+
+def test_rope_tables_closed_forms():
+    T, D, d_t, d_h = 6, 32, 16, 8
+    pt = np.array([0, 1, 2, 3, 4, 1000])
+    ph = np.array([0, 5, 0, 7, 1, 2])
+    pw = np.array([0, 0, 9, 1, 3, 4])
+    cs, sn = oracle.rope_tables(pt, ph, pw, D, d_t, d_h)
+    assert np.all(cs[0] == 1) and np.all(sn[0] == 0)
+    for off, w, p in ((0, d_t, pt), (d_t, d_h, ph), (d_t + d_h, d_h, pw)):
+        h = w // 2
+        assert np.array_equal(cs[:, off:off + h], cs[:, off + h:off + w])
+        assert np.array_equal(sn[:, off:off + h], sn[:, off + h:off + w])
+        # the first pair of every range has frequency 1: angle = position
+        assert np.array_equal(cs[:, off], np.cos(p.astype(np.float64)).astype(np.float32))
+        assert np.array_equal(sn[:, off], np.sin(p.astype(np.float64)).astype(np.float32))
+    # rotating with the tables equals rotate_half with the ladders (f32
+    # tables against double angles: within a few f32 ulps)
+    x = oracle.randn_mt(5, D)
+    got = np.empty(D, np.float64)
+    for off, w in ((0, d_t), (d_t, d_h), (d_t + d_h, d_h)):
+        h = w // 2
+        for j in range(h):
+            i = off + j
+            a, b = float(x[i]), float(x[i + h])
+            got[i] = a * cs[3, i] - b * sn[3, i]
+            got[i + h] = b * cs[3, i + h] + a * sn[3, i + h]
+    want = x.copy()
+    want[:d_t] = oracle.rope_half(want[:d_t], oracle.rope_inv_freq(d_t, 5e6), d_t, 3)
+    want[d_t:d_t + d_h] = oracle.rope_half(want[d_t:d_t + d_h],
+                                           oracle.rope_inv_freq(d_h, 1e4), d_h, 7)
+    want[d_t + d_h:] = oracle.rope_half(want[d_t + d_h:],
+                                        oracle.rope_inv_freq(d_h, 1e4), d_h, 1)
+    assert np.allclose(got, want, rtol=1e-6, atol=1e-6)

@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <cmath>
 #include <cstdlib>
 #include <cstring>
 #include <string>
@@ -815,6 +816,126 @@ u15h_f32_to_bf16(u15h_ctx* ctx, u15h_stream stream, const float* src,
   return launched(ctx,
                   u15h::launch_f32_to_bf16(src, n, dst, as_stream(stream)),
                   "f32_to_bf16");
+}
+
+static u15h_status
+check_head(u15h_ctx* ctx, int heads, int tokens, int head_dim, int d_t,
+           int d_h)
+{
+  if (heads <= 0 || tokens < 0 || head_dim <= 0 || head_dim % 2 != 0 ||
+      head_dim > 512) {
+    return fail(ctx, U15H_EINVAL, "heads=%d tokens=%d head_dim=%d", heads,
+                tokens, head_dim);
+  }
+  if (d_t <= 0 || d_h <= 0 || d_t % 2 != 0 || d_h % 2 != 0 ||
+      d_t + 2 * d_h != head_dim) {
+    return fail(ctx, U15H_EINVAL, "ranges d_t=%d d_h=%d do not split %d as "
+                "[t | h | w] with even widths", d_t, d_h, head_dim);
+  }
+  if ((long long)heads * tokens > (1LL << 30)) {
+    return fail(ctx, U15H_EINVAL, "heads x tokens too large");
+  }
+  return U15H_OK;
+}
+
+static u15h_status
+norm_rope(u15h_ctx* ctx, u15h_stream stream, u15h_bf16* x,
+          const u15h_bf16* w_t, const u15h_bf16* w_hw, const float* cosf,
+          const float* sinf, int heads, int tokens, int head_dim, int d_t,
+          int d_h, float eps, bool norm, bool rope, const char* what)
+{
+  if (ctx == nullptr) { return U15H_EINVAL; }
+  u15h_status st = check_head(ctx, heads, tokens, head_dim, d_t, d_h);
+  if (st != U15H_OK) { return st; }
+  if (tokens == 0) { ctx->err.clear(); return U15H_OK; }
+  if (x == nullptr || (norm && (w_t == nullptr || w_hw == nullptr)) ||
+      (rope && (cosf == nullptr || sinf == nullptr))) {
+    return fail(ctx, U15H_EINVAL, "%s: null operand", what);
+  }
+  if (norm && !(eps >= 0.0f)) {
+    return fail(ctx, U15H_EINVAL, "%s: eps must be >= 0", what);
+  }
+  if ((st = bind_device(ctx)) != U15H_OK) { return st; }
+  return launched(ctx,
+                  u15h::launch_split_norm_rope(x, w_t, w_hw, cosf, sinf,
+                                               heads * tokens, heads, head_dim,
+                                               d_t, d_h, eps, norm, rope,
+                                               as_stream(stream)),
+                  what);
+}
+
+u15h_status
+u15h_split_qk_norm(u15h_ctx* ctx, u15h_stream stream, u15h_bf16* x,
+                   const u15h_bf16* w_t, const u15h_bf16* w_hw, int heads,
+                   int tokens, int head_dim, float eps)
+{
+  return norm_rope(ctx, stream, x, w_t, w_hw, nullptr, nullptr, heads, tokens,
+                   head_dim, head_dim / 2, head_dim / 4, eps, true, false,
+                   "split_qk_norm");
+}
+
+u15h_status
+u15h_split_rope(u15h_ctx* ctx, u15h_stream stream, u15h_bf16* x,
+                const float* cos_tab, const float* sin_tab, int heads,
+                int tokens, int head_dim, int d_t, int d_h)
+{
+  return norm_rope(ctx, stream, x, nullptr, nullptr, cos_tab, sin_tab, heads,
+                   tokens, head_dim, d_t, d_h, 0.0f, false, true,
+                   "split_rope");
+}
+
+u15h_status
+u15h_split_qk_norm_rope(u15h_ctx* ctx, u15h_stream stream, u15h_bf16* x,
+                        const u15h_bf16* w_t, const u15h_bf16* w_hw,
+                        const float* cos_tab, const float* sin_tab, int heads,
+                        int tokens, int head_dim, int d_t, int d_h, float eps)
+{
+  return norm_rope(ctx, stream, x, w_t, w_hw, cos_tab, sin_tab, heads, tokens,
+                   head_dim, d_t, d_h, eps, true, true, "split_qk_norm_rope");
+}
+
+u15h_status
+u15h_build_rope_tables(const int32_t* pos_t, const int32_t* pos_h,
+                       const int32_t* pos_w, int tokens, int head_dim, int d_t,
+                       int d_h, double theta_t, double theta_hw,
+                       float* cos_tab, float* sin_tab)
+{
+  if (tokens < 0 || head_dim <= 0 || d_t <= 0 || d_h <= 0 || d_t % 2 != 0 ||
+      d_h % 2 != 0 || d_t + 2 * d_h != head_dim || !(theta_t > 0.0) ||
+      !(theta_hw > 0.0)) {
+    return U15H_EINVAL;
+  }
+  if (tokens == 0) { return U15H_OK; }
+  if (pos_t == nullptr || pos_h == nullptr || pos_w == nullptr ||
+      cos_tab == nullptr || sin_tab == nullptr) {
+    return U15H_EINVAL;
+  }
+  // Per range its own ladder 1/theta^(2i/width), the angle pos * inv in
+  // double, narrowed once; the range's second half repeats the first
+  // (rotate_half reads c[j] and c[j + width/2] for one pair).
+  struct Range { int off, width; double theta; const int32_t* pos; };
+  const Range ranges[3] = {{0, d_t, theta_t, pos_t},
+                           {d_t, d_h, theta_hw, pos_h},
+                           {d_t + d_h, d_h, theta_hw, pos_w}};
+  for (const Range& r : ranges) {
+    const int half = r.width / 2;
+    std::vector<double> inv((size_t)half);
+    for (int i = 0; i < half; ++i) {
+      inv[(size_t)i] = 1.0 / std::pow(r.theta, (double)(2 * i) / r.width);
+    }
+    for (int t = 0; t < tokens; ++t) {
+      const size_t base = (size_t)t * head_dim + r.off;
+      for (int i = 0; i < half; ++i) {
+        const double a = (double)r.pos[t] * inv[(size_t)i];
+        const float c = (float)std::cos(a), sn = (float)std::sin(a);
+        cos_tab[base + i] = c;
+        cos_tab[base + i + half] = c;
+        sin_tab[base + i] = sn;
+        sin_tab[base + i + half] = sn;
+      }
+    }
+  }
+  return U15H_OK;
 }
 
 u15h_status

@@ -92,6 +92,11 @@ hipError_t launch_swiglu(const uint16_t* g, const uint16_t* u, uint16_t* o,
 hipError_t launch_dequant_affine(const uint32_t* codes, const uint16_t* sc,
                                  const uint16_t* bi, int bits, int group, int N,
                                  int K, uint16_t* w, hipStream_t s);
+hipError_t launch_split_norm_rope(uint16_t* x, const uint16_t* w_t,
+                                  const uint16_t* w_hw, const float* cosf,
+                                  const float* sinf, int rows, int H, int D,
+                                  int d_t, int d_h, float eps, bool norm,
+                                  bool rope, hipStream_t s);
 hipError_t launch_bias_add(uint16_t* y, const uint16_t* b, int M, int N,
                            hipStream_t s);
 hipError_t launch_f32_to_bf16(const float* src, int64_t n, uint16_t* dst,

@@ -994,6 +994,76 @@ f32_to_bf16_kernel(const float4* __restrict__ src, uint2* __restrict__ dst,
   }
 }
 
+// ---- split q/k norm and three-way split RoPE ------------------------------
+// x [T][H*D] bf16 in place, one wave per (token, head) row of D elements,
+// four rows per workgroup.  The row is staged in LDS (f32) so the rotation
+// can read each element's partner, which sits in another lane.
+//   NORM: the halves [0, D/2) and [D/2, D) are RMS-normalised separately,
+//         y = x * rsqrt(mean(half^2) + eps) * w (w_t, w_hw), sums in f32.
+//   ROPE: rotate_half on the ranges [0,d_t) (t), [d_t,d_t+d_h) (h) and
+//         [d_t+d_h,D) (w) with the packed f32 tables cos/sin [T][D]:
+//         out[j] = x[j] c[j] - x[j+r] s[j],  out[j+r] = x[j+r] c[j+r] +
+//         x[j] s[j+r] (r = half the range; the tables are doubled).
+// With both, the normalised row stays in f32 between the two steps.
+constexpr int kNormRopeMaxD = 512;
+
+template <bool NORM, bool ROPE>
+__global__ __launch_bounds__(256) void
+split_norm_rope_kernel(uint16_t* __restrict__ x,
+                       const uint16_t* __restrict__ w_t,
+                       const uint16_t* __restrict__ w_hw,
+                       const float* __restrict__ cosf,
+                       const float* __restrict__ sinf, int rows, int H, int D,
+                       int d_t, int d_h, float eps)
+{
+  __shared__ float buf[4][kNormRopeMaxD];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + wave;
+  const bool active = row < rows;
+  const int half = D >> 1;
+  float* b = buf[wave];
+  uint16_t* xr = x + (size_t)(active ? row : 0) * D;
+  float st = 0.0f, sh = 0.0f;
+  if (active) {
+    for (int i = lane; i < D; i += 64) {
+      const float v = bf16_to_f32(xr[i]);
+      b[i] = v;
+      if (i < half) { st += v * v; } else { sh += v * v; }
+    }
+  }
+  if constexpr (NORM) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      st += __shfl_xor(st, o);
+      sh += __shfl_xor(sh, o);
+    }
+    const float it = rsqrtf(st / (float)half + eps);
+    const float ih = rsqrtf(sh / (float)half + eps);
+    if (active) {
+      for (int i = lane; i < D; i += 64) {
+        b[i] = i < half ? b[i] * it * bf16_to_f32(w_t[i])
+                        : b[i] * ih * bf16_to_f32(w_hw[i - half]);
+      }
+    }
+  }
+  __syncthreads();
+  if (!active) { return; }
+  const int t = row / H;
+  for (int i = lane; i < D; i += 64) {
+    float v = b[i];
+    if constexpr (ROPE) {
+      const int off = i < d_t ? 0 : (i < d_t + d_h ? d_t : d_t + d_h);
+      const int r = (i < d_t ? d_t : d_h) >> 1;
+      const int j = i - off;
+      const float c = cosf[(size_t)t * D + i];
+      const float sn = sinf[(size_t)t * D + i];
+      v = j < r ? v * c - b[i + r] * sn : v * c + b[i - r] * sn;
+    }
+    xr[i] = (uint16_t)bf16_bits(v);
+  }
+}
+
 // ---- row gather / scatter for per-token routing ------------------------
 template <bool kScatter>
 __global__ __launch_bounds__(256) void
@@ -1146,6 +1216,30 @@ launch_f32_to_bf16(const float* src, int64_t n, uint16_t* dst, hipStream_t s)
 }
 
 hipError_t
+launch_split_norm_rope(uint16_t* x, const uint16_t* w_t, const uint16_t* w_hw,
+                       const float* cosf, const float* sinf, int rows, int H,
+                       int D, int d_t, int d_h, float eps, bool norm, bool rope,
+                       hipStream_t s)
+{
+  if (rows <= 0) { return hipSuccess; }
+  const dim3 grid((unsigned)((rows + 3) / 4));
+  if (norm && rope) {
+    hipLaunchKernelGGL((split_norm_rope_kernel<true, true>), grid, dim3(256),
+                       0, s, x, w_t, w_hw, cosf, sinf, rows, H, D, d_t, d_h,
+                       eps);
+  } else if (norm) {
+    hipLaunchKernelGGL((split_norm_rope_kernel<true, false>), grid, dim3(256),
+                       0, s, x, w_t, w_hw, cosf, sinf, rows, H, D, d_t, d_h,
+                       eps);
+  } else {
+    hipLaunchKernelGGL((split_norm_rope_kernel<false, true>), grid, dim3(256),
+                       0, s, x, w_t, w_hw, cosf, sinf, rows, H, D, d_t, d_h,
+                       eps);
+  }
+  return hipGetLastError();
+}
+
+hipError_t
 launch_gather_rows(const uint16_t* src, const int32_t* perm, int M, int cols,
                    uint16_t* dst, bool scatter, hipStream_t s)
 {
@@ -1185,6 +1279,9 @@ bool
 kernels_loadable()
 {
   const void* fns[] = {
+      reinterpret_cast<const void*>(&split_norm_rope_kernel<true, true>),
+      reinterpret_cast<const void*>(&split_norm_rope_kernel<true, false>),
+      reinterpret_cast<const void*>(&split_norm_rope_kernel<false, true>),
       reinterpret_cast<const void*>(&quant_rows_i8_kernel<2>),
       reinterpret_cast<const void*>(&quant_rows_i8_kernel<6>),
       reinterpret_cast<const void*>(&swiglu_kernel),

@@ -104,6 +104,14 @@ def load_library() -> ctypes.CDLL:
         "u15h_swiglu_fused": (i, [vp, vp, vp, vp, vp, i, i, i]),
         "u15h_bias_add": (i, [vp, vp, vp, vp, i, i]),
         "u15h_f32_to_bf16": (i, [vp, vp, vp, i64, vp]),
+        "u15h_split_qk_norm": (i, [vp, vp, vp, vp, vp, i, i, i,
+                                   ctypes.c_float]),
+        "u15h_split_rope": (i, [vp, vp, vp, vp, vp, i, i, i, i, i]),
+        "u15h_split_qk_norm_rope": (i, [vp, vp, vp, vp, vp, vp, vp, i, i, i,
+                                        i, i, ctypes.c_float]),
+        "u15h_build_rope_tables": (i, [vp, vp, vp, i, i, i, i,
+                                       ctypes.c_double, ctypes.c_double, vp,
+                                       vp]),
         "u15h_gather_rows": (i, [vp, vp, vp, vp, i, i, vp]),
         "u15h_scatter_rows": (i, [vp, vp, vp, vp, i, i, vp]),
     }
@@ -132,6 +140,29 @@ def route_rows(expert) -> tuple[list[int], int, int]:
     if st != OK:
         raise U15hError(st, "u15h_route_rows: invalid expert ids")
     return perm[:M], mu.value, mg.value
+
+
+def build_rope_tables(pos_t, pos_h, pos_w, head_dim, d_t, d_h,
+                      theta_t=5000000.0, theta_hw=10000.0):
+    """MetalOps::build_rope_tables on the host: (cos, sin) numpy f32
+    [tokens][head_dim]."""
+    import numpy as np
+    lib = load_library()
+    pt = np.ascontiguousarray(pos_t, dtype=np.int32)
+    ph = np.ascontiguousarray(pos_h, dtype=np.int32)
+    pw = np.ascontiguousarray(pos_w, dtype=np.int32)
+    T = int(pt.size)
+    if ph.size != T or pw.size != T:
+        raise ValueError("pos_t, pos_h, pos_w must have one entry per token")
+    cs = np.empty((max(T, 1), head_dim), np.float32)
+    sn = np.empty((max(T, 1), head_dim), np.float32)
+    st = lib.u15h_build_rope_tables(pt.ctypes.data, ph.ctypes.data,
+                                    pw.ctypes.data, T, head_dim, d_t, d_h,
+                                    theta_t, theta_hw, cs.ctypes.data,
+                                    sn.ctypes.data)
+    if st != OK:
+        raise U15hError(st, "u15h_build_rope_tables: invalid arguments")
+    return cs[:T], sn[:T]
 
 
 def _ptr(t):
@@ -376,6 +407,45 @@ class Ops:
         h = event if isinstance(event, ctypes.c_void_p) else ctypes.c_void_p(event)
         self._check(self._lib.u15h_profile_next_gemm(self._ctx, h),
                     "u15h_profile_next_gemm")
+
+    # ---- the step after the q/k projections -------------------------------
+    def _head(self, x, heads, head_dim):
+        tokens = x.shape[0]
+        _need(x, torch.bfloat16, (tokens, heads * head_dim), "x")
+        return tokens
+
+    def split_qk_norm(self, x, w_t, w_hw, heads, head_dim, eps=1e-6,
+                      stream=None):
+        """MetalOps::split_qk_norm on x [tokens][heads*head_dim] in place."""
+        T = self._head(x, heads, head_dim)
+        _need(w_t, torch.bfloat16, (head_dim // 2,), "w_t")
+        _need(w_hw, torch.bfloat16, (head_dim // 2,), "w_hw")
+        st = self._lib.u15h_split_qk_norm(self._ctx, _stream(stream), _ptr(x),
+                                          _ptr(w_t), _ptr(w_hw), heads, T,
+                                          head_dim, eps)
+        self._check(st, "u15h_split_qk_norm")
+
+    def split_rope(self, x, cos, sin, heads, head_dim, d_t, d_h, stream=None):
+        """MetalOps::split_rope with device f32 tables [tokens][head_dim]."""
+        T = self._head(x, heads, head_dim)
+        _need(cos, torch.float32, (T, head_dim), "cos")
+        _need(sin, torch.float32, (T, head_dim), "sin")
+        st = self._lib.u15h_split_rope(self._ctx, _stream(stream), _ptr(x),
+                                       _ptr(cos), _ptr(sin), heads, T,
+                                       head_dim, d_t, d_h)
+        self._check(st, "u15h_split_rope")
+
+    def split_qk_norm_rope(self, x, w_t, w_hw, cos, sin, heads, head_dim, d_t,
+                           d_h, eps=1e-6, stream=None):
+        T = self._head(x, heads, head_dim)
+        _need(w_t, torch.bfloat16, (head_dim // 2,), "w_t")
+        _need(w_hw, torch.bfloat16, (head_dim // 2,), "w_hw")
+        _need(cos, torch.float32, (T, head_dim), "cos")
+        _need(sin, torch.float32, (T, head_dim), "sin")
+        st = self._lib.u15h_split_qk_norm_rope(
+            self._ctx, _stream(stream), _ptr(x), _ptr(w_t), _ptr(w_hw),
+            _ptr(cos), _ptr(sin), heads, T, head_dim, d_t, d_h, eps)
+        self._check(st, "u15h_split_qk_norm_rope")
 
     # ---- routing -------------------------------------------------------
     def gather_rows(self, src, perm, dst, stream=None):
