@@ -150,6 +150,31 @@ u15h_status u15h_linear_q(u15h_ctx* ctx, u15h_stream stream,
 u15h_status u15h_bias_add(u15h_ctx* ctx, u15h_stream stream, u15h_bf16* y,
                           const u15h_bf16* bias, int M, int N);
 
+/* f16 -> bf16 on the device: the weight loader's f16_to_bf16_
+ * (src/u15-weights.cc:66-94; the pack's scales and biases ship F16): widen
+ * to f32 exactly, then RNE.  src holds f16 bit patterns; n % 4 == 0, both
+ * pointers 8-byte aligned. */
+u15h_status u15h_f16_to_bf16(u15h_ctx* ctx, u15h_stream stream,
+                             const uint16_t* src, int64_t n, u15h_bf16* dst);
+
+/* The quantized-pack shape rule of bind_matrix_ (src/u15-weights.cc:
+ * 247-325), host only: from K and the column counts of `.scales` and
+ * `.weight` (u32 codes), group = K / scales_cols and bits = codes_cols *
+ * 32 / K.  U15H_EINVAL unless both close exactly on bits 4/8, group 32/64. */
+u15h_status u15h_qweight_geometry(int K, int64_t scales_cols,
+                                  int64_t codes_cols, int* bits, int* group);
+
+/* Affine pack -> per-output-channel symmetric int8, the int8 tier's weight
+ * format: the pack is expanded to bf16 (as u15h_dequant_affine, into the
+ * context's dequant scratch) and each row quantised as
+ * u15h_quant_rows_i8: sw[n] = absmax/127, wq[n][k] = clamp(round(w/sw)).
+ * No reference counterpart (the reference's int8 tier quantises its
+ * weights inside the un-vendored I8GemmContext); this is the repack the
+ * scope table names for feeding the int8 GEMM from a quantized checkpoint. */
+u15h_status u15h_repack_affine_i8(u15h_ctx* ctx, u15h_stream stream,
+                                  const u15h_qweight* w, int N, int K,
+                                  int8_t* wq, float* sw);
+
 /* f32 -> bf16 round-to-nearest-even on the device: the weight loader's
  * conversion (src/u15-weights.cc:51-64).  n % 4 == 0. */
 u15h_status u15h_f32_to_bf16(u15h_ctx* ctx, u15h_stream stream,

@@ -62,6 +62,7 @@ def lib() -> ctypes.CDLL:
             "u15o_pack_affine": [vp, ctypes.c_int, ctypes.c_int, sz, sz, vp, vp, vp, vp],
             "u15o_bias_add_bf16": [vp, vp, sz, sz],
             "u15o_rms_norm": [vp, vp, ctypes.c_float, sz, sz, vp],
+            "u15o_f16_to_bf16_n": [vp, sz, vp],
             "u15o_rope_inv_freq": [ctypes.c_int, ctypes.c_double, vp],
             "u15o_rope_half": [vp, vp, ctypes.c_int, ctypes.c_double],
             "u15o_rope_tables": [vp, vp, vp, sz, ctypes.c_int, ctypes.c_int,
@@ -120,6 +121,14 @@ def f32_to_bf16(x) -> np.ndarray:
     x, p = _c(x, np.float32)
     out = np.empty(x.shape, np.uint16)
     lib().u15o_f32_to_bf16_n(p, x.size, out.ctypes.data)
+    return out
+
+
+def f16_to_bf16(h) -> np.ndarray:
+    """f16 bit patterns (uint16) -> bf16 bit patterns, the loader's rule."""
+    h, p = _c(h, np.uint16)
+    out = np.empty(h.shape, np.uint16)
+    lib().u15o_f16_to_bf16_n(p, h.size, out.ctypes.data)
     return out
 
 

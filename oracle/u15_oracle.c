@@ -25,6 +25,10 @@
  *   u15o_gemm_i8_i32      brute-force Python integer sums; the exact
  *                         row/column-sum identity; +-127 extremes.
  *   u15o_dequant_*        float32 numpy evaluation of the same expression.
+ *   u15o_f16_to_bf16_n    every finite and infinite f16 pattern against
+ *                         numpy's f16 -> f32 widening then torch's RNE;
+ *                         NaN patterns follow the reference's bit rule
+ *                         (checked on the device, not independently).
  *   u15o_rms_norm, u15o_rope_inv_freq, u15o_rope_half
  *                         bit-equal to the compiled reference's
  *                         u15::ref::rms_norm / rope_inv_freq /
@@ -323,6 +327,36 @@ u15o_bias_add_bf16(uint16_t* y, const uint16_t* b, size_t rows, size_t N)
       const float v = u15o_bf16_to_f32(y[r * N + n]) + u15o_bf16_to_f32(b[n]);
       y[r * N + n] = u15o_f32_to_bf16(v);
     }
+  }
+}
+
+void
+u15o_f16_to_bf16_n(const uint16_t* in, size_t n, uint16_t* out)
+{
+  /* src/u15-weights.cc:66-94: f16 -> f32 by expanding the exponent
+   * (subnormals renormalised, Inf/NaN carried with the payload shifted
+   * up), then the same RNE as f32_to_bf16. */
+  for (size_t i = 0; i < n; ++i) {
+    const uint32_t h = in[i];
+    const uint32_t sign = (h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1fu;
+    uint32_t man = h & 0x3ffu;
+    uint32_t f;
+    if (exp == 0) {
+      if (man == 0) {
+        f = sign;
+      } else {
+        exp = 127 - 15 + 1;
+        while ((man & 0x400u) == 0) { man <<= 1; --exp; }
+        man &= 0x3ffu;
+        f = sign | (exp << 23) | (man << 13);
+      }
+    } else if (exp == 31) {
+      f = sign | 0x7f800000u | (man << 13);
+    } else {
+      f = sign | ((exp - 15 + 127) << 23) | (man << 13);
+    }
+    out[i] = (uint16_t)((f + ((f >> 16) & 1u) + 0x7fffu) >> 16);
   }
 }
 

@@ -110,6 +110,10 @@ void u15o_pack_affine(const float* w, int bits, int group, size_t N, size_t K,
  * (u15-metal-ops.cc:435-446). */
 void u15o_bias_add_bf16(uint16_t* y, const uint16_t* b, size_t rows, size_t N);
 
+/* f16 -> bf16 the loader's way (src/u15-weights.cc:66-94): widen to f32
+ * exactly, then RNE. */
+void u15o_f16_to_bf16_n(const uint16_t* in, size_t n, uint16_t* out);
+
 /* The step after the q/k projections (src/u15-ref.h:25-95):
  *   rms_norm      y = x * 1/sqrt(mean(x^2) + eps) * w, double arithmetic
  *   rope_inv_freq inv[i] = 1/theta^(2i/dim), i < dim/2

@@ -79,3 +79,15 @@ def test_build_rope_tables_matches_oracle():
         u15h.build_rope_tables(pt, ph, pw, D, 64, 30)   # 64 + 60 != 128
     c0, s0 = u15h.build_rope_tables([], [], [], D, 64, 32)
     assert c0.shape == (0, D)
+
+
+def test_qweight_geometry_rule():
+    """bind_matrix_'s shape rule (src/u15-weights.cc:247-325)."""
+    assert u15h.qweight_geometry(4096, 64, 1024) == (8, 64)
+    assert u15h.qweight_geometry(4096, 128, 512) == (4, 32)
+    assert u15h.qweight_geometry(12288, 192, 3072) == (8, 64)
+    for K, sc, cc in ((4096, 100, 1024), (4096, 64, 1000), (4096, 16, 1024),
+                      (4096, 64, 2048), (4096, 0, 1024), (0, 64, 1024),
+                      (4096, 128, 768)):
+        with pytest.raises(u15h.U15hError):
+            u15h.qweight_geometry(K, sc, cc)

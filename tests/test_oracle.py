@@ -503,3 +503,20 @@ def test_rope_tables_closed_forms():
     want[d_t + d_h:] = oracle.rope_half(want[d_t + d_h:],
                                         oracle.rope_inv_freq(d_h, 1e4), d_h, 1)
     assert np.allclose(got, want, rtol=1e-6, atol=1e-6)
+
+
+def test_f16_to_bf16_every_pattern():
+    """The loader's f16 -> bf16 (u15-weights.cc:66-94) on all 65536 f16
+    patterns: every finite and infinite one equals numpy's exact f16 -> f32
+    widening rounded by torch's RNE."""
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = oracle.f16_to_bf16(h)
+    f = h.view(np.float16).astype(np.float32)
+    ok = ~np.isnan(f)
+    want = torch_bf16_bits(f)
+    assert np.array_equal(got[ok], want[ok])
+    # subnormals, signed zeros and the largest finite value explicitly
+    for bits, val in ((0x0001, 2.0 ** -24), (0x03ff, 1023 * 2.0 ** -24),
+                      (0x8000, -0.0), (0x7bff, 65504.0)):
+        assert oracle.bf16_to_f32(got[bits]) == np.float32(
+            torch.tensor(val).to(torch.bfloat16).float().item())

@@ -663,6 +663,29 @@ u15h_mot_gemm_i8(u15h_ctx* ctx, u15h_stream stream, const int8_t* xq,
                             Epi::kDequantBf16);
 }
 
+// The grow-only bf16 expansion of an affine pack (the reference's _w_deq,
+// u15-metal-ops.h:461-469).  Growing waits for the stream, since the old
+// buffer may still be read by work queued on it.
+static u15h_status
+ensure_deq_scratch(u15h_ctx* ctx, u15h_stream stream, size_t need)
+{
+  if (ctx->w_deq_bytes >= need) { return U15H_OK; }
+  if (ctx->w_deq != nullptr) {
+    (void)hipStreamSynchronize(as_stream(stream));
+    (void)hipFree(ctx->w_deq);
+    ctx->w_deq = nullptr;
+    ctx->w_deq_bytes = 0;
+  }
+  u15h_status st = bind_device(ctx);
+  if (st != U15H_OK) { return st; }
+  if (hipMalloc(&ctx->w_deq, need) != hipSuccess) {
+    ctx->w_deq = nullptr;
+    return fail(ctx, U15H_ENOMEM, "dequant scratch of %zu bytes", need);
+  }
+  ctx->w_deq_bytes = need;
+  return U15H_OK;
+}
+
 static u15h_status
 check_qweight(u15h_ctx* ctx, const u15h_qweight* w, int N, int K)
 {
@@ -721,20 +744,8 @@ u15h_linear_q(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
       (bias != nullptr && !aligned16(bias))) {
     return fail(ctx, U15H_EINVAL, "x/y null, or x/y/bias misaligned");
   }
-  const size_t need = (size_t)N * K * 2;
-  if (ctx->w_deq_bytes < need) {
-    if (ctx->w_deq != nullptr) {
-      (void)hipStreamSynchronize(as_stream(stream));
-      (void)hipFree(ctx->w_deq);
-      ctx->w_deq = nullptr;
-      ctx->w_deq_bytes = 0;
-    }
-    if ((st = bind_device(ctx)) != U15H_OK) { return st; }
-    if (hipMalloc(&ctx->w_deq, need) != hipSuccess) {
-      ctx->w_deq = nullptr;
-      return fail(ctx, U15H_ENOMEM, "dequant scratch of %zu bytes", need);
-    }
-    ctx->w_deq_bytes = need;
+  if ((st = ensure_deq_scratch(ctx, stream, (size_t)N * K * 2)) != U15H_OK) {
+    return st;
   }
   u15h_bf16* wd = static_cast<u15h_bf16*>(ctx->w_deq);
   if ((st = u15h_dequant_affine(ctx, stream, w, N, K, wd)) != U15H_OK) {
@@ -816,6 +827,72 @@ u15h_f32_to_bf16(u15h_ctx* ctx, u15h_stream stream, const float* src,
   return launched(ctx,
                   u15h::launch_f32_to_bf16(src, n, dst, as_stream(stream)),
                   "f32_to_bf16");
+}
+
+u15h_status
+u15h_f16_to_bf16(u15h_ctx* ctx, u15h_stream stream, const uint16_t* src,
+                 int64_t n, u15h_bf16* dst)
+{
+  if (ctx == nullptr) { return U15H_EINVAL; }
+  if (n < 0 || n % 4 != 0) {
+    return fail(ctx, U15H_EINVAL, "n=%lld must be a multiple of 4",
+                (long long)n);
+  }
+  if (n == 0) { ctx->err.clear(); return U15H_OK; }
+  if (src == nullptr || dst == nullptr || reinterpret_cast<uintptr_t>(src) % 8 ||
+      reinterpret_cast<uintptr_t>(dst) % 8) {
+    return fail(ctx, U15H_EINVAL, "src/dst null or not 8-byte aligned");
+  }
+  u15h_status st = bind_device(ctx);
+  if (st != U15H_OK) { return st; }
+  return launched(ctx, u15h::launch_f16_to_bf16(src, n, dst, as_stream(stream)),
+                  "f16_to_bf16");
+}
+
+u15h_status
+u15h_qweight_geometry(int K, int64_t scales_cols, int64_t codes_cols,
+                      int* bits, int* group)
+{
+  // group = K / scales_cols and bits = codes_cols * 32 / K, accepted only
+  // when both close exactly on w4/w8, g32/g64.
+  if (bits == nullptr || group == nullptr || K <= 0 || scales_cols <= 0 ||
+      codes_cols <= 0) {
+    return U15H_EINVAL;
+  }
+  const int64_t g = (int64_t)K / scales_cols;
+  const int64_t b = codes_cols * 32 / (int64_t)K;
+  if ((g != 32 && g != 64) || (b != 4 && b != 8) || scales_cols * g != K ||
+      codes_cols * 32 != (int64_t)K * b) {
+    return U15H_EINVAL;
+  }
+  *bits = (int)b;
+  *group = (int)g;
+  return U15H_OK;
+}
+
+u15h_status
+u15h_repack_affine_i8(u15h_ctx* ctx, u15h_stream stream,
+                      const u15h_qweight* w, int N, int K, int8_t* wq,
+                      float* sw)
+{
+  if (ctx == nullptr) { return U15H_EINVAL; }
+  u15h_status st = check_qweight(ctx, w, N, K);
+  if (st != U15H_OK) { return st; }
+  if (wq == nullptr || sw == nullptr || !aligned16(wq) ||
+      reinterpret_cast<uintptr_t>(sw) % 4) {
+    return fail(ctx, U15H_EINVAL, "wq/sw null or misaligned");
+  }
+  if ((st = ensure_deq_scratch(ctx, stream, (size_t)N * K * 2)) != U15H_OK) {
+    return st;
+  }
+  u15h_bf16* wd = static_cast<u15h_bf16*>(ctx->w_deq);
+  if ((st = u15h_dequant_affine(ctx, stream, w, N, K, wd)) != U15H_OK) {
+    return st;
+  }
+  return launched(ctx,
+                  u15h::launch_quant_rows_i8(wd, N, K, wq, sw,
+                                             as_stream(stream)),
+                  "repack_affine_i8");
 }
 
 static u15h_status

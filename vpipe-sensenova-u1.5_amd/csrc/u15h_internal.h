@@ -97,6 +97,8 @@ hipError_t launch_split_norm_rope(uint16_t* x, const uint16_t* w_t,
                                   const float* sinf, int rows, int H, int D,
                                   int d_t, int d_h, float eps, bool norm,
                                   bool rope, hipStream_t s);
+hipError_t launch_f16_to_bf16(const uint16_t* src, int64_t n, uint16_t* dst,
+                              hipStream_t s);
 hipError_t launch_bias_add(uint16_t* y, const uint16_t* b, int M, int N,
                            hipStream_t s);
 hipError_t launch_f32_to_bf16(const float* src, int64_t n, uint16_t* dst,

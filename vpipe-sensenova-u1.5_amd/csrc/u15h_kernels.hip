@@ -1064,6 +1064,49 @@ split_norm_rope_kernel(uint16_t* __restrict__ x,
   }
 }
 
+// ---- f16 -> bf16, the loader's conversion -----------------------------------
+// Widen f16 to f32 with integer operations (subnormals renormalised; Inf
+// and NaN keep their payload bits, which the hardware conversion would
+// quiet), then the same RNE as every other bf16 rounding here.
+__device__ __forceinline__ uint32_t
+f16_bits_to_bf16(uint32_t h)
+{
+  const uint32_t sign = (h & 0x8000u) << 16;
+  uint32_t exp = (h >> 10) & 0x1fu;
+  uint32_t man = h & 0x3ffu;
+  uint32_t f;
+  if (exp == 0) {
+    if (man == 0) {
+      f = sign;
+    } else {
+      // a subnormal: shift the leading one into the implicit position
+      const int lz = __clz(man) - 21;            // leading zeros in 11 bits
+      man = (man << lz) & 0x3ffu;
+      f = sign | ((uint32_t)(127 - 15 + 1 - lz) << 23) | (man << 13);
+    }
+  } else if (exp == 31) {
+    f = sign | 0x7f800000u | (man << 13);
+  } else {
+    f = sign | ((exp - 15 + 127) << 23) | (man << 13);
+  }
+  return (f + ((f >> 16) & 1u) + 0x7fffu) >> 16;
+}
+
+__global__ __launch_bounds__(256) void
+f16_to_bf16_kernel(const uint2* __restrict__ src, uint2* __restrict__ dst,
+                   int64_t nvec)
+{
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nvec;
+       i += stride) {
+    const uint2 v = src[i];
+    dst[i] = make_uint2(f16_bits_to_bf16(v.x & 0xffffu) |
+                            (f16_bits_to_bf16(v.x >> 16) << 16),
+                        f16_bits_to_bf16(v.y & 0xffffu) |
+                            (f16_bits_to_bf16(v.y >> 16) << 16));
+  }
+}
+
 // ---- row gather / scatter for per-token routing ------------------------
 template <bool kScatter>
 __global__ __launch_bounds__(256) void
@@ -1240,6 +1283,19 @@ launch_split_norm_rope(uint16_t* x, const uint16_t* w_t, const uint16_t* w_hw,
 }
 
 hipError_t
+launch_f16_to_bf16(const uint16_t* src, int64_t n, uint16_t* dst, hipStream_t s)
+{
+  const int64_t nvec = n / 4;
+  if (nvec <= 0) { return hipSuccess; }
+  const int64_t want = (nvec + 255) / 256;
+  hipLaunchKernelGGL(f16_to_bf16_kernel,
+                     dim3((unsigned)(want < 8192 ? want : 8192)), dim3(256), 0,
+                     s, reinterpret_cast<const uint2*>(src),
+                     reinterpret_cast<uint2*>(dst), nvec);
+  return hipGetLastError();
+}
+
+hipError_t
 launch_gather_rows(const uint16_t* src, const int32_t* perm, int M, int cols,
                    uint16_t* dst, bool scatter, hipStream_t s)
 {
@@ -1279,6 +1335,7 @@ bool
 kernels_loadable()
 {
   const void* fns[] = {
+      reinterpret_cast<const void*>(&f16_to_bf16_kernel),
       reinterpret_cast<const void*>(&split_norm_rope_kernel<true, true>),
       reinterpret_cast<const void*>(&split_norm_rope_kernel<true, false>),
       reinterpret_cast<const void*>(&split_norm_rope_kernel<false, true>),

@@ -104,6 +104,11 @@ def load_library() -> ctypes.CDLL:
         "u15h_swiglu_fused": (i, [vp, vp, vp, vp, vp, i, i, i]),
         "u15h_bias_add": (i, [vp, vp, vp, vp, i, i]),
         "u15h_f32_to_bf16": (i, [vp, vp, vp, i64, vp]),
+        "u15h_f16_to_bf16": (i, [vp, vp, vp, i64, vp]),
+        "u15h_qweight_geometry": (i, [i, i64, i64, ctypes.POINTER(i),
+                                      ctypes.POINTER(i)]),
+        "u15h_repack_affine_i8": (i, [vp, vp, ctypes.POINTER(_QWeight), i, i,
+                                      vp, vp]),
         "u15h_split_qk_norm": (i, [vp, vp, vp, vp, vp, i, i, i,
                                    ctypes.c_float]),
         "u15h_split_rope": (i, [vp, vp, vp, vp, vp, i, i, i, i, i]),
@@ -163,6 +168,69 @@ def build_rope_tables(pos_t, pos_h, pos_w, head_dim, d_t, d_h,
     if st != OK:
         raise U15hError(st, "u15h_build_rope_tables: invalid arguments")
     return cs[:T], sn[:T]
+
+
+def qweight_geometry(K, scales_cols, codes_cols):
+    """(bits, group) of a quantized pack from its shapes, or U15hError if
+    they do not close (bind_matrix_'s rule, src/u15-weights.cc:247-325)."""
+    lib = load_library()
+    b, g = ctypes.c_int(0), ctypes.c_int(0)
+    st = lib.u15h_qweight_geometry(K, scales_cols, codes_cols, ctypes.byref(b),
+                                   ctypes.byref(g))
+    if st != OK:
+        raise U15hError(st, f"pack shapes do not close: K={K}, scales cols="
+                        f"{scales_cols}, codes cols={codes_cols}")
+    return b.value, g.value
+
+
+def load_bf16(ops, path, name):
+    """A tensor of a safetensors file on the device as bf16, the way the
+    reference's bind_bf16_ reads it (src/u15-weights.cc:96-151): the dtype
+    is per tensor in the file's header; BF16 is bound as it sits, F32 and
+    F16 are converted on the device with the loader's RNE."""
+    from safetensors import safe_open
+    with safe_open(str(path), framework="pt") as f:
+        t = f.get_tensor(name)
+    if t.dtype == torch.bfloat16:
+        return t.cuda().contiguous()
+    if t.dtype not in (torch.float32, torch.float16):
+        raise U15hError(EINVAL, f"{name}: dtype {t.dtype} is not BF16/F32/F16")
+    src = t.cuda().contiguous()
+    n = src.numel()
+    pad = (-n) % 4
+    if pad:
+        src = torch.cat([src.reshape(-1), src.new_zeros(pad)])
+    dst = torch.empty(n + pad, dtype=torch.bfloat16, device="cuda")
+    if t.dtype == torch.float32:
+        ops.f32_to_bf16(src.reshape(-1), dst)
+    else:
+        ops.f16_to_bf16(src.reshape(-1), dst)
+    return dst[:n].reshape(t.shape)
+
+
+def load_matrix(ops, path, name, K):
+    """A projection matrix `name` of a safetensors file, dense or quantized,
+    by bind_matrix_'s rule (src/u15-weights.cc:247-325): a `.scales`
+    sibling means `.weight` holds u32 codes, and (bits, group) follow from
+    the shapes.  Returns ("dense", w bf16 [N][K]) or ("affine", (codes
+    int32, scales bf16, biases bf16, bits, group))."""
+    from safetensors import safe_open
+    with safe_open(str(path), framework="pt") as f:
+        keys = set(f.keys())
+        if name + ".scales" in keys and name + ".weight" in keys:
+            codes = f.get_tensor(name + ".weight")
+            scols = f.get_slice(name + ".scales").get_shape()[1]
+        else:
+            codes = None
+    if codes is None:
+        return "dense", load_bf16(ops, path, name + ".weight")
+    bits, group = qweight_geometry(K, scols, codes.shape[1])
+    if codes.dtype not in (torch.int32, torch.uint32):
+        raise U15hError(EINVAL, f"{name}.weight: codes must be 32-bit")
+    codes = codes.view(torch.int32).cuda().contiguous()
+    scales = load_bf16(ops, path, name + ".scales").contiguous()
+    biases = load_bf16(ops, path, name + ".biases").contiguous()
+    return "affine", (codes, scales, biases, bits, group)
 
 
 def _ptr(t):
@@ -303,6 +371,27 @@ class Ops:
         st = self._lib.u15h_f32_to_bf16(self._ctx, _stream(stream), _ptr(src),
                                         src.numel(), _ptr(dst))
         self._check(st, "u15h_f32_to_bf16")
+
+    def f16_to_bf16(self, src, dst, stream=None):
+        """src: f16 values (torch.float16) or their bit patterns (int16)."""
+        if src.dtype not in (torch.float16, torch.int16):
+            raise TypeError("src must be float16 (or its int16 bits)")
+        _need(dst, torch.bfloat16, tuple(src.shape), "dst")
+        if not src.is_contiguous():
+            raise ValueError("src must be contiguous")
+        st = self._lib.u15h_f16_to_bf16(self._ctx, _stream(stream), _ptr(src),
+                                        src.numel(), _ptr(dst))
+        self._check(st, "u15h_f16_to_bf16")
+
+    def repack_affine_i8(self, qw, N, K, wq, sw, stream=None):
+        """Affine pack -> per-channel int8 (wq int8 [N][K], sw f32 [N])."""
+        _need(wq, torch.int8, (N, K), "wq")
+        _need(sw, torch.float32, (N,), "sw")
+        q = self._qweight(qw, N, K)
+        st = self._lib.u15h_repack_affine_i8(self._ctx, _stream(stream),
+                                             ctypes.byref(q), N, K, _ptr(wq),
+                                             _ptr(sw))
+        self._check(st, "u15h_repack_affine_i8")
 
     # ---- swiglu --------------------------------------------------------
     def swiglu_fused(self, x, w_fused, y, M, K, inter, stream=None):
