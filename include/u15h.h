@@ -231,6 +231,64 @@ u15h_status u15h_build_rope_tables(const int32_t* pos_t, const int32_t* pos_h,
                                    float* cos_tab, float* sin_tab);
 
 /* ------------------------------------------------------------------ */
+/* Attention over the K/V cache                                        */
+/* ------------------------------------------------------------------ */
+
+/* Replaces MetalOps::sdpa(enc, q, k, v, out, hq, hkv, tq, tk, d, cap,
+ * causal, q_offset) (src/u15-metal-ops.h:226-232, .cc:648-676) and, with
+ * causal = 0, sdpa_steel (h:289-295, the bidirectional flash path the
+ * backbone uses for generation, src/u15-backbone.cc:225-232).
+ *   q, out  HEAD-major [hq][tq][d] bf16
+ *   k, v    caches [hkv][cap][d] bf16; keys [0, tk) in use, so the stride
+ *           between kv heads is the CAPACITY cap, not tk
+ *   query head h reads kv head h / (hq / hkv)  (the GQA group size)
+ *   softmax(q.k / sqrt(d)) . v, f32 accumulation; causal: key j attends
+ *   iff j <= q_offset + i (queries sit at q_offset within the keys).
+ * d in {32, 64, 128}; hq % hkv == 0; tk <= cap. */
+u15h_status u15h_sdpa(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* q,
+                      const u15h_bf16* k, const u15h_bf16* v, u15h_bf16* out,
+                      int hq, int hkv, int tq, int tk, int d, int cap,
+                      int causal, int q_offset);
+
+/* Replaces MetalOps::sdpa_block_causal (src/u15-metal-ops.h:330-337;
+ * kernel src/u15-kernels.metal:186-255): key j attends to query i iff
+ * t_index[j] == t_index[q_offset + i] or j <= q_offset + i (causal across
+ * t blocks, bidirectional within one; src/u15-ref.cc:179-192).  t_index is
+ * device int32 covering positions [0, max(tk, q_offset + tq)). */
+u15h_status u15h_sdpa_block_causal(u15h_ctx* ctx, u15h_stream stream,
+                                   const u15h_bf16* q, const u15h_bf16* k,
+                                   const u15h_bf16* v, u15h_bf16* out,
+                                   const int32_t* t_index, int hq, int hkv,
+                                   int tq, int tk, int d, int cap,
+                                   int q_offset);
+
+/* The same attention reading q and writing out TOKEN-major [tq][hq*d] (the
+ * layout the projections produce and o_proj consumes), which folds away the
+ * transpose_thd before and the transpose_htd after the reference's head-
+ * major kernels (src/u15-backbone.cc:208, 241).  No reference counterpart.
+ * mode 0 bidirectional, 1 causal, 2 block-causal (t_index as above). */
+u15h_status u15h_attention_token_major(u15h_ctx* ctx, u15h_stream stream,
+                                       const u15h_bf16* q, const u15h_bf16* k,
+                                       const u15h_bf16* v, u15h_bf16* out,
+                                       const int32_t* t_index, int hq,
+                                       int hkv, int tq, int tk, int d,
+                                       int cap, int q_offset, int mode);
+
+/* Replace MetalOps::transpose_thd / transpose_htd / transpose_into_cache
+ * (src/u15-metal-ops.h:339-355): [T][H][D] <-> [H][T][D], and [T][H*D]
+ * into a cache [H][cap][D] at token offset `offset`.  D % 8 == 0. */
+u15h_status u15h_transpose_thd(u15h_ctx* ctx, u15h_stream stream,
+                               const u15h_bf16* in, u15h_bf16* out, int T,
+                               int H, int D);
+u15h_status u15h_transpose_htd(u15h_ctx* ctx, u15h_stream stream,
+                               const u15h_bf16* in, u15h_bf16* out, int T,
+                               int H, int D);
+u15h_status u15h_transpose_into_cache(u15h_ctx* ctx, u15h_stream stream,
+                                      const u15h_bf16* in, u15h_bf16* cache,
+                                      int T, int H, int D, int cap,
+                                      int offset);
+
+/* ------------------------------------------------------------------ */
 /* SwiGLU                                                              */
 /* ------------------------------------------------------------------ */
 

@@ -63,6 +63,8 @@ def lib() -> ctypes.CDLL:
             "u15o_bias_add_bf16": [vp, vp, sz, sz],
             "u15o_rms_norm": [vp, vp, ctypes.c_float, sz, sz, vp],
             "u15o_f16_to_bf16_n": [vp, sz, vp],
+            "u15o_attention": [vp, vp, vp, ctypes.c_int, vp, sz, sz, sz, sz,
+                               sz, sz, sz, vp],
             "u15o_rope_inv_freq": [ctypes.c_int, ctypes.c_double, vp],
             "u15o_rope_half": [vp, vp, ctypes.c_int, ctypes.c_double],
             "u15o_rope_tables": [vp, vp, vp, sz, ctypes.c_int, ctypes.c_int,
@@ -97,6 +99,8 @@ def ref_lib():
         R.u15ref_silu.argtypes = [vp, sz]
         for n, a in {
             "u15ref_rms_norm": [vp, vp, ctypes.c_float, sz, sz, vp],
+            "u15ref_attention": [vp, vp, vp, vp, sz, sz, sz, sz, sz, vp],
+            "u15ref_block_causal_mask": [vp, sz, vp],
             "u15ref_rope_inv_freq": [ctypes.c_int, ctypes.c_double, vp],
             "u15ref_rope_half": [vp, vp, ctypes.c_int, ctypes.c_double],
             "u15ref_split_rope_project": [vp, vp, vp, vp, vp, vp, vp, sz, sz,
@@ -391,6 +395,57 @@ def ref_split_rope_project(x, w_proj, w_norm, w_norm_hw, pos_t, pos_h, pos_w,
     R.u15ref_split_rope_project(px, pwp, pwn, pwh, a, b, c, T, hidden, heads,
                                 head_dim, theta_t, theta_hw, eps,
                                 out.ctypes.data)
+    return out
+
+
+# ---- attention -------------------------------------------------------------------
+MODES = {"bidirectional": 0, "causal": 1, "block_causal": 2}
+
+
+def attention(q, k, v, hkv, tk, mode="bidirectional", t_index=None,
+              q_offset=0):
+    """q [hq][tq][d]; k, v caches [hkv][cap][d] (keys [0, tk) used);
+    head-major f32 out [hq][tq][d]."""
+    q, pq = _c(q, np.float32)
+    k, pk = _c(k, np.float32)
+    v, pv = _c(v, np.float32)
+    hq, tq, d = q.shape
+    cap = k.shape[1]
+    pt = None
+    if t_index is not None:
+        t_index, pt = _c(t_index, np.int32)
+    out = np.empty((hq, tq, d), np.float32)
+    lib().u15o_attention(pq, pk, pv, MODES[mode], pt, hq, hkv, tq, tk, d, cap,
+                         q_offset, out.ctypes.data)
+    return out
+
+
+def ref_attention(q, k, v, mask, hkv):
+    """u15::ref::attention on packed k, v [hkv][tk][d]: TOKEN-major out
+    [tq][hq*d] (the reference's own layout)."""
+    R = ref_lib()
+    if R is None:
+        return None
+    q, pq = _c(q, np.float32)
+    k, pk = _c(k, np.float32)
+    v, pv = _c(v, np.float32)
+    hq, tq, d = q.shape
+    tk = k.shape[1]
+    pm = None
+    if mask is not None:
+        mask, pm = _c(mask, np.float32)
+    out = np.empty((tq, hq * d), np.float32)
+    R.u15ref_attention(pq, pk, pv, pm, hq, hkv, tq, tk, d, out.ctypes.data)
+    return out
+
+
+def ref_block_causal_mask(t_index):
+    R = ref_lib()
+    if R is None:
+        return None
+    t, pt = _c(t_index, np.int32)
+    out = np.empty((t.size, t.size), np.float32)
+    R.u15ref_block_causal_mask(pt, t.size, out.ctypes.data)
     return out
 
 

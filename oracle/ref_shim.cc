@@ -7,6 +7,7 @@
 //   u15ref_silu   -> u15::ref::silu     (src/u15-ref.h:38, u15-ref.cc:51-58)
 //   u15ref_rms_norm, u15ref_rope_inv_freq, u15ref_rope_half,
 //   u15ref_split_rope_project -> the RoPE/norm helpers (src/u15-ref.h:25-95)
+//   u15ref_attention, u15ref_block_causal_mask -> src/u15-ref.h:95-110
 #include "u15-ref.h"
 
 extern "C" void
@@ -63,4 +64,20 @@ u15ref_split_rope_project(const float* x, const float* w_proj,
       w(pos_w, pos_w + tokens);
   u15::ref::split_rope_project(x, w_proj, w_norm, w_norm_hw, t, h, w, tokens,
                                hidden, p, out);
+}
+
+extern "C" void
+u15ref_attention(const float* q, const float* k, const float* v,
+                 const float* mask, std::size_t hq, std::size_t hkv,
+                 std::size_t tq, std::size_t tk, std::size_t d, float* out)
+{
+  u15::ref::attention(q, k, v, mask, hq, hkv, tq, tk, d, out);
+}
+
+extern "C" void
+u15ref_block_causal_mask(const int* t_index, std::size_t n, float* out)
+{
+  const std::vector<int> t(t_index, t_index + n);
+  const std::vector<float> m = u15::ref::block_causal_mask(t);
+  for (std::size_t i = 0; i < m.size(); ++i) { out[i] = m[i]; }
 }

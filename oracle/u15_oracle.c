@@ -29,6 +29,12 @@
  *                         numpy's f16 -> f32 widening then torch's RNE;
  *                         NaN patterns follow the reference's bit rule
  *                         (checked on the device, not independently).
+ *   u15o_attention        bit-equal to the compiled reference's
+ *                         u15::ref::attention (with its block_causal_mask
+ *                         or a causal mask) on packed copies of the cache;
+ *                         the reference tests' controls: a wrong GQA group
+ *                         differs, block-causal differs from causal on an
+ *                         edit-shaped prefix and equals it on pure text.
  *   u15o_rms_norm, u15o_rope_inv_freq, u15o_rope_half
  *                         bit-equal to the compiled reference's
  *                         u15::ref::rms_norm / rope_inv_freq /
@@ -471,6 +477,65 @@ u15o_split_qk_norm_rope(float* x, const float* w_t, const float* w_hw,
       }
     }
   }
+}
+
+/* ---- attention ------------------------------------------------------ */
+
+static int
+attn_allowed(int mode, const int32_t* t_index, size_t qpos, size_t j)
+{
+  /* mode 0: bidirectional; 1: causal, j <= qpos; 2: block-causal
+   * (src/u15-ref.cc:179-192): t[j] == t[qpos] or j <= qpos. */
+  if (mode == 0) { return 1; }
+  if (j <= qpos) { return 1; }
+  return mode == 2 && t_index[j] == t_index[qpos];
+}
+
+void
+u15o_attention(const float* q, const float* k, const float* v, int mode,
+               const int32_t* t_index, size_t hq, size_t hkv, size_t tq,
+               size_t tk, size_t d, size_t cap, size_t q_offset, float* out)
+{
+  /* src/u15-ref.cc:194-235 (attention): per query head h, its kv head
+   * h / (hq/hkv); scores q.k in double scaled by 1/sqrt(d); masked keys
+   * dropped (the additive -inf); softmax in double; out = sum p v.
+   * Layouts as the GPU path keeps them: q and out head-major [hq][tq][d],
+   * k and v a cache [hkv][cap][d] of which keys [0, tk) are in use; the
+   * queries sit at key positions q_offset + i. */
+  const double scale = 1.0 / sqrt((double)d);
+  const size_t group = hq / hkv;
+  double* row = (double*)malloc(sizeof(double) * (tk > 0 ? tk : 1));
+  for (size_t h = 0; h < hq; ++h) {
+    const size_t hk = h / group;
+    for (size_t i = 0; i < tq; ++i) {
+      const float* qi = q + (h * tq + i) * d;
+      const size_t qpos = q_offset + i;
+      double mx = -INFINITY;
+      for (size_t j = 0; j < tk; ++j) {
+        if (!attn_allowed(mode, t_index, qpos, j)) { row[j] = -INFINITY; continue; }
+        const float* kj = k + (hk * cap + j) * d;
+        double acc = 0.0;
+        for (size_t c = 0; c < d; ++c) { acc += (double)qi[c] * (double)kj[c]; }
+        row[j] = acc * scale;
+        if (row[j] > mx) { mx = row[j]; }
+      }
+      double sum = 0.0;
+      for (size_t j = 0; j < tk; ++j) {
+        row[j] = isinf(row[j]) && row[j] < 0 ? 0.0 : exp(row[j] - mx);
+        sum += row[j];
+      }
+      const double inv = sum > 0.0 ? 1.0 / sum : 0.0;
+      float* o = out + (h * tq + i) * d;
+      for (size_t c = 0; c < d; ++c) {
+        double acc = 0.0;
+        for (size_t j = 0; j < tk; ++j) {
+          acc += row[j] * inv * (double)v[(hk * cap + j) * d + c];
+        }
+        o[c] = (float)acc;
+      }
+    }
+  }
+  free(row);
 }
 
 double

@@ -137,6 +137,16 @@ void u15o_split_qk_norm_rope(float* x, const float* w_t, const float* w_hw,
                              double theta_hw, float eps, int do_norm,
                              int do_rope);
 
+/* Grouped-query attention (src/u15-ref.cc:194-235), double arithmetic.
+ * q, out head-major [hq][tq][d]; k, v caches [hkv][cap][d], keys [0, tk)
+ * in use; query i sits at key position q_offset + i.  mode 0 bidirectional,
+ * 1 causal (j <= pos), 2 block-causal (t_index[j] == t_index[pos] or
+ * j <= pos; src/u15-ref.cc:179-192). */
+void u15o_attention(const float* q, const float* k, const float* v, int mode,
+                    const int32_t* t_index, size_t hq, size_t hkv, size_t tq,
+                    size_t tk, size_t d, size_t cap, size_t q_offset,
+                    float* out);
+
 /* rel-L2 = sqrt(sum (a-b)^2 / sum b^2), tests/u15-kernels-test.cc:95-105;
  * max-rel = max|a-b| / max|b|. */
 double u15o_rel_l2(const float* a, const float* b, size_t n);

@@ -520,3 +520,74 @@ def test_f16_to_bf16_every_pattern():
                       (0x8000, -0.0), (0x7bff, 65504.0)):
         assert oracle.bf16_to_f32(got[bits]) == np.float32(
             torch.tensor(val).to(torch.bfloat16).float().item())
+
+
+# ---- attention ------------------------------------------------------------------
+def _cache(kk, cap):
+    hkv, tk, d = kk.shape
+    c = np.zeros((hkv, cap, d), np.float32)
+    c[:, :tk] = kk
+    return c
+
+
+def _tm_to_hm(o, hq):
+    tq = o.shape[0]
+    return o.reshape(tq, hq, -1).transpose(1, 0, 2)
+
+
+@pytest.mark.skipif(not REF, reason="reference CPU path not built")
+def test_attention_equals_reference_all_masks():
+    """test_sdpa / test_block_causal inputs (tests/u15-kernels-test.cc:
+    510-600, 604-666): GQA, a cache longer than the keys in use."""
+    hq, hkv, tq, tk, d, cap = 4, 2, 6, 6, 32, 10
+    q = oracle.randn_mt(61, hq * tq * d).reshape(hq, tq, d)
+    kk = oracle.randn_mt(62, hkv * tk * d).reshape(hkv, tk, d)
+    vv = oracle.randn_mt(63, hkv * tk * d).reshape(hkv, tk, d)
+    k, v = _cache(kk, cap), _cache(vv, cap)
+    got = oracle.attention(q, k, v, hkv, tk)
+    want = _tm_to_hm(oracle.ref_attention(q, kk, vv, None, hkv), hq)
+    assert np.array_equal(got, want)
+    causal = np.where(np.arange(tk)[None, :] > np.arange(tq)[:, None],
+                      -np.inf, 0).astype(np.float32)
+    got = oracle.attention(q, k, v, hkv, tk, "causal")
+    assert np.array_equal(got, _tm_to_hm(oracle.ref_attention(q, kk, vv, causal, hkv), hq))
+    t_idx = np.array([0, 1, 2, 3, 3, 3, 3, 3, 3, 4, 5], np.int32)
+    T = t_idx.size
+    q = oracle.randn_mt(71, hq * T * d).reshape(hq, T, d)
+    kk = oracle.randn_mt(72, hkv * T * d).reshape(hkv, T, d)
+    vv = oracle.randn_mt(73, hkv * T * d).reshape(hkv, T, d)
+    mask = oracle.ref_block_causal_mask(t_idx)
+    got = oracle.attention(q, _cache(kk, T + 4), _cache(vv, T + 4), hkv, T,
+                           "block_causal", t_idx)
+    assert np.array_equal(got, _tm_to_hm(oracle.ref_attention(q, kk, vv, mask, hkv), hq))
+
+
+def test_attention_controls_and_closed_forms():
+    """The reference tests' controls (u15-kernels-test.cc:672-718, 806-825)
+    and closed forms."""
+    hq, hkv, d = 4, 2, 32
+    t_idx = np.array([0, 1, 2, 3, 3, 3, 3, 3, 3, 4, 5], np.int32)
+    T = t_idx.size
+    q = oracle.randn_mt(71, hq * T * d).reshape(hq, T, d)
+    k = _cache(oracle.randn_mt(72, hkv * T * d).reshape(hkv, T, d), T)
+    v = _cache(oracle.randn_mt(73, hkv * T * d).reshape(hkv, T, d), T)
+    blk = oracle.attention(q, k, v, hkv, T, "block_causal", t_idx)
+    cau = oracle.attention(q, k, v, hkv, T, "causal")
+    assert oracle.rel_l2(cau, blk) > 1e-2          # the block rule matters
+    text = np.arange(T, dtype=np.int32)
+    assert np.array_equal(oracle.attention(q, k, v, hkv, T, "block_causal", text), cau)
+    # the GQA group is load-bearing: kv head h // 2 vs h // 1 (a cache with
+    # hq heads whose extra heads hold other keys)
+    k4 = np.concatenate([k, oracle.randn_mt(74, 2 * T * d).reshape(2, T, d)])
+    v4 = np.concatenate([v, oracle.randn_mt(75, 2 * T * d).reshape(2, T, d)])
+    good = oracle.attention(q, k, v, hkv, T)
+    bad = oracle.attention(q, k4, v4, hq, T)
+    assert oracle.rel_l2(bad, good) > 1e-2
+    # identical keys: uniform weights, the output is the mean of the values
+    kc = np.repeat(k[:, :1], T, axis=1)
+    u = oracle.attention(q, kc, v, hkv, T)
+    mean = v.mean(axis=1)
+    assert np.allclose(u, np.repeat(mean, hq // hkv, axis=0)[:, None, :], atol=1e-6)
+    # one key: the output is that key's value row
+    one = oracle.attention(q, k, v, hkv, 1)
+    assert np.allclose(one, np.repeat(v[:, :1], hq // hkv, axis=0).repeat(T, 1), atol=1e-7)

@@ -896,6 +896,143 @@ u15h_repack_affine_i8(u15h_ctx* ctx, u15h_stream stream,
 }
 
 static u15h_status
+attention_call(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* q,
+               const u15h_bf16* k, const u15h_bf16* v, u15h_bf16* out,
+               const int32_t* t_index, int hq, int hkv, int tq, int tk, int d,
+               int cap, int q_offset, int mode, bool token_major,
+               const char* what)
+{
+  if (ctx == nullptr) { return U15H_EINVAL; }
+  if (hq <= 0 || hkv <= 0 || hq % hkv != 0 || tq < 0 || tk < 0 || cap < tk ||
+      q_offset < 0 || (d != 32 && d != 64 && d != 128)) {
+    return fail(ctx, U15H_EINVAL, "%s: hq=%d hkv=%d tq=%d tk=%d d=%d cap=%d "
+                "q_offset=%d (hq %% hkv == 0, tk <= cap, d in {32, 64, 128})",
+                what, hq, hkv, tq, tk, d, cap, q_offset);
+  }
+  if ((long long)hkv * cap * d > (1LL << 40) || (long long)hq * tq * d > (1LL << 40)) {
+    return fail(ctx, U15H_EINVAL, "%s: operands too large", what);
+  }
+  if (tq == 0) { ctx->err.clear(); return U15H_OK; }
+  if (q == nullptr || out == nullptr || (tk > 0 && (k == nullptr || v == nullptr)) ||
+      (mode == 2 && t_index == nullptr)) {
+    return fail(ctx, U15H_EINVAL, "%s: null operand", what);
+  }
+  if (!aligned16(q) || !aligned16(out) || !aligned16(k) || !aligned16(v)) {
+    return fail(ctx, U15H_EINVAL, "%s: pointers must be 16-byte aligned", what);
+  }
+  u15h_status st = bind_device(ctx);
+  if (st != U15H_OK) { return st; }
+  u15h::AttnArgs a;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.out = out;
+  a.t_index = t_index;
+  a.q_head = token_major ? d : (long long)tq * d;
+  a.q_tok = token_major ? (long long)hq * d : d;
+  a.o_head = a.q_head;
+  a.o_tok = a.q_tok;
+  a.hq = hq;
+  a.hkv = hkv;
+  a.tq = tq;
+  a.tk = tk;
+  a.cap = cap;
+  a.q_offset = q_offset;
+  a.d = d;
+  a.mode = mode;
+  return launched(ctx, u15h::launch_attention(a, as_stream(stream)), what);
+}
+
+u15h_status
+u15h_sdpa(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* q,
+          const u15h_bf16* k, const u15h_bf16* v, u15h_bf16* out, int hq,
+          int hkv, int tq, int tk, int d, int cap, int causal, int q_offset)
+{
+  return attention_call(ctx, stream, q, k, v, out, nullptr, hq, hkv, tq, tk, d,
+                        cap, q_offset, causal ? 1 : 0, false, "sdpa");
+}
+
+u15h_status
+u15h_sdpa_block_causal(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* q,
+                       const u15h_bf16* k, const u15h_bf16* v, u15h_bf16* out,
+                       const int32_t* t_index, int hq, int hkv, int tq,
+                       int tk, int d, int cap, int q_offset)
+{
+  return attention_call(ctx, stream, q, k, v, out, t_index, hq, hkv, tq, tk, d,
+                        cap, q_offset, 2, false, "sdpa_block_causal");
+}
+
+u15h_status
+u15h_attention_token_major(u15h_ctx* ctx, u15h_stream stream,
+                           const u15h_bf16* q, const u15h_bf16* k,
+                           const u15h_bf16* v, u15h_bf16* out,
+                           const int32_t* t_index, int hq, int hkv, int tq,
+                           int tk, int d, int cap, int q_offset, int mode)
+{
+  if (mode < 0 || mode > 2) {
+    if (ctx != nullptr) { return fail(ctx, U15H_EINVAL, "mode=%d", mode); }
+    return U15H_EINVAL;
+  }
+  return attention_call(ctx, stream, q, k, v, out, t_index, hq, hkv, tq, tk, d,
+                        cap, q_offset, mode, true, "attention_token_major");
+}
+
+static u15h_status
+transpose_call(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* in,
+               u15h_bf16* out, int T, int H, int D, long long src_t,
+               long long src_h, long long dst_t, long long dst_h,
+               const char* what)
+{
+  if (ctx == nullptr) { return U15H_EINVAL; }
+  if (T < 0 || H <= 0 || D <= 0 || D % 8 != 0) {
+    return fail(ctx, U15H_EINVAL, "%s: T=%d H=%d D=%d (D %% 8 == 0)", what, T,
+                H, D);
+  }
+  if (T == 0) { ctx->err.clear(); return U15H_OK; }
+  if (in == nullptr || out == nullptr || !aligned16(in) || !aligned16(out)) {
+    return fail(ctx, U15H_EINVAL, "%s: null or misaligned", what);
+  }
+  u15h_status st = bind_device(ctx);
+  if (st != U15H_OK) { return st; }
+  return launched(ctx,
+                  u15h::launch_transpose_rows(in, out, T, H, D, src_t, src_h,
+                                              dst_t, dst_h, as_stream(stream)),
+                  what);
+}
+
+u15h_status
+u15h_transpose_thd(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* in,
+                   u15h_bf16* out, int T, int H, int D)
+{
+  return transpose_call(ctx, stream, in, out, T, H, D, (long long)H * D, D, D,
+                        (long long)T * D, "transpose_thd");
+}
+
+u15h_status
+u15h_transpose_htd(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* in,
+                   u15h_bf16* out, int T, int H, int D)
+{
+  return transpose_call(ctx, stream, in, out, T, H, D, D, (long long)T * D,
+                        (long long)H * D, D, "transpose_htd");
+}
+
+u15h_status
+u15h_transpose_into_cache(u15h_ctx* ctx, u15h_stream stream,
+                          const u15h_bf16* in, u15h_bf16* cache, int T, int H,
+                          int D, int cap, int offset)
+{
+  if (ctx == nullptr) { return U15H_EINVAL; }
+  if (offset < 0 || cap <= 0 || (long long)offset + T > cap) {
+    return fail(ctx, U15H_EINVAL, "transpose_into_cache: offset %d + T %d "
+                "exceeds capacity %d", offset, T, cap);
+  }
+  return transpose_call(ctx, stream, in,
+                        cache == nullptr ? nullptr : cache + (size_t)offset * D,
+                        T, H, D, (long long)H * D, D, D,
+                        (long long)cap * D, "transpose_into_cache");
+}
+
+static u15h_status
 check_head(u15h_ctx* ctx, int heads, int tokens, int head_dim, int d_t,
            int d_h)
 {

@@ -97,6 +97,24 @@ hipError_t launch_split_norm_rope(uint16_t* x, const uint16_t* w_t,
                                   const float* sinf, int rows, int H, int D,
                                   int d_t, int d_h, float eps, bool norm,
                                   bool rope, hipStream_t s);
+// Attention operands.  q and out are addressed as q[h * q_head + t * q_tok
+// + c] (head-major: q_head = tq*d, q_tok = d; token-major: q_head = d,
+// q_tok = hq*d); k and v are caches [hkv][cap][d].  mode 0 bidirectional,
+// 1 causal, 2 block-causal (t_index).
+struct AttnArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* out;
+  const int32_t* t_index;
+  long long q_head, q_tok, o_head, o_tok;
+  int hq, hkv, tq, tk, cap, q_offset, d, mode;
+};
+hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
+hipError_t launch_transpose_rows(const uint16_t* src, uint16_t* dst, int T,
+                                 int H, int D, long long src_t, long long src_h,
+                                 long long dst_t, long long dst_h,
+                                 hipStream_t s);
 hipError_t launch_f16_to_bf16(const uint16_t* src, int64_t n, uint16_t* dst,
                               hipStream_t s);
 hipError_t launch_bias_add(uint16_t* y, const uint16_t* b, int M, int N,

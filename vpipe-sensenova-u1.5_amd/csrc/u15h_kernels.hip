@@ -1107,6 +1107,197 @@ f16_to_bf16_kernel(const uint2* __restrict__ src, uint2* __restrict__ dst,
   }
 }
 
+// ---- flash attention ------------------------------------------------------
+// Grouped-query attention over a K/V cache, one workgroup per 128 queries
+// of one head (four waves of 32), keys streamed in tiles of 64 through LDS.
+//
+// The score tile is computed TRANSPOSED, S^T = K Q^T, with the key
+// fragment as the MFMA's first operand: a lane then holds 16 scores of ONE
+// query (its column), so the online softmax is per lane plus one exchange
+// with the lane 32 apart, and the output rescale by exp(m_old - m_new) is
+// one scalar per lane.  The output is accumulated transposed too, O^T =
+// V^T P^T: the second operand is P^T, whose lane layout (8 keys of one
+// query) is exactly the lane's own probabilities when the keys of each 16
+// are taken in the order the score layout holds them; the V tile is stored
+// transposed in LDS with that key order (bits 2 and 3 of the key index
+// exchanged), so each lane reads its 8 keys as one 16-byte fragment.
+//
+// LDS: K [64][D] with 16-byte chunk c of row r at c ^ (r % (D/8)), so a
+// fragment read (32 rows, one chunk) spreads over the bank groups; V^T
+// [D][64 + 8] (rows padded by 16 bytes for the transposing stores).
+// Keys past tk (and rows past the cache's keys in use) read as zeros and
+// are masked; masked scores are -inf and add 0 to every sum.
+template <int D, int MODE>
+__global__ __launch_bounds__(256, 2) void
+attention_kernel(const AttnArgs A)
+{
+  constexpr int BK = 64;
+  constexpr int KCH = D / 8;                 // 16-byte chunks per K row
+  constexpr int NDS = D / 16;                // MFMA K-steps of the scores
+  constexpr int NCB = D / 32;                // 32-row blocks of O^T
+  constexpr int VROW = BK + 8;               // V^T row, elements
+  __shared__ __attribute__((aligned(16))) uint16_t ks[BK * D];
+  __shared__ __attribute__((aligned(16))) uint16_t vt[D * VROW];
+  __shared__ int32_t ts[BK];
+
+  // Work item: (query head, 128-query tile), ordered kv head first, so
+  // that cutting the list into 8 runs (one per XCD, workgroups b, b+8, ...
+  // run on XCD b % 8) keeps each kv head's keys in one XCD's L2.
+  const int ntq = (A.tq + 127) / 128;
+  const int items = A.hq * ntq;
+  const int b = blockIdx.x;
+  const int item = (items % 8 == 0) ? (b % 8) * (items / 8) + b / 8 : b;
+  const int h = item / ntq;
+  const int qt = item % ntq;
+  const int kvh = h / (A.hq / A.hkv);
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int lq = lane & 31;
+  const int half = lane >> 5;
+  const int qrow = qt * 128 + wave * 32 + lq;     // this lane's query
+  const bool qvalid = qrow < A.tq;
+  const int qpos = A.q_offset + qrow;
+  const float scale_log2 = 1.4426950408889634f * rsqrtf((float)D);
+
+  i32x4_t qf[NDS];
+  const uint16_t* qp = A.q + (long long)h * A.q_head + (long long)qrow * A.q_tok;
+#pragma unroll
+  for (int ds = 0; ds < NDS; ++ds) {
+    qf[ds] = qvalid ? *reinterpret_cast<const i32x4_t*>(qp + ds * 16 + half * 8)
+                    : i32x4_t{0, 0, 0, 0};
+  }
+  int tq_idx = 0;
+  if constexpr (MODE == 2) { tq_idx = qvalid ? A.t_index[qpos] : 0; }
+
+  f32x16_t o[NCB];
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) { o[cb] = f32x16_t{}; }
+  float m = -INFINITY, l = 0.0f;
+
+  const uint16_t* kc = A.k + (long long)kvh * A.cap * D;
+  const uint16_t* vc = A.v + (long long)kvh * A.cap * D;
+  for (int j0 = 0; j0 < A.tk; j0 += BK) {
+    // ---- stage the tile: K swizzled, V transposed in score key order ----
+    for (int idx = tid; idx < BK * KCH; idx += 256) {
+      const int r = idx / KCH, c = idx % KCH;
+      const int key = j0 + r;
+      i32x4_t kv4 = {0, 0, 0, 0}, vv4 = {0, 0, 0, 0};
+      if (key < A.tk) {
+        kv4 = *reinterpret_cast<const i32x4_t*>(kc + (long long)key * D + c * 8);
+        vv4 = *reinterpret_cast<const i32x4_t*>(vc + (long long)key * D + c * 8);
+      }
+      *reinterpret_cast<i32x4_t*>(ks + r * D + ((c ^ (r % KCH)) << 3)) = kv4;
+      const int pos = (r & ~15) | ((r & 8) >> 1) | ((r & 4) << 1) | (r & 3);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t w = (uint32_t)vv4[e];
+        vt[(c * 8 + 2 * e) * VROW + pos] = (uint16_t)(w & 0xffffu);
+        vt[(c * 8 + 2 * e + 1) * VROW + pos] = (uint16_t)(w >> 16);
+      }
+    }
+    if constexpr (MODE == 2) {
+      if (tid < BK) { ts[tid] = j0 + tid < A.tk ? A.t_index[j0 + tid] : 0; }
+    }
+    __syncthreads();
+
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      f32x16_t sc = f32x16_t{};
+      const int krow = kb * 32 + lq;
+#pragma unroll
+      for (int ds = 0; ds < NDS; ++ds) {
+        const i32x4_t kf = *reinterpret_cast<const i32x4_t*>(
+            ks + krow * D + (((ds * 2 + half) ^ (krow % KCH)) << 3));
+        sc = MmaBf16::run(kf, qf[ds], sc);
+      }
+      // scores of keys j0 + kb*32 + 8*(r/4) + 4*half + r%4 for this query
+      float s2[16];
+      float mb = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kl = kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        const int key = j0 + kl;
+        bool ok = key < A.tk;
+        if constexpr (MODE == 1) { ok = ok && key <= qpos; }
+        if constexpr (MODE == 2) { ok = ok && (key <= qpos || ts[kl] == tq_idx); }
+        s2[r] = ok ? sc[r] * scale_log2 : -INFINITY;
+        mb = fmaxf(mb, s2[r]);
+      }
+      mb = fmaxf(mb, __shfl_xor(mb, 32));
+      const float mn = fmaxf(m, mb);
+      const float alpha = mn == -INFINITY ? 1.0f : exp2f(m - mn);
+      float ps = 0.0f;
+      uint32_t pk[8];
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const float p0 = s2[r] == -INFINITY ? 0.0f : exp2f(s2[r] - mn);
+        const float p1 = s2[r + 1] == -INFINITY ? 0.0f : exp2f(s2[r + 1] - mn);
+        ps += p0 + p1;
+        pk[r >> 1] = bf16_bits(p0) | (bf16_bits(p1) << 16);
+      }
+      ps += __shfl_xor(ps, 32);
+      l = l * alpha + ps;
+      m = mn;
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) { o[cb][r] *= alpha; }
+      }
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2) {
+        const i32x4_t pf = {(int)pk[k2 * 4 + 0], (int)pk[k2 * 4 + 1],
+                            (int)pk[k2 * 4 + 2], (int)pk[k2 * 4 + 3]};
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) {
+          const i32x4_t vf = *reinterpret_cast<const i32x4_t*>(
+              vt + (cb * 32 + lq) * VROW + kb * 32 + k2 * 16 + half * 8);
+          o[cb] = MmaBf16::run(vf, pf, o[cb]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  if (!qvalid) { return; }
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  uint16_t* op = A.out + (long long)h * A.o_head + (long long)qrow * A.o_tok;
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int c = cb * 32 + 8 * g + 4 * half;
+      u32x2_t w = {bf16_bits(o[cb][4 * g + 0] * inv) |
+                       (bf16_bits(o[cb][4 * g + 1] * inv) << 16),
+                   bf16_bits(o[cb][4 * g + 2] * inv) |
+                       (bf16_bits(o[cb][4 * g + 3] * inv) << 16)};
+      *reinterpret_cast<u32x2_t*>(op + c) = w;
+    }
+  }
+}
+
+// Row re-layout of [T][H][D] data between two strided views: element
+// (t, h, c) moves from src[t * src_t + h * src_h + c] to dst[t * dst_t +
+// h * dst_h + c]; 16 bytes per thread.
+__global__ __launch_bounds__(256) void
+transpose_rows_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
+                      int T, int H, int D, long long src_t, long long src_h,
+                      long long dst_t, long long dst_h)
+{
+  const int per_row = D / 8;
+  const long long n = (long long)T * H * per_row;
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n;
+       i += (long long)gridDim.x * 256) {
+    const int c = (int)(i % per_row) * 8;
+    const long long th = i / per_row;
+    const int hh = (int)(th % H);
+    const long long t = th / H;
+    *reinterpret_cast<uint4*>(dst + t * dst_t + hh * dst_h + c) =
+        *reinterpret_cast<const uint4*>(src + t * src_t + hh * src_h + c);
+  }
+}
+
 // ---- row gather / scatter for per-token routing ------------------------
 template <bool kScatter>
 __global__ __launch_bounds__(256) void
@@ -1295,6 +1486,48 @@ launch_f16_to_bf16(const uint16_t* src, int64_t n, uint16_t* dst, hipStream_t s)
   return hipGetLastError();
 }
 
+template <int D, int MODE>
+hipError_t
+launch_attention_d(const AttnArgs& a, hipStream_t s)
+{
+  const int ntq = (a.tq + 127) / 128;
+  hipLaunchKernelGGL((attention_kernel<D, MODE>), dim3(a.hq * ntq), dim3(256),
+                     0, s, a);
+  return hipGetLastError();
+}
+
+template <int D>
+hipError_t
+launch_attention_mode(const AttnArgs& a, hipStream_t s)
+{
+  if (a.mode == 1) { return launch_attention_d<D, 1>(a, s); }
+  if (a.mode == 2) { return launch_attention_d<D, 2>(a, s); }
+  return launch_attention_d<D, 0>(a, s);
+}
+
+hipError_t
+launch_attention(const AttnArgs& a, hipStream_t s)
+{
+  if (a.tq <= 0) { return hipSuccess; }
+  if (a.d == 128) { return launch_attention_mode<128>(a, s); }
+  if (a.d == 64) { return launch_attention_mode<64>(a, s); }
+  return launch_attention_mode<32>(a, s);
+}
+
+hipError_t
+launch_transpose_rows(const uint16_t* src, uint16_t* dst, int T, int H, int D,
+                      long long src_t, long long src_h, long long dst_t,
+                      long long dst_h, hipStream_t s)
+{
+  const long long n = (long long)T * H * (D / 8);
+  if (n <= 0) { return hipSuccess; }
+  const long long want = (n + 255) / 256;
+  hipLaunchKernelGGL(transpose_rows_kernel,
+                     dim3((unsigned)(want < 8192 ? want : 8192)), dim3(256), 0,
+                     s, src, dst, T, H, D, src_t, src_h, dst_t, dst_h);
+  return hipGetLastError();
+}
+
 hipError_t
 launch_gather_rows(const uint16_t* src, const int32_t* perm, int M, int cols,
                    uint16_t* dst, bool scatter, hipStream_t s)
@@ -1336,6 +1569,16 @@ kernels_loadable()
 {
   const void* fns[] = {
       reinterpret_cast<const void*>(&f16_to_bf16_kernel),
+      reinterpret_cast<const void*>(&attention_kernel<128, 0>),
+      reinterpret_cast<const void*>(&attention_kernel<128, 1>),
+      reinterpret_cast<const void*>(&attention_kernel<128, 2>),
+      reinterpret_cast<const void*>(&attention_kernel<64, 0>),
+      reinterpret_cast<const void*>(&attention_kernel<64, 1>),
+      reinterpret_cast<const void*>(&attention_kernel<64, 2>),
+      reinterpret_cast<const void*>(&attention_kernel<32, 0>),
+      reinterpret_cast<const void*>(&attention_kernel<32, 1>),
+      reinterpret_cast<const void*>(&attention_kernel<32, 2>),
+      reinterpret_cast<const void*>(&transpose_rows_kernel),
       reinterpret_cast<const void*>(&split_norm_rope_kernel<true, true>),
       reinterpret_cast<const void*>(&split_norm_rope_kernel<true, false>),
       reinterpret_cast<const void*>(&split_norm_rope_kernel<false, true>),

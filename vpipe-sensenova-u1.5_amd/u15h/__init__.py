@@ -117,6 +117,14 @@ def load_library() -> ctypes.CDLL:
         "u15h_build_rope_tables": (i, [vp, vp, vp, i, i, i, i,
                                        ctypes.c_double, ctypes.c_double, vp,
                                        vp]),
+        "u15h_sdpa": (i, [vp, vp, vp, vp, vp, vp, i, i, i, i, i, i, i, i]),
+        "u15h_sdpa_block_causal": (i, [vp, vp, vp, vp, vp, vp, vp, i, i, i, i,
+                                       i, i, i]),
+        "u15h_attention_token_major": (i, [vp, vp, vp, vp, vp, vp, vp, i, i,
+                                           i, i, i, i, i, i]),
+        "u15h_transpose_thd": (i, [vp, vp, vp, vp, i, i, i]),
+        "u15h_transpose_htd": (i, [vp, vp, vp, vp, i, i, i]),
+        "u15h_transpose_into_cache": (i, [vp, vp, vp, vp, i, i, i, i, i]),
         "u15h_gather_rows": (i, [vp, vp, vp, vp, i, i, vp]),
         "u15h_scatter_rows": (i, [vp, vp, vp, vp, i, i, vp]),
     }
@@ -535,6 +543,69 @@ class Ops:
             self._ctx, _stream(stream), _ptr(x), _ptr(w_t), _ptr(w_hw),
             _ptr(cos), _ptr(sin), heads, T, head_dim, d_t, d_h, eps)
         self._check(st, "u15h_split_qk_norm_rope")
+
+    # ---- attention -------------------------------------------------------
+    def sdpa(self, q, k, v, out, hkv, tk, causal=False, q_offset=0,
+             stream=None):
+        """MetalOps::sdpa / sdpa_steel: q, out [hq][tq][d]; k, v caches
+        [hkv][cap][d] with keys [0, tk) in use."""
+        hq, tq, d = q.shape
+        cap = k.shape[1]
+        _need(q, torch.bfloat16, (hq, tq, d), "q")
+        _need(out, torch.bfloat16, (hq, tq, d), "out")
+        _need(k, torch.bfloat16, (hkv, cap, d), "k")
+        _need(v, torch.bfloat16, (hkv, cap, d), "v")
+        st = self._lib.u15h_sdpa(self._ctx, _stream(stream), _ptr(q), _ptr(k),
+                                 _ptr(v), _ptr(out), hq, hkv, tq, tk, d, cap,
+                                 1 if causal else 0, q_offset)
+        self._check(st, "u15h_sdpa")
+
+    def sdpa_block_causal(self, q, k, v, out, t_index, hkv, tk, q_offset=0,
+                          stream=None):
+        hq, tq, d = q.shape
+        cap = k.shape[1]
+        _need(q, torch.bfloat16, (hq, tq, d), "q")
+        _need(out, torch.bfloat16, (hq, tq, d), "out")
+        _need(k, torch.bfloat16, (hkv, cap, d), "k")
+        _need(v, torch.bfloat16, (hkv, cap, d), "v")
+        if t_index.dtype != torch.int32 or t_index.numel() < max(tk, q_offset + tq):
+            raise ValueError("t_index: int32 covering max(tk, q_offset + tq)")
+        st = self._lib.u15h_sdpa_block_causal(
+            self._ctx, _stream(stream), _ptr(q), _ptr(k), _ptr(v), _ptr(out),
+            _ptr(t_index), hq, hkv, tq, tk, d, cap, q_offset)
+        self._check(st, "u15h_sdpa_block_causal")
+
+    def attention_token_major(self, q, k, v, out, hq, hkv, tk, mode=0,
+                              t_index=None, q_offset=0, stream=None):
+        """q, out [tq][hq*d] token-major; mode 0/1/2 = bidirectional,
+        causal, block-causal."""
+        tq = q.shape[0]
+        cap, d = k.shape[1], k.shape[2]
+        _need(q, torch.bfloat16, (tq, hq * d), "q")
+        _need(out, torch.bfloat16, (tq, hq * d), "out")
+        _need(k, torch.bfloat16, (hkv, cap, d), "k")
+        _need(v, torch.bfloat16, (hkv, cap, d), "v")
+        st = self._lib.u15h_attention_token_major(
+            self._ctx, _stream(stream), _ptr(q), _ptr(k), _ptr(v), _ptr(out),
+            _ptr(t_index), hq, hkv, tq, tk, d, cap, q_offset, mode)
+        self._check(st, "u15h_attention_token_major")
+
+    def transpose_thd(self, x, out, T, H, D, stream=None):
+        st = self._lib.u15h_transpose_thd(self._ctx, _stream(stream), _ptr(x),
+                                          _ptr(out), T, H, D)
+        self._check(st, "u15h_transpose_thd")
+
+    def transpose_htd(self, x, out, T, H, D, stream=None):
+        st = self._lib.u15h_transpose_htd(self._ctx, _stream(stream), _ptr(x),
+                                          _ptr(out), T, H, D)
+        self._check(st, "u15h_transpose_htd")
+
+    def transpose_into_cache(self, x, cache, T, H, D, offset, stream=None):
+        cap = cache.shape[1]
+        st = self._lib.u15h_transpose_into_cache(self._ctx, _stream(stream),
+                                                 _ptr(x), _ptr(cache), T, H, D,
+                                                 cap, offset)
+        self._check(st, "u15h_transpose_into_cache")
 
     # ---- routing -------------------------------------------------------
     def gather_rows(self, src, perm, dst, stream=None):
