@@ -1109,24 +1109,29 @@ f16_to_bf16_kernel(const uint2* __restrict__ src, uint2* __restrict__ dst,
 
 // ---- flash attention ------------------------------------------------------
 // Grouped-query attention over a K/V cache, one workgroup per 128 queries
-// of one head (four waves of 32), keys streamed in tiles of 64 through LDS.
+// of one head (four waves of 32), keys streamed in tiles of 64 through a
+// double-buffered LDS stage: the next tile is loaded into registers while
+// the current one is computed, then written to the other buffer; one
+// barrier per tile.
 //
 // The score tile is computed TRANSPOSED, S^T = K Q^T, with the key
-// fragment as the MFMA's first operand: a lane then holds 16 scores of ONE
-// query (its column), so the online softmax is per lane plus one exchange
-// with the lane 32 apart, and the output rescale by exp(m_old - m_new) is
-// one scalar per lane.  The output is accumulated transposed too, O^T =
-// V^T P^T: the second operand is P^T, whose lane layout (8 keys of one
-// query) is exactly the lane's own probabilities when the keys of each 16
-// are taken in the order the score layout holds them; the V tile is stored
-// transposed in LDS with that key order (bits 2 and 3 of the key index
-// exchanged), so each lane reads its 8 keys as one 16-byte fragment.
+// fragment as the MFMA's first operand: a lane then holds 32 scores (two
+// 32-key blocks) of ONE query, its column, so the online softmax is per
+// lane plus one exchange with the lane 32 apart, and the output rescale by
+// exp(m_old - m_new) is one scalar per lane, applied once per tile.  The
+// output is accumulated transposed too, O^T = V^T P^T: the second operand
+// is P^T, whose lane layout (8 keys of one query) is exactly the lane's own
+// probabilities when the keys of each 16 are taken in the order the score
+// layout holds them; the V tile is stored transposed in LDS with that key
+// order (bits 2 and 3 of the key index exchanged), so a lane reads its 8
+// keys as one 16-byte fragment.  The transpose is done four keys at a time
+// in registers (byte permutes), so each 16-byte global chunk becomes eight
+// 8-byte LDS writes.
 //
-// LDS: K [64][D] with 16-byte chunk c of row r at c ^ (r % (D/8)), so a
-// fragment read (32 rows, one chunk) spreads over the bank groups; V^T
-// [D][64 + 8] (rows padded by 16 bytes for the transposing stores).
-// Keys past tk (and rows past the cache's keys in use) read as zeros and
-// are masked; masked scores are -inf and add 0 to every sum.
+// LDS per buffer: K [64][D] with 16-byte chunk c of row r at c ^ (r % (D/8))
+// (a fragment read, 32 rows at one chunk, spreads over the bank groups);
+// V^T [D][64 + 8].  Keys past tk read as zeros and are masked; masked
+// scores are -inf and add 0 to every sum.
 template <int D, int MODE>
 __global__ __launch_bounds__(256, 2) void
 attention_kernel(const AttnArgs A)
@@ -1136,9 +1141,12 @@ attention_kernel(const AttnArgs A)
   constexpr int NDS = D / 16;                // MFMA K-steps of the scores
   constexpr int NCB = D / 32;                // 32-row blocks of O^T
   constexpr int VROW = BK + 8;               // V^T row, elements
-  __shared__ __attribute__((aligned(16))) uint16_t ks[BK * D];
-  __shared__ __attribute__((aligned(16))) uint16_t vt[D * VROW];
-  __shared__ int32_t ts[BK];
+  constexpr int KPT = BK * KCH / 256;        // K chunks per thread per tile
+  constexpr int VGRP = BK / 4 * KCH;         // 4-key V groups per tile
+  constexpr int VPT = (VGRP + 255) / 256;    // V groups per thread
+  __shared__ __attribute__((aligned(16))) uint16_t ks[2][BK * D];
+  __shared__ __attribute__((aligned(16))) uint16_t vt[2][D * VROW];
+  __shared__ int32_t ts[2][BK];
 
   // Work item: (query head, 128-query tile), ordered kv head first, so
   // that cutting the list into 8 runs (one per XCD, workgroups b, b+8, ...
@@ -1171,37 +1179,87 @@ attention_kernel(const AttnArgs A)
   int tq_idx = 0;
   if constexpr (MODE == 2) { tq_idx = qvalid ? A.t_index[qpos] : 0; }
 
+  const uint16_t* kc = A.k + (long long)kvh * A.cap * D;
+  const uint16_t* vc = A.v + (long long)kvh * A.cap * D;
+
+  // ---- tile staging: global -> registers -> LDS ---------------------------
+  i32x4_t kr[KPT], vr[VPT][4];
+  int32_t tr = 0;
+  auto load_tile = [&](int j0) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int idx = tid + i * 256;
+      const int r = idx / KCH, c = idx % KCH;
+      kr[i] = j0 + r < A.tk
+                  ? *reinterpret_cast<const i32x4_t*>(kc + (long long)(j0 + r) * D + c * 8)
+                  : i32x4_t{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int g = tid + i * 256;                  // (4-key group, chunk)
+      const int c = g % KCH, r0 = (g / KCH) * 4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vr[i][e] = (g < VGRP && j0 + r0 + e < A.tk)
+                       ? *reinterpret_cast<const i32x4_t*>(
+                             vc + (long long)(j0 + r0 + e) * D + c * 8)
+                       : i32x4_t{0, 0, 0, 0};
+      }
+    }
+    if constexpr (MODE == 2) {
+      if (tid < BK) { tr = j0 + tid < A.tk ? A.t_index[j0 + tid] : 0; }
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int idx = tid + i * 256;
+      const int r = idx / KCH, c = idx % KCH;
+      *reinterpret_cast<i32x4_t*>(&ks[buf][r * D + ((c ^ (r % KCH)) << 3)]) = kr[i];
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int g = tid + i * 256;
+      if (g >= VGRP) { continue; }
+      const int c = g % KCH, r0 = (g / KCH) * 4;
+      // keys r0..r0+3 stay contiguous under the bit-2/3 exchange
+      const int pos = (r0 & ~15) | ((r0 & 8) >> 1) | ((r0 & 4) << 1);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t a0 = (uint32_t)vr[i][0][w], a1 = (uint32_t)vr[i][1][w];
+        const uint32_t a2 = (uint32_t)vr[i][2][w], a3 = (uint32_t)vr[i][3][w];
+        // element 2w of keys 0..3, then element 2w+1
+        const u32x2_t lo = {__builtin_amdgcn_perm(a1, a0, 0x05040100u),
+                            __builtin_amdgcn_perm(a3, a2, 0x05040100u)};
+        const u32x2_t hi = {__builtin_amdgcn_perm(a1, a0, 0x07060302u),
+                            __builtin_amdgcn_perm(a3, a2, 0x07060302u)};
+        *reinterpret_cast<u32x2_t*>(&vt[buf][(c * 8 + 2 * w) * VROW + pos]) = lo;
+        *reinterpret_cast<u32x2_t*>(&vt[buf][(c * 8 + 2 * w + 1) * VROW + pos]) = hi;
+      }
+    }
+    if constexpr (MODE == 2) {
+      if (tid < BK) { ts[buf][tid] = tr; }
+    }
+  };
+
   f32x16_t o[NCB];
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) { o[cb] = f32x16_t{}; }
   float m = -INFINITY, l = 0.0f;
 
-  const uint16_t* kc = A.k + (long long)kvh * A.cap * D;
-  const uint16_t* vc = A.v + (long long)kvh * A.cap * D;
-  for (int j0 = 0; j0 < A.tk; j0 += BK) {
-    // ---- stage the tile: K swizzled, V transposed in score key order ----
-    for (int idx = tid; idx < BK * KCH; idx += 256) {
-      const int r = idx / KCH, c = idx % KCH;
-      const int key = j0 + r;
-      i32x4_t kv4 = {0, 0, 0, 0}, vv4 = {0, 0, 0, 0};
-      if (key < A.tk) {
-        kv4 = *reinterpret_cast<const i32x4_t*>(kc + (long long)key * D + c * 8);
-        vv4 = *reinterpret_cast<const i32x4_t*>(vc + (long long)key * D + c * 8);
-      }
-      *reinterpret_cast<i32x4_t*>(ks + r * D + ((c ^ (r % KCH)) << 3)) = kv4;
-      const int pos = (r & ~15) | ((r & 8) >> 1) | ((r & 4) << 1) | (r & 3);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t w = (uint32_t)vv4[e];
-        vt[(c * 8 + 2 * e) * VROW + pos] = (uint16_t)(w & 0xffffu);
-        vt[(c * 8 + 2 * e + 1) * VROW + pos] = (uint16_t)(w >> 16);
-      }
-    }
-    if constexpr (MODE == 2) {
-      if (tid < BK) { ts[tid] = j0 + tid < A.tk ? A.t_index[j0 + tid] : 0; }
-    }
+  const int ntiles = (A.tk + BK - 1) / BK;
+  if (ntiles > 0) {
+    load_tile(0);
+    store_tile(0);
+    if (ntiles > 1) { load_tile(BK); }
     __syncthreads();
-
+  }
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    const int j0 = t * BK;
+    // ---- scores of the tile's 64 keys for this lane's query -------------
+    float s2[32];
+    float mb = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       f32x16_t sc = f32x16_t{};
@@ -1209,53 +1267,59 @@ attention_kernel(const AttnArgs A)
 #pragma unroll
       for (int ds = 0; ds < NDS; ++ds) {
         const i32x4_t kf = *reinterpret_cast<const i32x4_t*>(
-            ks + krow * D + (((ds * 2 + half) ^ (krow % KCH)) << 3));
+            &ks[buf][krow * D + (((ds * 2 + half) ^ (krow % KCH)) << 3)]);
         sc = MmaBf16::run(kf, qf[ds], sc);
       }
-      // scores of keys j0 + kb*32 + 8*(r/4) + 4*half + r%4 for this query
-      float s2[16];
-      float mb = -INFINITY;
+      // key of sc[r]: j0 + kb*32 + 8*(r/4) + 4*half + r%4
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int kl = kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
         const int key = j0 + kl;
         bool ok = key < A.tk;
         if constexpr (MODE == 1) { ok = ok && key <= qpos; }
-        if constexpr (MODE == 2) { ok = ok && (key <= qpos || ts[kl] == tq_idx); }
-        s2[r] = ok ? sc[r] * scale_log2 : -INFINITY;
-        mb = fmaxf(mb, s2[r]);
+        if constexpr (MODE == 2) { ok = ok && (key <= qpos || ts[buf][kl] == tq_idx); }
+        s2[kb * 16 + r] = ok ? sc[r] * scale_log2 : -INFINITY;
+        mb = fmaxf(mb, s2[kb * 16 + r]);
       }
-      mb = fmaxf(mb, __shfl_xor(mb, 32));
-      const float mn = fmaxf(m, mb);
-      const float alpha = mn == -INFINITY ? 1.0f : exp2f(m - mn);
-      float ps = 0.0f;
-      uint32_t pk[8];
+    }
+    mb = fmaxf(mb, __shfl_xor(mb, 32));
+    const float mn = fmaxf(m, mb);
+    const float alpha = mn == -INFINITY ? 1.0f : exp2f(m - mn);
+    float ps = 0.0f;
+    uint32_t pk[16];
 #pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        const float p0 = s2[r] == -INFINITY ? 0.0f : exp2f(s2[r] - mn);
-        const float p1 = s2[r + 1] == -INFINITY ? 0.0f : exp2f(s2[r + 1] - mn);
-        ps += p0 + p1;
-        pk[r >> 1] = bf16_bits(p0) | (bf16_bits(p1) << 16);
-      }
-      ps += __shfl_xor(ps, 32);
-      l = l * alpha + ps;
-      m = mn;
+    for (int r = 0; r < 32; r += 2) {
+      const float p0 = s2[r] == -INFINITY ? 0.0f : exp2f(s2[r] - mn);
+      const float p1 = s2[r + 1] == -INFINITY ? 0.0f : exp2f(s2[r + 1] - mn);
+      ps += p0 + p1;
+      pk[r >> 1] = bf16_bits(p0) | (bf16_bits(p1) << 16);
+    }
+    ps += __shfl_xor(ps, 32);
+    l = l * alpha + ps;
+    m = mn;
+    if (alpha != 1.0f) {
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) { o[cb][r] *= alpha; }
       }
+    }
+    // ---- O^T += V^T P^T over the tile's four 16-key steps ---------------
 #pragma unroll
-      for (int k2 = 0; k2 < 2; ++k2) {
-        const i32x4_t pf = {(int)pk[k2 * 4 + 0], (int)pk[k2 * 4 + 1],
-                            (int)pk[k2 * 4 + 2], (int)pk[k2 * 4 + 3]};
+    for (int k4 = 0; k4 < 4; ++k4) {
+      const i32x4_t pf = {(int)pk[k4 * 4 + 0], (int)pk[k4 * 4 + 1],
+                          (int)pk[k4 * 4 + 2], (int)pk[k4 * 4 + 3]};
 #pragma unroll
-        for (int cb = 0; cb < NCB; ++cb) {
-          const i32x4_t vf = *reinterpret_cast<const i32x4_t*>(
-              vt + (cb * 32 + lq) * VROW + kb * 32 + k2 * 16 + half * 8);
-          o[cb] = MmaBf16::run(vf, pf, o[cb]);
-        }
+      for (int cb = 0; cb < NCB; ++cb) {
+        const i32x4_t vf = *reinterpret_cast<const i32x4_t*>(
+            &vt[buf][(cb * 32 + lq) * VROW + k4 * 16 + half * 8]);
+        o[cb] = MmaBf16::run(vf, pf, o[cb]);
       }
+    }
+    // ---- the next tile into the other buffer, the one after into regs ---
+    if (t + 1 < ntiles) {
+      store_tile(buf ^ 1);
+      if (t + 2 < ntiles) { load_tile((t + 2) * BK); }
     }
     __syncthreads();
   }
