@@ -909,7 +909,9 @@ attention_call(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* q,
                 "q_offset=%d (hq %% hkv == 0, tk <= cap, d in {32, 64, 128})",
                 what, hq, hkv, tq, tk, d, cap, q_offset);
   }
-  if ((long long)hkv * cap * d > (1LL << 40) || (long long)hq * tq * d > (1LL << 40)) {
+  // one kv head's keys are read through a buffer resource: 2^31 bytes at most
+  if ((long long)hkv * cap * d > (1LL << 40) || (long long)hq * tq * d > (1LL << 40) ||
+      (long long)tk * d * 2 >= (1LL << 31)) {
     return fail(ctx, U15H_EINVAL, "%s: operands too large", what);
   }
   if (tq == 0) { ctx->err.clear(); return U15H_OK; }

@@ -1117,21 +1117,58 @@ f16_to_bf16_kernel(const uint2* __restrict__ src, uint2* __restrict__ dst,
 // The score tile is computed TRANSPOSED, S^T = K Q^T, with the key
 // fragment as the MFMA's first operand: a lane then holds 32 scores (two
 // 32-key blocks) of ONE query, its column, so the online softmax is per
-// lane plus one exchange with the lane 32 apart, and the output rescale by
-// exp(m_old - m_new) is one scalar per lane, applied once per tile.  The
-// output is accumulated transposed too, O^T = V^T P^T: the second operand
-// is P^T, whose lane layout (8 keys of one query) is exactly the lane's own
-// probabilities when the keys of each 16 are taken in the order the score
-// layout holds them; the V tile is stored transposed in LDS with that key
-// order (bits 2 and 3 of the key index exchanged), so a lane reads its 8
-// keys as one 16-byte fragment.  The transpose is done four keys at a time
-// in registers (byte permutes), so each 16-byte global chunk becomes eight
-// 8-byte LDS writes.
+// lane plus one exchange with the lane 32 apart, and the output rescale is
+// one scalar per lane.  The output is accumulated transposed too,
+// O^T = V^T P^T: the second operand is P^T, whose lane layout (8 keys of
+// one query) is exactly the lane's own probabilities when the keys of each
+// 16 are taken in the order the score layout holds them; the V tile is
+// stored transposed in LDS with that key order (bits 2 and 3 of the key
+// index exchanged), so a lane reads its 8 keys as one 16-byte fragment.
+// The transpose is done four keys at a time in registers (byte permutes),
+// so each 16-byte global chunk becomes eight 8-byte LDS writes.
+//
+// The softmax work per score is one FMA (scale and running max), one
+// exp2, one add and half a bf16 pack; a tile needing no mask (every key
+// below tk and, for the causal masks, below the workgroup's first query)
+// skips the mask.  The running max m is raised only when a tile's max
+// exceeds it by more than kLazy/scale: until then probabilities are
+// exp2((s - m) * scale) <= 2^kLazy, and the output and the sum share the
+// same m, so the quotient is unchanged while most tiles skip the rescale.
 //
 // LDS per buffer: K [64][D] with 16-byte chunk c of row r at c ^ (r % (D/8))
 // (a fragment read, 32 rows at one chunk, spreads over the bank groups);
-// V^T [D][64 + 8].  Keys past tk read as zeros and are masked; masked
-// scores are -inf and add 0 to every sum.
+// V^T [D][64 + 8].  K and V are read through buffer resources bounded at
+// tk rows, so keys past tk read as zeros; they are masked to -inf, which
+// adds 0 to every sum.
+__device__ __forceinline__ uint32_t
+pack_bf16x2(float lo, float hi)
+{
+  // v_cvt_pk_bf16_f32: round to nearest even
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t,
+                            __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
+}
+
+// max of v over lanes l and l ^ 32
+__device__ __forceinline__ float
+max_halves(float v)
+{
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
+                                                  __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+
+__device__ __forceinline__ float
+sum_halves(float v)
+{
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
+                                                  __float_as_uint(v), false, false);
+  return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+
+constexpr float kLazy = 8.0f;
+
 template <int D, int MODE>
 __global__ __launch_bounds__(256, 2) void
 attention_kernel(const AttnArgs A)
@@ -1167,7 +1204,8 @@ attention_kernel(const AttnArgs A)
   const int qrow = qt * 128 + wave * 32 + lq;     // this lane's query
   const bool qvalid = qrow < A.tq;
   const int qpos = A.q_offset + qrow;
-  const float scale_log2 = 1.4426950408889634f * rsqrtf((float)D);
+  const float scale = 1.4426950408889634f * rsqrtf((float)D);
+  const float lazy = kLazy / scale;               // in raw score units
 
   i32x4_t qf[NDS];
   const uint16_t* qp = A.q + (long long)h * A.q_head + (long long)qrow * A.q_tok;
@@ -1179,8 +1217,10 @@ attention_kernel(const AttnArgs A)
   int tq_idx = 0;
   if constexpr (MODE == 2) { tq_idx = qvalid ? A.t_index[qpos] : 0; }
 
-  const uint16_t* kc = A.k + (long long)kvh * A.cap * D;
-  const uint16_t* vc = A.v + (long long)kvh * A.cap * D;
+  const __amdgpu_buffer_rsrc_t krs =
+      make_rsrc(A.k + (long long)kvh * A.cap * D, A.tk * D * 2);
+  const __amdgpu_buffer_rsrc_t vrs =
+      make_rsrc(A.v + (long long)kvh * A.cap * D, A.tk * D * 2);
 
   // ---- tile staging: global -> registers -> LDS ---------------------------
   i32x4_t kr[KPT], vr[VPT][4];
@@ -1190,9 +1230,8 @@ attention_kernel(const AttnArgs A)
     for (int i = 0; i < KPT; ++i) {
       const int idx = tid + i * 256;
       const int r = idx / KCH, c = idx % KCH;
-      kr[i] = j0 + r < A.tk
-                  ? *reinterpret_cast<const i32x4_t*>(kc + (long long)(j0 + r) * D + c * 8)
-                  : i32x4_t{0, 0, 0, 0};
+      kr[i] = __builtin_bit_cast(i32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                              krs, ((j0 + r) * D + c * 8) * 2, 0, 0));
     }
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
@@ -1200,10 +1239,9 @@ attention_kernel(const AttnArgs A)
       const int c = g % KCH, r0 = (g / KCH) * 4;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        vr[i][e] = (g < VGRP && j0 + r0 + e < A.tk)
-                       ? *reinterpret_cast<const i32x4_t*>(
-                             vc + (long long)(j0 + r0 + e) * D + c * 8)
-                       : i32x4_t{0, 0, 0, 0};
+        vr[i][e] = __builtin_bit_cast(
+            i32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                         vrs, ((j0 + r0 + e) * D + c * 8) * 2, 0, 0));
       }
     }
     if constexpr (MODE == 2) {
@@ -1245,9 +1283,11 @@ attention_kernel(const AttnArgs A)
   f32x16_t o[NCB];
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) { o[cb] = f32x16_t{}; }
-  float m = -INFINITY, l = 0.0f;
+  float m = -INFINITY;      // running max, raw score units
+  float l = 0.0f;           // this half's share of the running sum
 
   const int ntiles = (A.tk + BK - 1) / BK;
+  const int q_first = A.q_offset + qt * 128;      // workgroup's first query
   if (ntiles > 0) {
     load_tile(0);
     store_tile(0);
@@ -1258,51 +1298,59 @@ attention_kernel(const AttnArgs A)
     const int buf = t & 1;
     const int j0 = t * BK;
     // ---- scores of the tile's 64 keys for this lane's query -------------
+    f32x16_t sc[2] = {f32x16_t{}, f32x16_t{}};
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds) {
+      // rows lq and 32 + lq share their swizzle (D/8 divides 32)
+      const int off = lq * D + (((ds * 2 + half) ^ (lq % KCH)) << 3);
+      const i32x4_t k0 = *reinterpret_cast<const i32x4_t*>(&ks[buf][off]);
+      const i32x4_t k1 = *reinterpret_cast<const i32x4_t*>(&ks[buf][32 * D + off]);
+      sc[0] = MmaBf16::run(k0, qf[ds], sc[0]);
+      sc[1] = MmaBf16::run(k1, qf[ds], sc[1]);
+    }
+    // key of sc[kb][r]: j0 + kb*32 + 8*(r/4) + 4*half + r%4
     float s2[32];
-    float mb = -INFINITY;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      f32x16_t sc = f32x16_t{};
-      const int krow = kb * 32 + lq;
+    for (int r = 0; r < 16; ++r) { s2[r] = sc[0][r]; s2[16 + r] = sc[1][r]; }
+    const bool full = j0 + BK <= A.tk && (MODE == 0 || j0 + BK - 1 <= q_first);
+    if (!full) {
+      // branch-free: every lane reads its t entry (kl < 64 is in bounds)
+      // and the conditions combine bitwise, so the mask is a select
 #pragma unroll
-      for (int ds = 0; ds < NDS; ++ds) {
-        const i32x4_t kf = *reinterpret_cast<const i32x4_t*>(
-            &ks[buf][krow * D + (((ds * 2 + half) ^ (krow % KCH)) << 3)]);
-        sc = MmaBf16::run(kf, qf[ds], sc);
-      }
-      // key of sc[r]: j0 + kb*32 + 8*(r/4) + 4*half + r%4
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int kl = kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+      for (int r = 0; r < 32; ++r) {
+        const int kl = (r >> 4) * 32 + 8 * ((r & 15) >> 2) + 4 * half + (r & 3);
         const int key = j0 + kl;
         bool ok = key < A.tk;
-        if constexpr (MODE == 1) { ok = ok && key <= qpos; }
-        if constexpr (MODE == 2) { ok = ok && (key <= qpos || ts[buf][kl] == tq_idx); }
-        s2[kb * 16 + r] = ok ? sc[r] * scale_log2 : -INFINITY;
-        mb = fmaxf(mb, s2[kb * 16 + r]);
+        if constexpr (MODE == 1) { ok = ok & (key <= qpos); }
+        if constexpr (MODE == 2) {
+          const int t_key = ts[buf][kl];
+          ok = ok & ((key <= qpos) | (t_key == tq_idx));
+        }
+        s2[r] = ok ? s2[r] : -INFINITY;
       }
     }
-    mb = fmaxf(mb, __shfl_xor(mb, 32));
-    const float mn = fmaxf(m, mb);
-    const float alpha = mn == -INFINITY ? 1.0f : exp2f(m - mn);
-    float ps = 0.0f;
-    uint32_t pk[16];
+    float mb = s2[0];
 #pragma unroll
-    for (int r = 0; r < 32; r += 2) {
-      const float p0 = s2[r] == -INFINITY ? 0.0f : exp2f(s2[r] - mn);
-      const float p1 = s2[r + 1] == -INFINITY ? 0.0f : exp2f(s2[r + 1] - mn);
-      ps += p0 + p1;
-      pk[r >> 1] = bf16_bits(p0) | (bf16_bits(p1) << 16);
-    }
-    ps += __shfl_xor(ps, 32);
-    l = l * alpha + ps;
-    m = mn;
-    if (alpha != 1.0f) {
+    for (int r = 1; r < 32; ++r) { mb = fmaxf(mb, s2[r]); }
+    mb = max_halves(mb);
+    if (mb > m + lazy) {
+      const float alpha = exp2f((m - mb) * scale);     // 0 while m is -inf
+      l *= alpha;
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) { o[cb][r] *= alpha; }
       }
+      m = mb;
+    }
+    const float mc = m == -INFINITY ? 0.0f : m * scale;
+    uint32_t pk[16];
+#pragma unroll
+    for (int r = 0; r < 32; r += 2) {
+      const float p0 = __builtin_amdgcn_exp2f(fmaf(s2[r], scale, -mc));
+      const float p1 = __builtin_amdgcn_exp2f(fmaf(s2[r + 1], scale, -mc));
+      l += p0 + p1;
+      pk[r >> 1] = pack_bf16x2(p0, p1);
     }
     // ---- O^T += V^T P^T over the tile's four 16-key steps ---------------
 #pragma unroll
@@ -1324,6 +1372,7 @@ attention_kernel(const AttnArgs A)
     __syncthreads();
   }
 
+  l = sum_halves(l);
   if (!qvalid) { return; }
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
   uint16_t* op = A.out + (long long)h * A.o_head + (long long)qrow * A.o_tok;
