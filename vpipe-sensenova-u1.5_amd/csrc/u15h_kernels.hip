@@ -1137,9 +1137,13 @@ f16_to_bf16_kernel(const uint2* __restrict__ src, uint2* __restrict__ dst,
 //
 // LDS per buffer: K [64][D] with 16-byte chunk c of row r at c ^ (r % (D/8))
 // (a fragment read, 32 rows at one chunk, spreads over the bank groups);
-// V^T [D][64 + 8].  K and V are read through buffer resources bounded at
-// tk rows, so keys past tk read as zeros; they are masked to -inf, which
-// adds 0 to every sum.
+// V^T [D][64 + 8] with the 8-element block b of row d at b ^ ((d / 16) % 8).
+// A thread writes the four keys that land at V^T positions 4g..4g+3 of
+// chunk c, so each 32-lane write half covers both 8-byte halves of the
+// blocks; with the row padding and the block swizzle the V^T writes and the
+// fragment reads (32 rows at one block) hit every bank once.  K and V are
+// read through buffer resources bounded at tk rows, so keys past tk read as
+// zeros; they are masked to -inf, which adds 0 to every sum.
 __device__ __forceinline__ uint32_t
 pack_bf16x2(float lo, float hi)
 {
@@ -1168,6 +1172,23 @@ sum_halves(float v)
 }
 
 constexpr float kLazy = 8.0f;
+constexpr int kVRow = 64 + 8;                // V^T row pitch, elements
+
+// V^T element (row d, key position p)
+__device__ __forceinline__ int
+vt_at(int d, int p)
+{
+  return d * kVRow + ((((p >> 3) ^ (d >> 4)) & 7) << 3) + (p & 7);
+}
+
+// The keys stored at V^T positions p..p+3 (p a multiple of 4): within each
+// 16, position bits 2 and 3 are the key index's bits 3 and 2, the order in
+// which a lane's score fragment holds them.
+__device__ __forceinline__ int
+vt_keys(int p)
+{
+  return (p & ~15) | ((p & 8) >> 1) | ((p & 4) << 1);
+}
 
 template <int D, int MODE>
 __global__ __launch_bounds__(256, 2) void
@@ -1177,12 +1198,11 @@ attention_kernel(const AttnArgs A)
   constexpr int KCH = D / 8;                 // 16-byte chunks per K row
   constexpr int NDS = D / 16;                // MFMA K-steps of the scores
   constexpr int NCB = D / 32;                // 32-row blocks of O^T
-  constexpr int VROW = BK + 8;               // V^T row, elements
   constexpr int KPT = BK * KCH / 256;        // K chunks per thread per tile
   constexpr int VGRP = BK / 4 * KCH;         // 4-key V groups per tile
   constexpr int VPT = (VGRP + 255) / 256;    // V groups per thread
   __shared__ __attribute__((aligned(16))) uint16_t ks[2][BK * D];
-  __shared__ __attribute__((aligned(16))) uint16_t vt[2][D * VROW];
+  __shared__ __attribute__((aligned(16))) uint16_t vt[2][D * kVRow];
   __shared__ int32_t ts[2][BK];
 
   // Work item: (query head, 128-query tile), ordered kv head first, so
@@ -1236,7 +1256,7 @@ attention_kernel(const AttnArgs A)
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
       const int g = tid + i * 256;                  // (4-key group, chunk)
-      const int c = g % KCH, r0 = (g / KCH) * 4;
+      const int c = g % KCH, r0 = vt_keys((g / KCH) * 4);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         vr[i][e] = __builtin_bit_cast(
@@ -1259,9 +1279,7 @@ attention_kernel(const AttnArgs A)
     for (int i = 0; i < VPT; ++i) {
       const int g = tid + i * 256;
       if (g >= VGRP) { continue; }
-      const int c = g % KCH, r0 = (g / KCH) * 4;
-      // keys r0..r0+3 stay contiguous under the bit-2/3 exchange
-      const int pos = (r0 & ~15) | ((r0 & 8) >> 1) | ((r0 & 4) << 1);
+      const int c = g % KCH, pos = (g / KCH) * 4;
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         const uint32_t a0 = (uint32_t)vr[i][0][w], a1 = (uint32_t)vr[i][1][w];
@@ -1271,8 +1289,8 @@ attention_kernel(const AttnArgs A)
                             __builtin_amdgcn_perm(a3, a2, 0x05040100u)};
         const u32x2_t hi = {__builtin_amdgcn_perm(a1, a0, 0x07060302u),
                             __builtin_amdgcn_perm(a3, a2, 0x07060302u)};
-        *reinterpret_cast<u32x2_t*>(&vt[buf][(c * 8 + 2 * w) * VROW + pos]) = lo;
-        *reinterpret_cast<u32x2_t*>(&vt[buf][(c * 8 + 2 * w + 1) * VROW + pos]) = hi;
+        *reinterpret_cast<u32x2_t*>(&vt[buf][vt_at(c * 8 + 2 * w, pos)]) = lo;
+        *reinterpret_cast<u32x2_t*>(&vt[buf][vt_at(c * 8 + 2 * w + 1, pos)]) = hi;
       }
     }
     if constexpr (MODE == 2) {
@@ -1360,7 +1378,7 @@ attention_kernel(const AttnArgs A)
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) {
         const i32x4_t vf = *reinterpret_cast<const i32x4_t*>(
-            &vt[buf][(cb * 32 + lq) * VROW + k4 * 16 + half * 8]);
+            &vt[buf][vt_at(cb * 32 + lq, k4 * 16 + half * 8)]);
         o[cb] = MmaBf16::run(vf, pf, o[cb]);
       }
     }
