@@ -1109,10 +1109,7 @@ f16_to_bf16_kernel(const uint2* __restrict__ src, uint2* __restrict__ dst,
 
 // ---- flash attention ------------------------------------------------------
 // Grouped-query attention over a K/V cache, one workgroup per 128 queries
-// of one head (four waves of 32), keys streamed in tiles of 64 through a
-// double-buffered LDS stage: the next tile is loaded into registers while
-// the current one is computed, then written to the other buffer; one
-// barrier per tile.
+// of one head (four waves of 32), keys streamed in tiles of 64.
 //
 // The score tile is computed TRANSPOSED, S^T = K Q^T, with the key
 // fragment as the MFMA's first operand: a lane then holds 32 scores (two
@@ -1121,11 +1118,21 @@ f16_to_bf16_kernel(const uint2* __restrict__ src, uint2* __restrict__ dst,
 // one scalar per lane.  The output is accumulated transposed too,
 // O^T = V^T P^T: the second operand is P^T, whose lane layout (8 keys of
 // one query) is exactly the lane's own probabilities when the keys of each
-// 16 are taken in the order the score layout holds them; the V tile is
-// stored transposed in LDS with that key order (bits 2 and 3 of the key
-// index exchanged), so a lane reads its 8 keys as one 16-byte fragment.
-// The transpose is done four keys at a time in registers (byte permutes),
-// so each 16-byte global chunk becomes eight 8-byte LDS writes.
+// 16 are taken in the order the score layout holds them (key 8*(e/4) +
+// 4*half + e%4 at operand position 8*half + e).  The first operand, V^T,
+// comes from V in its natural [key][dim] layout by LDS transpose reads:
+// ds_read_b64_tr_b16 hands lane B+i of each 16-lane group element i%4 of
+// the 4-element chunks addressed by lanes B + i/4 + 4j, j = 0..3, so lane
+// s addresses dims 16*((s/16)%2) + 4*(s%4) of key 4*half + (s%16)/4 (and
+// that key + 8 for the second read).
+//
+// Software pipeline, one barrier per tile: iteration t takes the scores of
+// tile t+1 (MFMA) while it exponentiates tile t (VALU), then accumulates
+// tile t's P V; K of tile t+2 and V of tile t+1 are copied global -> LDS
+// directly (no registers) meanwhile.  Each buffer is its own __shared__
+// object and the loop is unrolled by two so every buffer choice is static:
+// the compiler then knows a copy into one buffer does not alias reads of
+// the other and does not hold those reads until the copy lands.
 //
 // The softmax work per score is one FMA (scale and running max), one
 // exp2, one add and half a bf16 pack; a tile needing no mask (every key
@@ -1135,15 +1142,14 @@ f16_to_bf16_kernel(const uint2* __restrict__ src, uint2* __restrict__ dst,
 // exp2((s - m) * scale) <= 2^kLazy, and the output and the sum share the
 // same m, so the quotient is unchanged while most tiles skip the rescale.
 //
-// LDS per buffer: K [64][D] with 16-byte chunk c of row r at c ^ (r % (D/8))
-// (a fragment read, 32 rows at one chunk, spreads over the bank groups);
-// V^T [D][64 + 8] with the 8-element block b of row d at b ^ ((d / 16) % 8).
-// A thread writes the four keys that land at V^T positions 4g..4g+3 of
-// chunk c, so each 32-lane write half covers both 8-byte halves of the
-// blocks; with the row padding and the block swizzle the V^T writes and the
-// fragment reads (32 rows at one block) hit every bank once.  K and V are
-// read through buffer resources bounded at tk rows, so keys past tk read as
-// zeros; they are masked to -inf, which adds 0 to every sum.
+// LDS layouts (per buffer): K [64][D] with 16-byte chunk c of row r at
+// c ^ (r % (D/8)), so a fragment read (32 rows at one chunk) spreads over
+// the banks; V [64][D] with 64-byte block b of row r at b ^ vswz(r), so
+// the transpose reads (4 rows x 64 bytes per half-wave) hit every bank
+// once.  The copies place each lane's 16 bytes at its landing slot and
+// fetch the chunk the swizzle puts there.  K and V are read through
+// buffer resources bounded at tk keys: keys past tk read as zeros and are
+// masked to -inf, which adds 0 to every sum.
 __device__ __forceinline__ uint32_t
 pack_bf16x2(float lo, float hi)
 {
@@ -1172,38 +1178,36 @@ sum_halves(float v)
 }
 
 constexpr float kLazy = 8.0f;
-constexpr int kVRow = 64 + 8;                // V^T row pitch, elements
 
-// V^T element (row d, key position p)
+// 64-byte block swizzle of V row r: four consecutive rows at one block
+// land on four different 64-byte bank ranges
+template <int D>
 __device__ __forceinline__ int
-vt_at(int d, int p)
+vswz(int r)
 {
-  return d * kVRow + ((((p >> 3) ^ (d >> 4)) & 7) << 3) + (p & 7);
+  return (r * (D / 32) / 4) % (D / 32);
 }
 
-// The keys stored at V^T positions p..p+3 (p a multiple of 4): within each
-// 16, position bits 2 and 3 are the key index's bits 3 and 2, the order in
-// which a lane's score fragment holds them.
-__device__ __forceinline__ int
-vt_keys(int p)
-{
-  return (p & ~15) | ((p & 8) >> 1) | ((p & 4) << 1);
-}
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef short i16x2_t __attribute__((ext_vector_type(2)));
 
 template <int D, int MODE>
 __global__ __launch_bounds__(256, 2) void
 attention_kernel(const AttnArgs A)
 {
   constexpr int BK = 64;
-  constexpr int KCH = D / 8;                 // 16-byte chunks per K row
+  constexpr int KCH = D / 8;                 // 16-byte chunks per row
   constexpr int NDS = D / 16;                // MFMA K-steps of the scores
   constexpr int NCB = D / 32;                // 32-row blocks of O^T
-  constexpr int KPT = BK * KCH / 256;        // K chunks per thread per tile
-  constexpr int VGRP = BK / 4 * KCH;         // 4-key V groups per tile
-  constexpr int VPT = (VGRP + 255) / 256;    // V groups per thread
-  __shared__ __attribute__((aligned(16))) uint16_t ks[2][BK * D];
-  __shared__ __attribute__((aligned(16))) uint16_t vt[2][D * kVRow];
-  __shared__ int32_t ts[2][BK];
+  constexpr int CPW = D / 32;                // 1 KiB copies per wave per tile
+  // Tile j's K sits in ks<j & 1>, its V in vs<j & 1>, its t entries in
+  // ts[j % 3]: iteration t reads K of tile t+1, V and t of tile t, and
+  // writes K of tile t+2, V of tile t+1, t of tile t+2.
+  __shared__ __attribute__((aligned(16))) uint16_t ks0[BK * D];
+  __shared__ __attribute__((aligned(16))) uint16_t ks1[BK * D];
+  __shared__ __attribute__((aligned(16))) uint16_t vs0[BK * D];
+  __shared__ __attribute__((aligned(16))) uint16_t vs1[BK * D];
+  __shared__ int32_t ts[3][BK];
 
   // Work item: (query head, 128-query tile), ordered kv head first, so
   // that cutting the list into 8 runs (one per XCD, workgroups b, b+8, ...
@@ -1241,95 +1245,66 @@ attention_kernel(const AttnArgs A)
       make_rsrc(A.k + (long long)kvh * A.cap * D, A.tk * D * 2);
   const __amdgpu_buffer_rsrc_t vrs =
       make_rsrc(A.v + (long long)kvh * A.cap * D, A.tk * D * 2);
+  const __amdgpu_buffer_rsrc_t trs =
+      make_rsrc(A.t_index, MODE == 2 ? A.tk * 4 : 0);   // read in mode 2 only
 
-  // ---- tile staging: global -> registers -> LDS ---------------------------
-  i32x4_t kr[KPT], vr[VPT][4];
+  // ---- tile copies: global -> LDS ------------------------------------------
   int32_t tr = 0;
-  auto load_tile = [&](int j0) {
+  auto copy_k = [&](int j0, uint16_t* dst_tile) {
+    char* dst = reinterpret_cast<char*>(dst_tile) + wave * CPW * 1024;
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      const int idx = tid + i * 256;
-      const int r = idx / KCH, c = idx % KCH;
-      kr[i] = __builtin_bit_cast(i32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                              krs, ((j0 + r) * D + c * 8) * 2, 0, 0));
-    }
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      const int g = tid + i * 256;                  // (4-key group, chunk)
-      const int c = g % KCH, r0 = vt_keys((g / KCH) * 4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        vr[i][e] = __builtin_bit_cast(
-            i32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                         vrs, ((j0 + r0 + e) * D + c * 8) * 2, 0, 0));
-      }
+    for (int i = 0; i < CPW; ++i) {
+      const int idx = (wave * CPW + i) * 64 + lane;   // landing chunk
+      const int r = idx / KCH, c = (idx % KCH) ^ (r % KCH);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          krs, (__attribute__((address_space(3))) void*)(dst + i * 1024), 16,
+          ((j0 + r) * D + c * 8) * 2, 0, 0, 0);
     }
     if constexpr (MODE == 2) {
-      if (tid < BK) { tr = j0 + tid < A.tk ? A.t_index[j0 + tid] : 0; }
+      tr = (int)__builtin_amdgcn_raw_buffer_load_b32(trs, (j0 + (tid & 63)) * 4, 0, 0);
     }
   };
-  auto store_tile = [&](int buf) {
+  auto copy_v = [&](int j0, uint16_t* dst_tile) {
+    char* dst = reinterpret_cast<char*>(dst_tile) + wave * CPW * 1024;
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      const int idx = tid + i * 256;
-      const int r = idx / KCH, c = idx % KCH;
-      *reinterpret_cast<i32x4_t*>(&ks[buf][r * D + ((c ^ (r % KCH)) << 3)]) = kr[i];
+    for (int i = 0; i < CPW; ++i) {
+      const int idx = (wave * CPW + i) * 64 + lane;
+      const int r = idx / KCH, c = (idx % KCH) ^ (4 * vswz<D>(r));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          vrs, (__attribute__((address_space(3))) void*)(dst + i * 1024), 16,
+          ((j0 + r) * D + c * 8) * 2, 0, 0, 0);
     }
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      const int g = tid + i * 256;
-      if (g >= VGRP) { continue; }
-      const int c = g % KCH, pos = (g / KCH) * 4;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const uint32_t a0 = (uint32_t)vr[i][0][w], a1 = (uint32_t)vr[i][1][w];
-        const uint32_t a2 = (uint32_t)vr[i][2][w], a3 = (uint32_t)vr[i][3][w];
-        // element 2w of keys 0..3, then element 2w+1
-        const u32x2_t lo = {__builtin_amdgcn_perm(a1, a0, 0x05040100u),
-                            __builtin_amdgcn_perm(a3, a2, 0x05040100u)};
-        const u32x2_t hi = {__builtin_amdgcn_perm(a1, a0, 0x07060302u),
-                            __builtin_amdgcn_perm(a3, a2, 0x07060302u)};
-        *reinterpret_cast<u32x2_t*>(&vt[buf][vt_at(c * 8 + 2 * w, pos)]) = lo;
-        *reinterpret_cast<u32x2_t*>(&vt[buf][vt_at(c * 8 + 2 * w + 1, pos)]) = hi;
-      }
-    }
+  };
+  auto store_t = [&](int tbuf) {
     if constexpr (MODE == 2) {
-      if (tid < BK) { ts[buf][tid] = tr; }
+      if (tid < BK) { ts[tbuf][tid] = tr; }
     }
   };
+
+  // per-lane fragment offsets (elements)
+  const int koff = lq * D;                             // + swizzled chunk
+  const int vrow = 4 * half + ((lane & 15) >> 2);      // transpose-read key
+  const int vcol = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
   f32x16_t o[NCB];
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) { o[cb] = f32x16_t{}; }
   float m = -INFINITY;      // running max, raw score units
   float l = 0.0f;           // this half's share of the running sum
+  f32x16_t sc[2];
 
   const int ntiles = (A.tk + BK - 1) / BK;
   const int q_first = A.q_offset + qt * 128;      // workgroup's first query
-  if (ntiles > 0) {
-    load_tile(0);
-    store_tile(0);
-    if (ntiles > 1) { load_tile(BK); }
-    __syncthreads();
-  }
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
+
+  // One iteration; KB / VB are the static buffers of tile t+1's K and
+  // tile t's V.
+  auto iteration = [&](int t, const uint16_t* kread, uint16_t* kfill,
+                       const uint16_t* vread, uint16_t* vfill) {
     const int j0 = t * BK;
-    // ---- scores of the tile's 64 keys for this lane's query -------------
-    f32x16_t sc[2] = {f32x16_t{}, f32x16_t{}};
-#pragma unroll
-    for (int ds = 0; ds < NDS; ++ds) {
-      // rows lq and 32 + lq share their swizzle (D/8 divides 32)
-      const int off = lq * D + (((ds * 2 + half) ^ (lq % KCH)) << 3);
-      const i32x4_t k0 = *reinterpret_cast<const i32x4_t*>(&ks[buf][off]);
-      const i32x4_t k1 = *reinterpret_cast<const i32x4_t*>(&ks[buf][32 * D + off]);
-      sc[0] = MmaBf16::run(k0, qf[ds], sc[0]);
-      sc[1] = MmaBf16::run(k1, qf[ds], sc[1]);
-    }
+    copy_k((t + 2) * BK, kfill);        // past the last tile: zeros, unread
+    copy_v((t + 1) * BK, vfill);
+    // ---- mask and max of tile t's scores ---------------------------------
     // key of sc[kb][r]: j0 + kb*32 + 8*(r/4) + 4*half + r%4
-    float s2[32];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) { s2[r] = sc[0][r]; s2[16 + r] = sc[1][r]; }
     const bool full = j0 + BK <= A.tk && (MODE == 0 || j0 + BK - 1 <= q_first);
     if (!full) {
       // branch-free: every lane reads its t entry (kl < 64 is in bounds)
@@ -1341,15 +1316,15 @@ attention_kernel(const AttnArgs A)
         bool ok = key < A.tk;
         if constexpr (MODE == 1) { ok = ok & (key <= qpos); }
         if constexpr (MODE == 2) {
-          const int t_key = ts[buf][kl];
+          const int t_key = ts[t % 3][kl];
           ok = ok & ((key <= qpos) | (t_key == tq_idx));
         }
-        s2[r] = ok ? s2[r] : -INFINITY;
+        sc[r >> 4][r & 15] = ok ? sc[r >> 4][r & 15] : -INFINITY;
       }
     }
-    float mb = s2[0];
+    float mb = sc[0][0];
 #pragma unroll
-    for (int r = 1; r < 32; ++r) { mb = fmaxf(mb, s2[r]); }
+    for (int r = 1; r < 32; ++r) { mb = fmaxf(mb, sc[r >> 4][r & 15]); }
     mb = max_halves(mb);
     if (mb > m + lazy) {
       const float alpha = exp2f((m - mb) * scale);     // 0 while m is -inf
@@ -1362,32 +1337,80 @@ attention_kernel(const AttnArgs A)
       m = mb;
     }
     const float mc = m == -INFINITY ? 0.0f : m * scale;
+
+    // ---- tile t+1's scores (MFMA) beside tile t's exponentials (VALU) ----
+    // (past the last tile the scores come from stale K and are dropped)
+    constexpr int EPS = 32 / NDS;               // exponentials per K-step
+    f32x16_t sn[2] = {f32x16_t{}, f32x16_t{}};
     uint32_t pk[16];
+    float ps = 0.0f;
 #pragma unroll
-    for (int r = 0; r < 32; r += 2) {
-      const float p0 = __builtin_amdgcn_exp2f(fmaf(s2[r], scale, -mc));
-      const float p1 = __builtin_amdgcn_exp2f(fmaf(s2[r + 1], scale, -mc));
-      l += p0 + p1;
-      pk[r >> 1] = pack_bf16x2(p0, p1);
+    for (int ds = 0; ds < NDS; ++ds) {
+      const int off = koff + (((ds * 2 + half) ^ (lq % KCH)) << 3);
+      const i32x4_t k0 = *reinterpret_cast<const i32x4_t*>(kread + off);
+      const i32x4_t k1 = *reinterpret_cast<const i32x4_t*>(kread + 32 * D + off);
+      sn[0] = MmaBf16::run(k0, qf[ds], sn[0]);
+      sn[1] = MmaBf16::run(k1, qf[ds], sn[1]);
+#pragma unroll
+      for (int e = 0; e < EPS; e += 2) {
+        const int r = ds * EPS + e;
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[r >> 4][r & 15], scale, -mc));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[r >> 4][(r & 15) + 1], scale, -mc));
+        ps += p0 + p1;
+        pk[r >> 1] = pack_bf16x2(p0, p1);
+      }
     }
-    // ---- O^T += V^T P^T over the tile's four 16-key steps ---------------
+    l += ps;
+
+    // ---- O^T += V^T P^T over the tile's four 16-key steps ----------------
 #pragma unroll
     for (int k4 = 0; k4 < 4; ++k4) {
       const i32x4_t pf = {(int)pk[k4 * 4 + 0], (int)pk[k4 * 4 + 1],
                           (int)pk[k4 * 4 + 2], (int)pk[k4 * 4 + 3]};
+      const int r0 = k4 * 16 + vrow;
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) {
-        const i32x4_t vf = *reinterpret_cast<const i32x4_t*>(
-            &vt[buf][vt_at(cb * 32 + lq, k4 * 16 + half * 8)]);
+        const int c = (((cb ^ vswz<D>(r0)) << 5) | vcol);   // r0, r0+8 share it
+        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4_t*)(vread + r0 * D + c));
+        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4_t*)(vread + (r0 + 8) * D + c));
+        const i32x4_t vf = {__builtin_bit_cast(int, (i16x2_t){lo[0], lo[1]}),
+                            __builtin_bit_cast(int, (i16x2_t){lo[2], lo[3]}),
+                            __builtin_bit_cast(int, (i16x2_t){hi[0], hi[1]}),
+                            __builtin_bit_cast(int, (i16x2_t){hi[2], hi[3]})};
         o[cb] = MmaBf16::run(vf, pf, o[cb]);
       }
     }
-    // ---- the next tile into the other buffer, the one after into regs ---
-    if (t + 1 < ntiles) {
-      store_tile(buf ^ 1);
-      if (t + 2 < ntiles) { load_tile((t + 2) * BK); }
+    store_t((t + 2) % 3);
+    __syncthreads();
+    sc[0] = sn[0];
+    sc[1] = sn[1];
+  };
+
+  if (ntiles > 0) {
+    // K and t of tiles 0 and 1, V of tile 0; the scores of tile 0, read
+    // by every wave before the first iteration refills ks0
+    copy_k(0, ks0);
+    store_t(0);
+    copy_k(BK, ks1);
+    store_t(1);
+    copy_v(0, vs0);
+    __syncthreads();
+    sc[0] = f32x16_t{};
+    sc[1] = f32x16_t{};
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds) {
+      const int off = koff + (((ds * 2 + half) ^ (lq % KCH)) << 3);
+      sc[0] = MmaBf16::run(*reinterpret_cast<const i32x4_t*>(ks0 + off), qf[ds], sc[0]);
+      sc[1] = MmaBf16::run(*reinterpret_cast<const i32x4_t*>(ks0 + 32 * D + off),
+                           qf[ds], sc[1]);
     }
     __syncthreads();
+  }
+  for (int t = 0; t < ntiles; t += 2) {
+    iteration(t, ks1, ks0, vs0, vs1);
+    if (t + 1 < ntiles) { iteration(t + 1, ks0, ks1, vs1, vs0); }
   }
 
   l = sum_halves(l);
