@@ -1221,7 +1221,7 @@ attention_kernel(const AttnArgs A)
   const int kvh = h / (A.hq / A.hkv);
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
   const int lane = tid & 63;
   const int lq = lane & 31;
   const int half = lane >> 5;
@@ -1241,38 +1241,50 @@ attention_kernel(const AttnArgs A)
   int tq_idx = 0;
   if constexpr (MODE == 2) { tq_idx = qvalid ? A.t_index[qpos] : 0; }
 
-  const __amdgpu_buffer_rsrc_t krs =
-      make_rsrc(A.k + (long long)kvh * A.cap * D, A.tk * D * 2);
-  const __amdgpu_buffer_rsrc_t vrs =
-      make_rsrc(A.v + (long long)kvh * A.cap * D, A.tk * D * 2);
-  const __amdgpu_buffer_rsrc_t trs =
-      make_rsrc(A.t_index, MODE == 2 ? A.tk * 4 : 0);   // read in mode 2 only
-
   // ---- tile copies: global -> LDS ------------------------------------------
+  // Each copy reads through a buffer resource based at the tile's first key
+  // whose range ends at key tk: keys past tk read as zeros, and the
+  // per-lane offsets (landing slot -> swizzled source chunk) are the same
+  // for every tile.  Instruction i of a wave fills 1 KiB of the tile (64
+  // lanes x 16 bytes).
+  const uint16_t* kbase = A.k + (long long)kvh * A.cap * D;
+  const uint16_t* vbase = A.v + (long long)kvh * A.cap * D;
+  // (vectors, not arrays: a lambda capturing a local array of template-
+  // dependent size loses the kernel's host-side launch stub)
+  static_assert(CPW <= 4, "copy offsets hold four instructions");
+  i32x4_t koffs = {}, voffs = {};
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) {
+    const int idx = (wave * CPW + i) * 64 + lane;     // landing chunk
+    const int r = idx / KCH;
+    koffs[i] = (r * D + (((idx % KCH) ^ (r % KCH)) << 3)) * 2;
+    voffs[i] = (r * D + (((idx % KCH) ^ (4 * vswz<D>(r))) << 3)) * 2;
+  }
   int32_t tr = 0;
   auto copy_k = [&](int j0, uint16_t* dst_tile) {
+    const int left = max(A.tk - j0, 0);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(kbase + (long long)j0 * D, left * D * 2);
     char* dst = reinterpret_cast<char*>(dst_tile) + wave * CPW * 1024;
 #pragma unroll
     for (int i = 0; i < CPW; ++i) {
-      const int idx = (wave * CPW + i) * 64 + lane;   // landing chunk
-      const int r = idx / KCH, c = (idx % KCH) ^ (r % KCH);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          krs, (__attribute__((address_space(3))) void*)(dst + i * 1024), 16,
-          ((j0 + r) * D + c * 8) * 2, 0, 0, 0);
+          rs, (__attribute__((address_space(3))) void*)(dst + i * 1024), 16, koffs[i],
+          0, 0, 0);
     }
     if constexpr (MODE == 2) {
-      tr = (int)__builtin_amdgcn_raw_buffer_load_b32(trs, (j0 + (tid & 63)) * 4, 0, 0);
+      const __amdgpu_buffer_rsrc_t ts_rs = make_rsrc(A.t_index + j0, left * 4);
+      tr = (int)__builtin_amdgcn_raw_buffer_load_b32(ts_rs, (tid & 63) * 4, 0, 0);
     }
   };
   auto copy_v = [&](int j0, uint16_t* dst_tile) {
+    const int left = max(A.tk - j0, 0);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(vbase + (long long)j0 * D, left * D * 2);
     char* dst = reinterpret_cast<char*>(dst_tile) + wave * CPW * 1024;
 #pragma unroll
     for (int i = 0; i < CPW; ++i) {
-      const int idx = (wave * CPW + i) * 64 + lane;
-      const int r = idx / KCH, c = (idx % KCH) ^ (4 * vswz<D>(r));
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          vrs, (__attribute__((address_space(3))) void*)(dst + i * 1024), 16,
-          ((j0 + r) * D + c * 8) * 2, 0, 0, 0);
+          rs, (__attribute__((address_space(3))) void*)(dst + i * 1024), 16, voffs[i],
+          0, 0, 0);
     }
   };
   auto store_t = [&](int tbuf) {
@@ -1291,41 +1303,77 @@ attention_kernel(const AttnArgs A)
   for (int cb = 0; cb < NCB; ++cb) { o[cb] = f32x16_t{}; }
   float m = -INFINITY;      // running max, raw score units
   float l = 0.0f;           // this half's share of the running sum
-  f32x16_t sc[2];
+  f32x16_t sc[2];           // scores of the current tile
+  float mb = -INFINITY;     // their max over the row (both halves)
 
   const int ntiles = (A.tk + BK - 1) / BK;
   const int q_first = A.q_offset + qt * 128;      // workgroup's first query
 
-  // One iteration; KB / VB are the static buffers of tile t+1's K and
-  // tile t's V.
+  // -inf for the scores of tile j0 that the mode hides; a no-op for a tile
+  // whose keys are all below tk and (causal masks) the first query
+  auto mask = [&](f32x16_t (&s)[2], int j0, int tbuf) {
+    const bool full = j0 + BK <= A.tk && (MODE == 0 || j0 + BK - 1 <= q_first);
+    if (full) { return; }
+    // branch-free: every lane reads its t entry (kl < 64 is in bounds) and
+    // the conditions combine bitwise, so the mask is a select
+#pragma unroll
+    for (int r = 0; r < 32; ++r) {
+      const int kl = (r >> 4) * 32 + 8 * ((r & 15) >> 2) + 4 * half + (r & 3);
+      const int key = j0 + kl;
+      bool ok = key < A.tk;
+      if constexpr (MODE == 1) { ok = ok & (key <= qpos); }
+      if constexpr (MODE == 2) {
+        const int t_key = ts[tbuf][kl];
+        ok = ok & ((key <= qpos) | (t_key == tq_idx));
+      }
+      s[r >> 4][r & 15] = ok ? s[r >> 4][r & 15] : -INFINITY;
+    }
+  };
+  // one probability pair: exp2((s - m) * scale), packed to bf16 and
+  // summed as packed (one dot with (1, 1)): the sum then counts exactly
+  // the rounded weights the P V product uses
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  uint32_t pk[16];
+  float ps;
+  float mc;
+  auto expo = [&](const f32x16_t& s, int r, int slot) {
+    const float p0 = __builtin_amdgcn_exp2f(fmaf(s[r], scale, -mc));
+    const float p1 = __builtin_amdgcn_exp2f(fmaf(s[r + 1], scale, -mc));
+    pk[slot] = pack_bf16x2(p0, p1);
+    ps = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk[slot]),
+                                         __builtin_bit_cast(bf16x2_t, 0x3f803f80u), ps,
+                                         false);
+  };
+  // O^T block cb += V^T (16-key step k4) P^T
+  auto pv = [&](const uint16_t* vread, int k4, int cb) {
+    const i32x4_t pf = {(int)pk[k4 * 4 + 0], (int)pk[k4 * 4 + 1],
+                        (int)pk[k4 * 4 + 2], (int)pk[k4 * 4 + 3]};
+    const int r0 = k4 * 16 + vrow;
+    const int c = (((cb ^ vswz<D>(r0)) << 5) | vcol);     // r0, r0+8 share it
+    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) i16x4_t*)(vread + r0 * D + c));
+    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) i16x4_t*)(vread + (r0 + 8) * D + c));
+    const i32x4_t vf = {__builtin_bit_cast(int, (i16x2_t){lo[0], lo[1]}),
+                        __builtin_bit_cast(int, (i16x2_t){lo[2], lo[3]}),
+                        __builtin_bit_cast(int, (i16x2_t){hi[0], hi[1]}),
+                        __builtin_bit_cast(int, (i16x2_t){hi[2], hi[3]})};
+    o[cb] = MmaBf16::run(vf, pf, o[cb]);
+  };
+
+  // One iteration over tile t, in three sections that each pair MFMA work
+  // with VALU work of about the same length:
+  //   A  scores of tile t+1 (16 MFMA)   | exponentials of keys 0..31
+  //   B  P V of keys 0..31 (8 MFMA)     | exponentials of keys 32..63
+  //   C  P V of keys 32..63 (8 MFMA)    | max of tile t+1's scores
+  // kread / kfill are tile t+1's and tile t+2's K buffers, vread / vfill
+  // tile t's and tile t+1's V buffers.
+  constexpr int EPA = 16 / NDS;               // probabilities per K-step (A)
+  constexpr int EPB = 16 / (2 * NCB);         // probabilities per MFMA (B)
+  constexpr int MPC = 32 / (2 * NCB);         // maxed scores per MFMA (C)
   auto iteration = [&](int t, const uint16_t* kread, uint16_t* kfill,
                        const uint16_t* vread, uint16_t* vfill) {
     const int j0 = t * BK;
-    copy_k((t + 2) * BK, kfill);        // past the last tile: zeros, unread
-    copy_v((t + 1) * BK, vfill);
-    // ---- mask and max of tile t's scores ---------------------------------
-    // key of sc[kb][r]: j0 + kb*32 + 8*(r/4) + 4*half + r%4
-    const bool full = j0 + BK <= A.tk && (MODE == 0 || j0 + BK - 1 <= q_first);
-    if (!full) {
-      // branch-free: every lane reads its t entry (kl < 64 is in bounds)
-      // and the conditions combine bitwise, so the mask is a select
-#pragma unroll
-      for (int r = 0; r < 32; ++r) {
-        const int kl = (r >> 4) * 32 + 8 * ((r & 15) >> 2) + 4 * half + (r & 3);
-        const int key = j0 + kl;
-        bool ok = key < A.tk;
-        if constexpr (MODE == 1) { ok = ok & (key <= qpos); }
-        if constexpr (MODE == 2) {
-          const int t_key = ts[t % 3][kl];
-          ok = ok & ((key <= qpos) | (t_key == tq_idx));
-        }
-        sc[r >> 4][r & 15] = ok ? sc[r >> 4][r & 15] : -INFINITY;
-      }
-    }
-    float mb = sc[0][0];
-#pragma unroll
-    for (int r = 1; r < 32; ++r) { mb = fmaxf(mb, sc[r >> 4][r & 15]); }
-    mb = max_halves(mb);
     if (mb > m + lazy) {
       const float alpha = exp2f((m - mb) * scale);     // 0 while m is -inf
       l *= alpha;
@@ -1336,52 +1384,74 @@ attention_kernel(const AttnArgs A)
       }
       m = mb;
     }
-    const float mc = m == -INFINITY ? 0.0f : m * scale;
+    mc = m == -INFINITY ? 0.0f : m * scale;
+    ps = 0.0f;
+    copy_k((t + 2) * BK, kfill);        // past the last tile: zeros, unread
+    copy_v((t + 1) * BK, vfill);
 
-    // ---- tile t+1's scores (MFMA) beside tile t's exponentials (VALU) ----
+    // ---- A --------------------------------------------------------------
     // (past the last tile the scores come from stale K and are dropped)
-    constexpr int EPS = 32 / NDS;               // exponentials per K-step
     f32x16_t sn[2] = {f32x16_t{}, f32x16_t{}};
-    uint32_t pk[16];
-    float ps = 0.0f;
 #pragma unroll
     for (int ds = 0; ds < NDS; ++ds) {
       const int off = koff + (((ds * 2 + half) ^ (lq % KCH)) << 3);
       const i32x4_t k0 = *reinterpret_cast<const i32x4_t*>(kread + off);
       const i32x4_t k1 = *reinterpret_cast<const i32x4_t*>(kread + 32 * D + off);
       sn[0] = MmaBf16::run(k0, qf[ds], sn[0]);
+#pragma unroll
+      for (int e = 0; e < EPA; e += 2) { expo(sc[0], ds * EPA + e, (ds * EPA + e) >> 1); }
       sn[1] = MmaBf16::run(k1, qf[ds], sn[1]);
-#pragma unroll
-      for (int e = 0; e < EPS; e += 2) {
-        const int r = ds * EPS + e;
-        const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[r >> 4][r & 15], scale, -mc));
-        const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[r >> 4][(r & 15) + 1], scale, -mc));
-        ps += p0 + p1;
-        pk[r >> 1] = pack_bf16x2(p0, p1);
-      }
     }
-    l += ps;
-
-    // ---- O^T += V^T P^T over the tile's four 16-key steps ----------------
+    // ---- B --------------------------------------------------------------
 #pragma unroll
-    for (int k4 = 0; k4 < 4; ++k4) {
-      const i32x4_t pf = {(int)pk[k4 * 4 + 0], (int)pk[k4 * 4 + 1],
-                          (int)pk[k4 * 4 + 2], (int)pk[k4 * 4 + 3]};
-      const int r0 = k4 * 16 + vrow;
+    for (int k4 = 0; k4 < 2; ++k4) {
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) {
-        const int c = (((cb ^ vswz<D>(r0)) << 5) | vcol);   // r0, r0+8 share it
-        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) i16x4_t*)(vread + r0 * D + c));
-        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) i16x4_t*)(vread + (r0 + 8) * D + c));
-        const i32x4_t vf = {__builtin_bit_cast(int, (i16x2_t){lo[0], lo[1]}),
-                            __builtin_bit_cast(int, (i16x2_t){lo[2], lo[3]}),
-                            __builtin_bit_cast(int, (i16x2_t){hi[0], hi[1]}),
-                            __builtin_bit_cast(int, (i16x2_t){hi[2], hi[3]})};
-        o[cb] = MmaBf16::run(vf, pf, o[cb]);
+        pv(vread, k4, cb);
+        const int r = (k4 * NCB + cb) * EPB;
+#pragma unroll
+        for (int e = 0; e < EPB; e += 2) { expo(sc[1], r + e, 8 + ((r + e) >> 1)); }
       }
     }
+    // schedule A and B: each step's LDS reads one step ahead of its MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);                // reads 0, 1
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);              // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 6 * EPA / 4, 0);    // VALU
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);              // reads +2
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);              // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 6 * EPA / 4, 0);    // VALU
+    }
+#pragma unroll
+    for (int i = 0; i < 2 * NCB; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);              // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 6 * EPB / 4, 0);    // VALU
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);              // reads +2
+      __builtin_amdgcn_sched_group_barrier(0x002, 6 * EPB / 4, 0);    // VALU
+    }
+    // ---- C --------------------------------------------------------------
+    mask(sn, j0 + BK, (t + 1) % 3);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int k4 = 2; k4 < 4; ++k4) {
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) {
+        pv(vread, k4, cb);
+        const int r = ((k4 - 2) * NCB + cb) * MPC;
+#pragma unroll
+        for (int e = 0; e < MPC; ++e) { mx = fmaxf(mx, sn[(r + e) >> 4][(r + e) & 15]); }
+      }
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);                // reads 0, 1
+#pragma unroll
+    for (int i = 0; i < 2 * NCB; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);              // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, MPC / 2, 0);        // VALU
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);              // reads +2
+    }
+    mb = max_halves(mx);
+    l += ps;
     store_t((t + 2) % 3);
     __syncthreads();
     sc[0] = sn[0];
@@ -1406,6 +1476,11 @@ attention_kernel(const AttnArgs A)
       sc[1] = MmaBf16::run(*reinterpret_cast<const i32x4_t*>(ks0 + 32 * D + off),
                            qf[ds], sc[1]);
     }
+    mask(sc, 0, 0);
+    float mx = sc[0][0];
+#pragma unroll
+    for (int r = 1; r < 32; ++r) { mx = fmaxf(mx, sc[r >> 4][r & 15]); }
+    mb = max_halves(mx);
     __syncthreads();
   }
   for (int t = 0; t < ntiles; t += 2) {
