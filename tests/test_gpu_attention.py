@@ -205,3 +205,64 @@ def test_attention_rejects_bad_shapes(ops):
     assert L.u15h_sdpa(c, s, p(q), p(k), p(k), p(o), 4, 2, 8, 8, 96, 16, 0, 0) == u15h.EINVAL
     assert L.u15h_sdpa_block_causal(c, s, p(q), p(k), p(k), p(o), None, 4, 2,
                                     8, 8, 128, 16, 0) == u15h.EINVAL
+
+
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("mode", ["bidirectional", "causal", "block_causal"])
+@pytest.mark.parametrize("tk", [1, 63, 64, 65, 128, 192, 257])
+def test_tile_counts_head_dims_and_masks(ops, d, mode, tk):
+    """Every head_dim the entry points accept, every mask, and key counts
+    giving 1, 2, 3, 4 and 5 key tiles, partial and whole: the pipelined
+    loop runs tiles in pairs and prefetches two ahead.  Queries are the
+    last tq keys (q_offset = tk - tq), as in a generation block."""
+    hq, hkv = 8, 2
+    tq = min(tk, 70)
+    pre = tk - tq
+    cap = tk + 9
+    rng = np.random.default_rng(d * 1000 + tk)
+    qb = oracle.f32_to_bf16(rng.standard_normal((hq, tq, d)).astype(np.float32))
+    kb = bf16_cache(rng.standard_normal((hkv, tk, d)).astype(np.float32), cap)
+    vb = bf16_cache(rng.standard_normal((hkv, tk, d)).astype(np.float32), cap)
+    # image-like blocks of 5 keys sharing a t, after a text prefix
+    t_idx = np.concatenate([np.arange(pre), pre + np.arange(tq) // 5]).astype(np.int32)
+    q = dev_bf16(qb)
+    out = torch.empty_like(q)
+    if mode == "block_causal":
+        ops.sdpa_block_causal(q, dev_bf16(kb), dev_bf16(vb), out,
+                              torch.from_numpy(t_idx).cuda(), hkv, tk, pre)
+    else:
+        ops.sdpa(q, dev_bf16(kb), dev_bf16(vb), out, hkv, tk, mode == "causal", pre)
+    torch.cuda.synchronize()
+    ref = oracle.attention(widen(qb), widen(kb), widen(vb), hkv, tk, mode,
+                           t_idx, q_offset=pre)
+    got = host_f32(out)
+    assert np.all(np.isfinite(got))
+    assert rel_l2(got, ref) < BAR
+    assert max_rel(got, ref) <= 1e-2
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+def test_token_major_masked_matches_head_major(ops, mode):
+    """The token-major entry point runs the same kernel on other strides:
+    bit-identical to the head-major result for the masked modes too."""
+    hq, hkv, d, tq, tk = 16, 4, 128, 200, 330
+    pre = tk - tq
+    cap = tk + 3
+    g = torch.Generator(device="cuda").manual_seed(mode)
+    q = torch.randn(hq, tq, d, generator=g, device="cuda").to(torch.bfloat16)
+    k = torch.randn(hkv, cap, d, generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn(hkv, cap, d, generator=g, device="cuda").to(torch.bfloat16)
+    t_idx = torch.from_numpy(np.concatenate(
+        [np.arange(pre), pre + np.arange(tq) // 16]).astype(np.int32)).cuda()
+    out = torch.empty_like(q)
+    if mode == 1:
+        ops.sdpa(q, k, v, out, hkv, tk, True, pre)
+    else:
+        ops.sdpa_block_causal(q, k, v, out, t_idx, hkv, tk, pre)
+    qt = q.transpose(0, 1).contiguous().view(tq, hq * d)
+    ot = torch.empty_like(qt)
+    ops.attention_token_major(qt, k, v, ot, hq, hkv, tk, t_index=t_idx,
+                              q_offset=pre, mode=mode)
+    torch.cuda.synchronize()
+    assert torch.equal(ot.view(tq, hq, d).transpose(0, 1).contiguous().view(torch.int16),
+                       out.view(torch.int16))
