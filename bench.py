@@ -13,7 +13,8 @@ measured beside it: per-token activation quantisation + int8 GEMM with the
 fused dequant, weights quantised per output channel once, up front.
 
 Prints ONE JSON line (rank 0).  `value` is bf16 TFLOP/s of the whole step;
-the int8 tier's TOPS ride in "int8".  "roofline" is the dominant kernel
+the int8 tier's TOPS ride in "int8"; "attention" times the layer's
+attention over the K/V cache at config 2's generation-pass shape.  "roofline" is the dominant kernel
 (the bf16 grouped GEMM), timed per launch with HIP events on the stream it
 runs on; "cpu_baseline" times the reference's CPU linear (or the oracle's
 restatement) on a bounded sample of config 1 on this host, single thread.
@@ -65,6 +66,8 @@ def parse():
     ap.add_argument("--m-gen", type=int, default=None)
     ap.add_argument("--no-int8", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-attn", action="store_true",
+                    help="skip the attention measurement")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="target length of the bounded CPU-baseline sample")
     ap.add_argument("--fused-swiglu", action="store_true",
@@ -308,6 +311,43 @@ def timed_kernels(torch, ops, runs, steps):
     return per, red
 
 
+# config 2's generation pass through attention: 32 query heads over 8 kv
+# heads, head_dim 128, the 4096 gen queries against the 128-token prefix
+# plus themselves, bidirectional (the image block sees itself whole)
+ATTN = dict(hq=32, hkv=8, d=128, tq=4096, tk=4224)
+
+
+def attention_measure(torch, ops, gen, launches):
+    """Average launch time of the attention kernel at ATTN's shape, HIP
+    events on the launch stream around `launches` back-to-back calls."""
+    a = ATTN
+    q = torch.randn(a["hq"], a["tq"], a["d"], generator=gen, device="cuda").to(torch.bfloat16)
+    k = torch.randn(a["hkv"], a["tk"], a["d"], generator=gen, device="cuda").to(torch.bfloat16)
+    v = torch.randn(a["hkv"], a["tk"], a["d"], generator=gen, device="cuda").to(torch.bfloat16)
+    out = torch.empty_like(q)
+    for _ in range(3):
+        ops.sdpa(q, k, v, out, a["hkv"], a["tk"])
+    hev = HipEvents()
+    stream = torch.cuda.current_stream()
+    e0, e1 = hev.create(), hev.create()
+    torch.cuda.synchronize()
+    hev.record(e0, stream)
+    for _ in range(launches):
+        ops.sdpa(q, k, v, out, a["hkv"], a["tk"])
+    hev.record(e1, stream)
+    torch.cuda.synchronize()
+    ms = hev.elapsed(e0, e1) / launches
+    hev.close()
+    flop = 4 * a["hq"] * a["tq"] * a["tk"] * a["d"]
+    tf = flop / (ms * 1e-3) / 1e12
+    return {"kernel": "attention_kernel<128, 0>", "shape": dict(a),
+            "mask": "bidirectional", "avg_launch_ms": round(ms, 5),
+            "flop_per_launch": flop, "value": round(tf, 2), "unit": "TFLOP/s",
+            "roofline": {"bound": "mfma", "achieved": round(tf, 2),
+                         "peak": PEAK_BF16, "unit": "TFLOP/s",
+                         "frac": round(tf / PEAK_BF16, 4)}}
+
+
 def cpu_baseline(target_s):
     """Reference CPU linear (u15::ref::linear compiled from the reference,
     or the oracle's restatement when that is not built), single thread, on
@@ -443,6 +483,8 @@ def main():
                              "achieved_GBps": round(q_bytes / (q_ms * 1e-3) / 1e9, 1),
                              "peak": PEAK_HBM},
         }
+    if not args.no_attn:
+        result["attention"] = attention_measure(torch, ops, gen, args.steps)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     ops.close()
