@@ -14,7 +14,8 @@ fused dequant, weights quantised per output channel once, up front.
 
 Prints ONE JSON line (rank 0).  `value` is bf16 TFLOP/s of the whole step;
 the int8 tier's TOPS ride in "int8"; "attention" times the layer's
-attention over the K/V cache at config 2's generation-pass shape.  "roofline" is the dominant kernel
+attention over the K/V cache at config 2's generation-pass shape and
+"split_norm_rope" the fused q/k norm + RoPE pass on its q and k rows.  "roofline" is the dominant kernel
 (the bf16 grouped GEMM), timed per launch with HIP events on the stream it
 runs on; "cpu_baseline" times the reference's CPU linear (or the oracle's
 restatement) on a bounded sample of config 1 on this host, single thread.
@@ -68,6 +69,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-attn", action="store_true",
                     help="skip the attention measurement")
+    ap.add_argument("--attn-only", action="store_true",
+                    help="only the attention measurement (--steps launches), "
+                         "printed as its own JSON object")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="target length of the bounded CPU-baseline sample")
     ap.add_argument("--fused-swiglu", action="store_true",
@@ -348,6 +352,44 @@ def attention_measure(torch, ops, gen, launches):
                          "frac": round(tf / PEAK_BF16, 4)}}
 
 
+def norm_rope_measure(torch, ops, gen, launches):
+    """Average launch time of the fused split q/k norm + split RoPE pass
+    over config 2's q (32 heads) and k (8 heads) rows: 4224 tokens,
+    head_dim 128 = t 64 | h 32 | w 32.  HBM-bound: each launch reads and
+    writes x once and reads the two f32 tables once."""
+    T, D, d_t, d_h = 4224, 128, 64, 32
+    cs = torch.rand(T, D, generator=gen, device="cuda")
+    sn = torch.rand(T, D, generator=gen, device="cuda")
+    hev = HipEvents()
+    stream = torch.cuda.current_stream()
+    out = {}
+    for name, H in (("q", 32), ("k", 8)):
+        x = torch.randn(T, H * D, generator=gen, device="cuda").to(torch.bfloat16)
+        wt = torch.randn(D // 2, generator=gen, device="cuda").to(torch.bfloat16)
+        wh = torch.randn(D // 2, generator=gen, device="cuda").to(torch.bfloat16)
+        for _ in range(3):
+            ops.split_qk_norm_rope(x, wt, wh, cs, sn, H, D, d_t, d_h)
+        e0, e1 = hev.create(), hev.create()
+        torch.cuda.synchronize()
+        hev.record(e0, stream)
+        for _ in range(launches):
+            ops.split_qk_norm_rope(x, wt, wh, cs, sn, H, D, d_t, d_h)
+        hev.record(e1, stream)
+        torch.cuda.synchronize()
+        ms = hev.elapsed(e0, e1) / launches
+        nbytes = 2 * T * H * D * 2 + 2 * T * D * 4 + 2 * D * 2
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"heads": H, "avg_launch_ms": round(ms, 5),
+                     "alg_bytes_per_launch": nbytes, "achieved_GBps": round(gbs, 1)}
+    hev.close()
+    return {"kernel": "split_norm_rope_vec_kernel<true, true>",
+            "shape": {"tokens": T, "head_dim": D, "d_t": d_t, "d_h": d_h},
+            **out,
+            "roofline": {"bound": "hbm", "achieved": out["q"]["achieved_GBps"],
+                         "peak": PEAK_HBM, "unit": "GB/s",
+                         "frac": round(out["q"]["achieved_GBps"] / PEAK_HBM, 4)}}
+
+
 def cpu_baseline(target_s):
     """Reference CPU linear (u15::ref::linear compiled from the reference,
     or the oracle's restatement when that is not built), single thread, on
@@ -414,6 +456,10 @@ def main():
         __graft_entry__.build()
     ops = u15h.Ops(0)
     gen = torch.Generator(device="cuda").manual_seed(args.seed)
+    if args.attn_only:
+        print(json.dumps(attention_measure(torch, ops, gen, args.steps)), flush=True)
+        ops.close()
+        return
     want_i8 = not args.no_int8
     layers = [Layer(gen, torch, want_i8, ops) for _ in range(args.layers)]
     A = activations(gen, torch, args.m_und, args.m_gen)
@@ -485,6 +531,7 @@ def main():
         }
     if not args.no_attn:
         result["attention"] = attention_measure(torch, ops, gen, args.steps)
+        result["split_norm_rope"] = norm_rope_measure(torch, ops, gen, args.steps)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     ops.close()

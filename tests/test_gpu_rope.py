@@ -149,3 +149,39 @@ def test_norm_rope_rejects_bad_shapes(ops):
     assert L.u15h_split_qk_norm(c, s, p(x), p(x), p(x), 1, 1, 1024, 1e-6) == u15h.EINVAL
     # zero tokens is a no-op
     assert L.u15h_split_rope(c, s, None, None, None, 2, 0, 128, 64, 32) == u15h.OK
+
+
+@pytest.mark.parametrize("D,d_t,d_h", [(64, 32, 16), (128, 64, 32), (256, 128, 64)])
+@pytest.mark.parametrize("misaligned", [False, True])
+def test_chunked_and_row_kernels(ops, D, d_t, d_h, misaligned):
+    """Two kernels serve these entry points: one 16-byte chunk per thread
+    (16-byte-aligned operands, power-of-two ranges) and one row per wave
+    (everything else).  A row view 8 bytes off alignment takes the second;
+    both match the oracle, fused and two-step."""
+    H, T = 8, 97
+    rng = np.random.default_rng(D + misaligned)
+    xb = oracle.f32_to_bf16(rng.standard_normal((T, H * D)).astype(np.float32))
+    wtb = oracle.f32_to_bf16(rng.normal(1, 0.2, D // 2).astype(np.float32))
+    whb = oracle.f32_to_bf16(rng.normal(1, 0.2, D // 2).astype(np.float32))
+    pt = rng.integers(0, 3000, T)
+    ph = rng.integers(0, 64, T)
+    pw = rng.integers(0, 64, T)
+    cs, sn = (dev_f32(t) for t in u15h.build_rope_tables(pt, ph, pw, D, d_t, d_h))
+    ref = oracle.split_qk_norm_rope(widen(xb), widen(wtb), widen(whb), pt, ph,
+                                    pw, H, D, d_t, d_h)
+    for fused in (True, False):
+        flat = torch.zeros(T * H * D + 4, dtype=torch.bfloat16, device="cuda")
+        x = flat[4:] if misaligned else flat[:-4]
+        x.view(T, H * D).copy_(dev_bf16(xb))
+        x2 = x.view(T, H * D)
+        assert (x2.data_ptr() % 16 != 0) == misaligned
+        if fused:
+            ops.split_qk_norm_rope(x2, dev_bf16(wtb), dev_bf16(whb), cs, sn, H, D,
+                                   d_t, d_h)
+        else:
+            ops.split_qk_norm(x2, dev_bf16(wtb), dev_bf16(whb), H, D)
+            ops.split_rope(x2, cs, sn, H, D, d_t, d_h)
+        torch.cuda.synchronize()
+        got = host_f32(x2)
+        assert rel_l2(got, ref) < BAR
+        assert max_rel(got, ref) <= MAX_REL

@@ -1064,6 +1064,79 @@ split_norm_rope_kernel(uint16_t* __restrict__ x,
   }
 }
 
+// The same pass with one thread per 16-byte chunk (8 elements), the row's
+// D/8 chunks on D/8 adjacent lanes: the half sums reduce by xor shuffles
+// over the D/16 lanes of each half, and an element's rotation partner, r
+// elements away (r = half its range), sits on the lane r/8 away (xor, as
+// every range starts at a multiple of its own width).  Shapes: D a power of
+// two in [16, 512], d_t/16 and d_h/16 powers of two, d_h dividing d_t.
+template <bool NORM, bool ROPE>
+__global__ __launch_bounds__(256) void
+split_norm_rope_vec_kernel(uint16_t* __restrict__ x,
+                           const uint16_t* __restrict__ w_t,
+                           const uint16_t* __restrict__ w_hw,
+                           const float* __restrict__ cosf,
+                           const float* __restrict__ sinf, int rows, int H,
+                           int D, int d_t, int d_h, float eps)
+{
+  const int cpr = D >> 3;                          // chunks (lanes) per row
+  const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
+  const long long row = gid / cpr;
+  const int c = (int)(gid % cpr);
+  const bool active = row < rows;
+  uint16_t* p = x + (active ? row : 0) * D + c * 8;
+  i32x4_t raw = active ? *reinterpret_cast<const i32x4_t*>(p) : i32x4_t{0, 0, 0, 0};
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float((uint32_t)raw[i] << 16);
+    v[2 * i + 1] = __uint_as_float((uint32_t)raw[i] & 0xffff0000u);
+  }
+  const int hc = cpr >> 1;                         // chunks per half
+  if constexpr (NORM) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) { ss += v[i] * v[i]; }
+    for (int o = 1; o < hc; o <<= 1) { ss += __shfl_xor(ss, o); }
+    const float inv = rsqrtf(ss / (float)(D >> 1) + eps);
+    const uint16_t* w = c < hc ? w_t + c * 8 : w_hw + (c - hc) * 8;
+    const i32x4_t wr = *reinterpret_cast<const i32x4_t*>(w);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = v[2 * i] * inv * __uint_as_float((uint32_t)wr[i] << 16);
+      v[2 * i + 1] = v[2 * i + 1] * inv * __uint_as_float((uint32_t)wr[i] & 0xffff0000u);
+    }
+  }
+  if constexpr (ROPE) {
+    const int e0 = c * 8;
+    const int off = e0 < d_t ? 0 : (e0 < d_t + d_h ? d_t : d_t + d_h);
+    const int r = (e0 < d_t ? d_t : d_h) >> 1;
+    const bool lower = e0 - off < r;
+    float vp[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) { vp[i] = __shfl_xor(v[i], r >> 3); }
+    const long long t = (active ? row : 0) / H;
+    const float* cp = cosf + t * D + e0;
+    const float* sp = sinf + t * D + e0;
+    float cs[8], sn[8];
+    *reinterpret_cast<i32x4_t*>(cs) = *reinterpret_cast<const i32x4_t*>(cp);
+    *reinterpret_cast<i32x4_t*>(cs + 4) = *reinterpret_cast<const i32x4_t*>(cp + 4);
+    *reinterpret_cast<i32x4_t*>(sn) = *reinterpret_cast<const i32x4_t*>(sp);
+    *reinterpret_cast<i32x4_t*>(sn + 4) = *reinterpret_cast<const i32x4_t*>(sp + 4);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      v[i] = lower ? v[i] * cs[i] - vp[i] * sn[i] : v[i] * cs[i] + vp[i] * sn[i];
+    }
+  }
+  if (!active) { return; }
+  i32x4_t o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o[i] = (int)(bf16_bits(v[2 * i]) | (bf16_bits(v[2 * i + 1]) << 16));
+  }
+  *reinterpret_cast<i32x4_t*>(p) = o;
+}
+
 // ---- f16 -> bf16, the loader's conversion -----------------------------------
 // Widen f16 to f32 with integer operations (subnormals renormalised; Inf
 // and NaN keep their payload bits, which the hardware conversion would
@@ -1685,6 +1758,28 @@ launch_split_norm_rope(uint16_t* x, const uint16_t* w_t, const uint16_t* w_hw,
                        hipStream_t s)
 {
   if (rows <= 0) { return hipSuccess; }
+  auto pow2 = [](int v) { return v > 0 && (v & (v - 1)) == 0; };
+  const uintptr_t addr_bits =
+      reinterpret_cast<uintptr_t>(x) |
+      (norm ? reinterpret_cast<uintptr_t>(w_t) | reinterpret_cast<uintptr_t>(w_hw) : 0) |
+      (rope ? reinterpret_cast<uintptr_t>(cosf) | reinterpret_cast<uintptr_t>(sinf) : 0);
+  const bool ranges_ok = d_t % 16 == 0 && d_h % 16 == 0 && pow2(d_t / 16) &&
+                         pow2(d_h / 16) && d_t % d_h == 0;
+  if (addr_bits % 16 == 0 && pow2(D) && D >= 16 && D <= 512 && (!rope || ranges_ok)) {
+    const long long threads = (long long)rows * (D / 8);
+    const dim3 vgrid((unsigned)((threads + 255) / 256));
+    if (norm && rope) {
+      hipLaunchKernelGGL((split_norm_rope_vec_kernel<true, true>), vgrid, dim3(256), 0, s,
+                         x, w_t, w_hw, cosf, sinf, rows, H, D, d_t, d_h, eps);
+    } else if (norm) {
+      hipLaunchKernelGGL((split_norm_rope_vec_kernel<true, false>), vgrid, dim3(256), 0, s,
+                         x, w_t, w_hw, cosf, sinf, rows, H, D, d_t, d_h, eps);
+    } else {
+      hipLaunchKernelGGL((split_norm_rope_vec_kernel<false, true>), vgrid, dim3(256), 0, s,
+                         x, w_t, w_hw, cosf, sinf, rows, H, D, d_t, d_h, eps);
+    }
+    return hipGetLastError();
+  }
   const dim3 grid((unsigned)((rows + 3) / 4));
   if (norm && rope) {
     hipLaunchKernelGGL((split_norm_rope_kernel<true, true>), grid, dim3(256),
@@ -1811,6 +1906,9 @@ kernels_loadable()
       reinterpret_cast<const void*>(&split_norm_rope_kernel<true, true>),
       reinterpret_cast<const void*>(&split_norm_rope_kernel<true, false>),
       reinterpret_cast<const void*>(&split_norm_rope_kernel<false, true>),
+      reinterpret_cast<const void*>(&split_norm_rope_vec_kernel<true, true>),
+      reinterpret_cast<const void*>(&split_norm_rope_vec_kernel<true, false>),
+      reinterpret_cast<const void*>(&split_norm_rope_vec_kernel<false, true>),
       reinterpret_cast<const void*>(&quant_rows_i8_kernel<2>),
       reinterpret_cast<const void*>(&quant_rows_i8_kernel<6>),
       reinterpret_cast<const void*>(&swiglu_kernel),
