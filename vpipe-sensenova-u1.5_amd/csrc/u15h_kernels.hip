@@ -820,27 +820,50 @@ split_reduce_kernel(const GemmBatch B)
 
 // ---- per-row symmetric int8 quantisation ------------------------------
 // One workgroup per row: absmax over the row (bf16 widened exactly), then
-// q = clamp(round_half_away(x / s), -127, 127) with s = absmax / 127
-// (fp32 division, correctly rounded).  The row is read once: each thread
-// keeps its CPT 16-byte chunks in registers across the block reduction
+// q = clamp(round_half_away(x / s), -127, 127) with s = absmax / 127 (fp32
+// division, correctly rounded).  The row is read once: each thread keeps
+// its CPT 16-byte chunks in registers across the block reduction
 // (CPT * 8 * 256 >= K); rows longer than that take a second read.
+//
+// The per-element quotient is not divided.  u = fma(x, inv, 128) with
+// inv = 1/s correctly rounded once per row is the biased code before
+// rounding: it lies within 2.3e-5 of the exact x/s + 128 (inv's error on
+// |x/s| <= 127.00001, plus the fma's half ulp at 255), and the correctly
+// rounded x/s within 3.8e-6 of the exact quotient, so rint(u) - 128 and
+// round_half_away(x/s) agree unless u is within 2.7e-5 of a half-integer.
+// A chunk with any element within 5e-5 of one is redone with the
+// division.  |x/s| < 127.5, so the fast path needs no clamp; the bytes are
+// packed biased (v_cvt_pk_u8_f32) and unbiased by flipping bit 7.  The
+// codes are the division's, bit for bit.
 __device__ __forceinline__ uint2
-quant8(const uint4 v, float s)
+quant8(const uint4 v, float s, float inv)
 {
+  if (s == 0.0f) { return make_uint2(0u, 0u); }       // row of zeros
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  float x[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    x[2 * e] = __uint_as_float(w[e] << 16);
+    x[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+  }
   uint32_t packed[2] = {0u, 0u};
+  float dev = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const uint32_t h = (e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffffu);
-    int cq = 0;
-    if (s != 0.0f) {
-      const float t = bf16_to_f32(h) / s;
-      cq = (int)roundf(t);
-      cq = max(-127, min(127, cq));
-    }
-    packed[e >> 2] |= ((uint32_t)(cq & 0xff)) << ((e & 3) * 8);
+    const float u = fmaf(x[e], inv, 128.0f);
+    const float n = rintf(u);
+    dev = fmaxf(dev, fabsf(u - n));
+    packed[e >> 2] = __builtin_amdgcn_cvt_pk_u8_f32(n, e & 3, packed[e >> 2]);
   }
-  return make_uint2(packed[0], packed[1]);
+  if (dev > 0.5f - 5e-5f) {
+    packed[0] = packed[1] = 0u;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float n = fminf(127.0f, fmaxf(-127.0f, roundf(x[e] / s)));
+      packed[e >> 2] |= ((uint32_t)((int)n + 128)) << ((e & 3) * 8);
+    }
+  }
+  return make_uint2(packed[0] ^ 0x80808080u, packed[1] ^ 0x80808080u);
 }
 
 __device__ __forceinline__ float
@@ -881,15 +904,16 @@ quant_rows_i8_kernel(const uint16_t* __restrict__ x, int K,
   __syncthreads();
   amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float s = amax / 127.0f;
+  const float inv = s != 0.0f ? 1.0f / s : 0.0f;
   if (threadIdx.x == 0) { sc[r] = s; }
   uint2* qr = reinterpret_cast<uint2*>(q + (size_t)r * K);
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
     const int c = threadIdx.x + i * 256;
-    if (c < nchunk) { qr[c] = quant8(v[i], s); }
+    if (c < nchunk) { qr[c] = quant8(v[i], s, inv); }
   }
   for (int c = threadIdx.x + CPT * 256; c < nchunk; c += 256) {
-    qr[c] = quant8(xr[c], s);
+    qr[c] = quant8(xr[c], s, inv);
   }
 }
 
