@@ -42,6 +42,28 @@ def test_quant_rows_bit_exact(ops):
     assert list(q[4, :7].cpu().numpy()) == [127, 3, -3, 1, -1, 2, -127]
 
 
+def test_quant_rows_every_tie(ops):
+    """Every half-integer quotient from -126.5 to 126.5 at scales 2^-3, 1
+    and 2^5 (amax = 127 * scale, so x / s is exact and each element is a
+    tie): the codes round half away from zero, as the oracle's division."""
+    half = np.arange(-126.5, 127.0, 1.0)
+    rows = []
+    for e in (-3, 0, 5):
+        row = np.zeros(256, np.float32)
+        row[0] = 127.0 * 2.0 ** e
+        row[1:1 + half.size] = half * 2.0 ** e
+        rows.append(row)
+    xb = oracle.f32_to_bf16(np.stack(rows))
+    assert np.array_equal(oracle.bf16_to_f32(xb), np.stack(rows))   # exact
+    q, s = quant_gpu(ops, xb)
+    qo, so = oracle.quant_rows_i8(xb)
+    assert np.array_equal(q.cpu().numpy(), qo)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
+    want = np.sign(half) * np.floor(np.abs(half) + 0.5)
+    assert np.array_equal(q.cpu().numpy()[:, 1:1 + half.size],
+                          np.tile(want.astype(np.int8), (3, 1)))
+
+
 @pytest.mark.parametrize("K", [8, 136, 12288])
 def test_quant_rows_other_widths(ops, K):
     rng = np.random.default_rng(K)
