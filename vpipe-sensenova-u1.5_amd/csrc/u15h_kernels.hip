@@ -757,62 +757,81 @@ split_reduce_kernel(const GemmBatch B)
   tile_origin<E>(P, tile, &row0, &col0);
   const int32_t* wsb =
       static_cast<const int32_t*>(B.ws) + (size_t)ts * B.split * (kBM * kBN);
-  const int q = threadIdx.x & 63;             // column quad within the tile
-  for (int rr = threadIdx.x >> 6; rr < kRowsPerBlock; rr += 4) {
-    const int ml = (blockIdx.x % (kBM / kRowsPerBlock)) * kRowsPerBlock + rr;
-    const int m = row0 + ml;
-    if (m >= P.rows) { return; }
-    const int nl = q * 4;
-    auto sum4 = [&](int col) {
-      int4 r = make_int4(0, 0, 0, 0);
-      float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
-      for (int sh = 0; sh < B.split; ++sh) {
-        const int4 v = *reinterpret_cast<const int4*>(
-            wsb + (size_t)sh * (kBM * kBN) + ml * kBN + col);
+  // Thread: column quad q of the tile, rows r, r+4, r+8, r+12 of the
+  // block.  The four rows of a share are loaded together (rows past the
+  // problem read stale slot values that are never stored), and the share
+  // loop is unrolled, so many loads are in flight; each sum still runs in
+  // share order.
+  const int q = threadIdx.x & 63;
+  const int mlb = (blockIdx.x % (kBM / kRowsPerBlock)) * kRowsPerBlock +
+                  (threadIdx.x >> 6);
+  const int nl = q * 4;
+  constexpr int kCols = E == Epi::kSwiglu ? 2 : 1;   // gate (+ up) columns
+  int col[kCols];
+  col[0] = nl;
+  if constexpr (E == Epi::kSwiglu) {
+    // Gate columns sit at tile columns wn*NW + [0, NW/2), their up
+    // partners NW/2 further on; the output column is col0 + wn*NW/2 +
+    // that offset.
+    if ((nl % NW) >= NW / 2) { return; }
+    col[1] = nl + NW / 2;
+  }
+  float4 f[kCols][4];
+  int4 r[kCols][4];
+#pragma unroll
+  for (int c = 0; c < kCols; ++c) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      f[c][k] = make_float4(0.f, 0.f, 0.f, 0.f);
+      r[c][k] = make_int4(0, 0, 0, 0);
+    }
+  }
+#pragma unroll 4
+  for (int sh = 0; sh < B.split; ++sh) {
+    const int32_t* base = wsb + (size_t)sh * (kBM * kBN);
+    int4 v[kCols][4];
+#pragma unroll
+    for (int c = 0; c < kCols; ++c) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        v[c][k] = *reinterpret_cast<const int4*>(base + (mlb + 4 * k) * kBN + col[c]);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < kCols; ++c) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
         if constexpr (kInt) {
-          r.x += v.x; r.y += v.y; r.z += v.z; r.w += v.w;
+          r[c][k].x += v[c][k].x; r[c][k].y += v[c][k].y;
+          r[c][k].z += v[c][k].z; r[c][k].w += v[c][k].w;
         } else {
-          f.x += bits_as<float>(v.x);
-          f.y += bits_as<float>(v.y);
-          f.z += bits_as<float>(v.z);
-          f.w += bits_as<float>(v.w);
+          f[c][k].x += bits_as<float>(v[c][k].x);
+          f[c][k].y += bits_as<float>(v[c][k].y);
+          f[c][k].z += bits_as<float>(v[c][k].z);
+          f[c][k].w += bits_as<float>(v[c][k].w);
         }
       }
-      if constexpr (kInt) {
-        return make_float4(bits_as<float>(r.x),
-                           bits_as<float>(r.y),
-                           bits_as<float>(r.z),
-                           bits_as<float>(r.w));
-      } else {
-        return f;
-      }
-    };
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int m = row0 + mlb + 4 * k;
+    if (m >= P.rows) { break; }
     if constexpr (E == Epi::kSwiglu) {
-      // Gate columns sit at tile columns wn*NW + [0, NW/2), their up
-      // partners NW/2 further on; the output column is col0 + wn*NW/2 +
-      // that offset.
-      if ((nl % NW) >= NW / 2) { continue; }
       const int n = col0 + (nl / NW) * (NW / 2) + (nl % NW);
       if (n >= P.n) { continue; }
-      const float4 g = sum4(nl), u = sum4(nl + NW / 2);
-      const float gv[4] = {g.x, g.y, g.z, g.w};
-      const float uv[4] = {u.x, u.y, u.z, u.w};
+      const float gv[4] = {f[0][k].x, f[0][k].y, f[0][k].z, f[0][k].w};
+      const float uv[4] = {f[1][k].x, f[1][k].y, f[1][k].z, f[1][k].w};
       store_swiglu4(P, m, n, gv, uv);
     } else {
       const int n = col0 + nl;
       if (n >= P.n) { continue; }
-      const float4 v = sum4(nl);
       if constexpr (E == Epi::kI32) {
-        store_i32x4(P, m, n, bits_as<int>(v.x),
-                    bits_as<int>(v.y), bits_as<int>(v.z),
-                    bits_as<int>(v.w));
+        store_i32x4(P, m, n, r[0][k].x, r[0][k].y, r[0][k].z, r[0][k].w);
       } else if constexpr (E == Epi::kDequantBf16) {
-        store_dequant4(P, m, n, bits_as<int>(v.x),
-                       bits_as<int>(v.y),
-                       bits_as<int>(v.z),
-                       bits_as<int>(v.w));
+        store_dequant4(P, m, n, r[0][k].x, r[0][k].y, r[0][k].z, r[0][k].w);
       } else {
-        store_bf16x4(P, m, n, v.x, v.y, v.z, v.w);
+        store_bf16x4(P, m, n, f[0][k].x, f[0][k].y, f[0][k].z, f[0][k].w);
       }
     }
   }
