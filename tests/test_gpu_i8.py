@@ -273,3 +273,40 @@ def test_i32_per_item_launch_bit_exact():
     assert np.array_equal(out[Mu:].astype(np.int64).sum(axis=1), rs)
     assert np.array_equal(out[Mu:].astype(np.int64).sum(axis=0), cs)
     ops_pi.close()
+
+
+@pytest.mark.parametrize("Mu,Mg,K,N", [(128, 4096, 4096, 4096), (37, 263, 12288, 264)])
+def test_i32_four_wave_workgroup_bit_exact(Mu, Mg, K, N):
+    """The 4-wave GEMM workgroup (U15H_WAVES=4: 16x16x64 MFMAs, 128x128
+    per wave): exact accumulators -- every row sum and column sum, sampled
+    rows in full, split-K tail included."""
+    import os
+    import u15h
+    old = os.environ.get("U15H_WAVES")
+    os.environ["U15H_WAVES"] = "4"
+    try:
+        o4 = u15h.Ops(0)
+    finally:
+        if old is None:
+            del os.environ["U15H_WAVES"]
+        else:
+            os.environ["U15H_WAVES"] = old
+    rng = np.random.default_rng(K + N)
+    M = Mu + Mg
+    xq = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    wu = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    wg = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    y = torch.empty(M, N, dtype=torch.int32, device="cuda")
+    o4.mot_gemm_i8_i32(torch.from_numpy(xq).cuda(), Mu, Mg, K,
+                       [_proj(torch.from_numpy(wu).cuda(), None,
+                              torch.from_numpy(wg).cuda(), None, y)])
+    torch.cuda.synchronize()
+    out = y.cpu().numpy()
+    for lo, hi, w in ((0, Mu, wu), (Mu, M, wg)):
+        rs, cs = oracle.i8_product_sums(xq[lo:hi], w)
+        assert np.array_equal(out[lo:hi].astype(np.int64).sum(axis=1), rs)
+        assert np.array_equal(out[lo:hi].astype(np.int64).sum(axis=0), cs)
+    for r in (0, Mu - 1, Mu, M // 2, M - 1):
+        w = wu if r < Mu else wg
+        assert np.array_equal(out[r:r + 1], oracle.gemm_i8_i32(xq[r:r + 1], w))
+    o4.close()
