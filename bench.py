@@ -522,7 +522,7 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(g_tops, 2),
                          "peak": PEAK_I8, "unit": "TOPS",
                          "frac": round(g_tops / PEAK_I8, 4),
-                         "kernel": "mot_gemm_kernel<MmaI8, kDequantBf16, 4>",
+                         "kernel": "mot_gemm_kernel<MmaI8x16, kDequantBf16, 4>",
                          "avg_launch_ms": round(g_ms, 5),
                          "split_reduce_ms_per_step": round(red8 / args.steps, 5)},
             "quant_kernel": {"bound": "hbm", "avg_launch_ms": round(q_ms, 5),
