@@ -7,15 +7,16 @@
 // the kernel arguments.  Row-wise every problem is the reference's
 // MetalOps::linear (src/u15-metal-ops.cc:327-346) with one weight set.
 //
-// Tile: 256 activation rows x 256 weight rows, 4 waves of 64 in a 2x2 grid,
-// each wave owning a 128x128 block of 4x4 MFMA 32x32 accumulators.  K is
-// staged through LDS 128 bytes at a time (64 bf16 or 128 int8): both
-// element types share one byte layout, one load schedule and one swizzle;
-// only the MFMA differs (v_mfma_f32_32x32x16_bf16 / v_mfma_i32_32x32x32_i8,
-// each taking 16 bytes of K per lane).
+// Tile: 256 activation rows x 256 weight rows.  The default workgroup has
+// 8 waves (2 per SIMD) in a 2x4 grid, each owning 128 activation rows x 64
+// weight rows; the 4-wave workgroup owns 128x128 per wave.  K is staged
+// through LDS 128 bytes at a time (64 bf16 or 128 int8): both element types
+// share one byte layout, one load schedule and one swizzle.  The MFMA is a
+// trait (Mma*): v_mfma_f32_32x32x16_bf16 for bf16, v_mfma_i32_16x16x64_i8
+// for int8 by default, each taking 16 bytes of K per lane.
 //
 // Operand order: the WEIGHT fragment is the MFMA's first operand, so the
-// 32x32 accumulator's rows are output columns.  A lane then holds four
+// accumulator's rows are output columns.  A lane then holds groups of four
 // consecutive output columns of one activation row, which the epilogue
 // stores as one 8-byte (bf16) or 16-byte (int32) write.
 //
