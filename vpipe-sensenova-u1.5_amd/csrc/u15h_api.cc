@@ -214,6 +214,10 @@ check_n(u15h_ctx* ctx, int N)
   if (N <= 0 || N % 8 != 0) {
     return fail(ctx, U15H_EINVAL, "N=%d must be a positive multiple of 8", N);
   }
+  // a 256-row output tile of ldy = N bf16 columns addresses below 2^30 bytes
+  if (N > (1 << 20)) {
+    return fail(ctx, U15H_EINVAL, "N=%d too large (at most 2^20)", N);
+  }
   return U15H_OK;
 }
 

@@ -41,12 +41,14 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 typedef int i32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kStage = (kBM + kBN) * kKB;   // 64 KiB per LDS stage
 constexpr int kRsrcWord3 = 0x00020000;      // raw buffer, 32-bit data format
 constexpr int kOobOffset = 0x40000000;      // any offset past every resource
+constexpr int kNonTemporal = 2;             // buffer cache policy: nt
 
 // A buffer resource whose base and size are made explicitly wave-uniform,
 // so it lives in SGPRs: a resource the compiler cannot prove uniform turns
@@ -69,6 +71,17 @@ bf16_bits(float f)
   // weight loader use (finite values).
   const uint32_t u = __builtin_bit_cast(uint32_t, f);
   return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Two floats as packed bf16 (lo in the low half) in one v_cvt_pk_bf16_f32:
+// round to nearest even, the same result as bf16_bits for finite values.
+__device__ __forceinline__ uint32_t
+pack_bf16x2(float lo, float hi)
+{
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t,
+                            __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
 }
 
 __device__ __forceinline__ float
@@ -197,12 +210,18 @@ store_dequant4(const GemmProblem& P, int m, int n, int a0, int a1, int a2,
 
 // SwiGLU: gate and up are rounded to bf16 first (the unfused GEMMs' output
 // precision), then silu(gate) * up in fp32, rounded to bf16.
-__device__ __forceinline__ uint32_t
-swiglu1(float g, float u)
+__device__ __forceinline__ float
+swiglu_f(float g, float u)
 {
   const float gv = bf16_round(g);
   const float uv = bf16_round(u);
-  return bf16_bits((gv / (1.0f + expf(-gv))) * uv);
+  return (gv / (1.0f + expf(-gv))) * uv;
+}
+
+__device__ __forceinline__ uint32_t
+swiglu1(float g, float u)
+{
+  return bf16_bits(swiglu_f(g, u));
 }
 
 __device__ __forceinline__ void
@@ -216,15 +235,6 @@ store_swiglu4(const GemmProblem& P, int m, int n, const float g[4],
                             n) = o;
 }
 
-// One 16-byte chunk of an output row, written non-temporally: the staged
-// epilogue writes whole 128-byte lines with such stores, so the output
-// bypasses allocation in L2 instead of evicting the activation and weight
-// rows that the tiles still running on the XCD stream through it.
-__device__ __forceinline__ void
-store_line16(void* p, const i32x4_t& v)
-{
-  __builtin_nontemporal_store(v, static_cast<i32x4_t*>(p));
-}
 
 // Which problem a linear tile index belongs to (uniform over the block).
 __device__ __forceinline__ int
@@ -326,6 +336,16 @@ interleave_loads_reads()
   }
 }
 
+// Workgroup barrier for LDS hand-offs: waits for this wave's LDS accesses
+// but not for its global loads and stores (__syncthreads' fence waits for
+// all of them).  The memory clobber keeps the compiler from moving memory
+// accesses across it.
+__device__ __forceinline__ void
+lds_barrier()
+{
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // bf16 epilogue of a whole tile through LDS.  The MFMA layout gives each
 // lane 4 consecutive output columns of one row per store, so direct stores
 // write every 128-byte output line in 16-byte pieces from 8 instructions.
@@ -353,6 +373,31 @@ gemm_epilogue_staged(const GemmProblem& P, const TileWork& t, int wm, int wn,
   constexpr int CH = RB / 16;                 // 16-byte chunks per row
   const int lr = lane % kF;
   const int lh = lane / kF;
+  // Scales and bias of every row and column group this lane writes, loaded
+  // together before any is used (inside the per-fragment conditionals each
+  // load would be waited for on its own).  Indices past the problem are
+  // clamped to a valid element; those outputs are staged but never stored.
+  constexpr bool kScaled = E == Epi::kDequantBf16;
+  constexpr int kCols = E == Epi::kSwiglu ? 1 : FI * kGr;   // column groups
+  float sam[kScaled ? FJ : 1];
+  float4 swn[kScaled ? kCols : 1];
+  uint2 bia[E == Epi::kSwiglu ? 1 : kCols];
+  const bool has_bias = E != Epi::kSwiglu && P.bias != nullptr;
+  if constexpr (E != Epi::kSwiglu) {
+#pragma unroll
+    for (int c = 0; c < kCols; ++c) {
+      const int i = c / kGr, g = c % kGr;
+      const int n = min(t.col0 + wn * NW + i * kF + g * kGs + lh * 4, P.n - 4);
+      if constexpr (kScaled) { swn[c] = *reinterpret_cast<const float4*>(P.sw + n); }
+      bia[c] = has_bias ? *reinterpret_cast<const uint2*>(P.bias + n) : uint2{0u, 0u};
+    }
+  }
+  if constexpr (kScaled) {
+#pragma unroll
+    for (int j = 0; j < FJ; ++j) {
+      sam[j] = P.sa[min(t.row0 + wm * 128 + j * kF + lr, P.rows - 1)];
+    }
+  }
   // Every wave is past its last fragment read of the main loop.
   __syncthreads();
   char* const half = wm ? ring[1] : ring[0];
@@ -365,18 +410,19 @@ gemm_epilogue_staged(const GemmProblem& P, const TileWork& t, int wm, int wn,
 #pragma unroll
   for (int j = 0; j < FJ; ++j) {
     const int row = j * kF + lr;
-    const int m = t.row0 + wm * 128 + row;
     if constexpr (E == Epi::kSwiglu) {
 #pragma unroll
       for (int i = 0; i < FI / 2; ++i) {
 #pragma unroll
         for (int g = 0; g < kGr; ++g) {
           const int col = wn * (NW / 2) + i * kF + g * kGs + lh * 4;
+          const auto& ga = acc[i][j];
+          const auto& ua = acc[i + FI / 2][j];
           put(row, col,
-              swiglu1(acc[i][j][g * 4 + 0], acc[i + FI / 2][j][g * 4 + 0]) |
-                  (swiglu1(acc[i][j][g * 4 + 1], acc[i + FI / 2][j][g * 4 + 1]) << 16),
-              swiglu1(acc[i][j][g * 4 + 2], acc[i + FI / 2][j][g * 4 + 2]) |
-                  (swiglu1(acc[i][j][g * 4 + 3], acc[i + FI / 2][j][g * 4 + 3]) << 16));
+              pack_bf16x2(swiglu_f(ga[g * 4 + 0], ua[g * 4 + 0]),
+                          swiglu_f(ga[g * 4 + 1], ua[g * 4 + 1])),
+              pack_bf16x2(swiglu_f(ga[g * 4 + 2], ua[g * 4 + 2]),
+                          swiglu_f(ga[g * 4 + 3], ua[g * 4 + 3])));
         }
       }
     } else {
@@ -384,39 +430,31 @@ gemm_epilogue_staged(const GemmProblem& P, const TileWork& t, int wm, int wn,
       for (int i = 0; i < FI; ++i) {
 #pragma unroll
         for (int g = 0; g < kGr; ++g) {
+          const int c = i * kGr + g;
           const int col = wn * NW + i * kF + g * kGs + lh * 4;
-          const int n = t.col0 + col;
           const auto& a = acc[i][j];
           float v[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            if constexpr (E == Epi::kDequantBf16) {
+            if constexpr (kScaled) {
               v[e] = (float)bits_as<int>(a[g * 4 + e]);
             } else {
               v[e] = a[g * 4 + e];
             }
           }
-          // Columns and rows past the problem are staged but never stored;
-          // their scale and bias reads stay inside the problem.
-          if (n < P.n && m < P.rows) {
-            if constexpr (E == Epi::kDequantBf16) {
-              const float sam = P.sa[m];
-              const float4 swn = *reinterpret_cast<const float4*>(P.sw + n);
-              v[0] = (v[0] * sam) * swn.x;
-              v[1] = (v[1] * sam) * swn.y;
-              v[2] = (v[2] * sam) * swn.z;
-              v[3] = (v[3] * sam) * swn.w;
-            }
-            if (P.bias != nullptr) {
-              const uint2 bb = *reinterpret_cast<const uint2*>(P.bias + n);
-              v[0] += bf16_to_f32(bb.x & 0xffffu);
-              v[1] += bf16_to_f32(bb.x >> 16);
-              v[2] += bf16_to_f32(bb.y & 0xffffu);
-              v[3] += bf16_to_f32(bb.y >> 16);
-            }
+          if constexpr (kScaled) {
+            v[0] = (v[0] * sam[j]) * swn[c].x;
+            v[1] = (v[1] * sam[j]) * swn[c].y;
+            v[2] = (v[2] * sam[j]) * swn[c].z;
+            v[3] = (v[3] * sam[j]) * swn[c].w;
           }
-          put(row, col, bf16_bits(v[0]) | (bf16_bits(v[1]) << 16),
-              bf16_bits(v[2]) | (bf16_bits(v[3]) << 16));
+          if (has_bias) {
+            v[0] += bf16_to_f32(bia[c].x & 0xffffu);
+            v[1] += bf16_to_f32(bia[c].x >> 16);
+            v[2] += bf16_to_f32(bia[c].y & 0xffffu);
+            v[3] += bf16_to_f32(bia[c].y >> 16);
+          }
+          put(row, col, pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
         }
       }
     }
@@ -427,23 +465,39 @@ gemm_epilogue_staged(const GemmProblem& P, const TileWork& t, int wm, int wn,
   constexpr int RW = kBM / (2 * WN);
   const int wave = (int)(threadIdx.x >> 6);
   constexpr int kRowsPerRead = 64 / CH;
+  // The read-back addresses depend on the lane only; computed from an
+  // opaque copy of it they stay here instead of being hoisted out of the
+  // tile loop, where they would be spilled across the main loop and each
+  // reload would wait for every store in flight.
+  int lane_o = lane;
+  asm volatile("" : "+v"(lane_o));
   const int first = wave * RW;                          // first tile row
   const char* const src = first >= 128 ? ring[1] : ring[0];
+  // Whole 128-byte output lines go out as non-temporal stores, so the
+  // output bypasses allocation in L2 instead of evicting the activation and
+  // weight rows that the tiles still running on the XCD stream through it.
+  // Buffer stores over the tile's valid rows: rows past the problem fall
+  // outside the resource and are dropped, columns past it get an
+  // out-of-range offset (the host bounds ldy so that 256 rows of it stay
+  // below kOobOffset).
+  const __amdgpu_buffer_rsrc_t yr =
+      make_rsrc(static_cast<uint16_t*>(P.y) + (size_t)t.row0 * P.ldy,
+                min(kBM, P.rows - t.row0) * P.ldy * 2);
+  const int c = lane_o % CH;
+  const int n = t.col0 + c * 8;
+  int voff = n < P.n ? ((first + lane_o / CH) * P.ldy + n) * 2 : kOobOffset;
+  const int rstep = kRowsPerRead * P.ldy * 2;
 #pragma unroll
   for (int r = 0; r < RW; r += kRowsPerRead) {
-    const int hrow = first % 128 + r + lane / CH;       // row within the half
-    const int trow = first + r + lane / CH;             // row within the tile
-    const int c = lane % CH;
-    const i32x4_t v = *reinterpret_cast<const i32x4_t*>(
+    const int hrow = first % 128 + r + lane_o / CH;     // row within the half
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(
         src + hrow * RB + ((c ^ (hrow % CH)) << 4));
-    const int m = t.row0 + trow;
-    const int n = t.col0 + c * 8;
-    if (m < P.rows && n < P.n) {
-      store_line16(static_cast<uint16_t*>(P.y) + (size_t)m * P.ldy + n, v);
-    }
+    __builtin_amdgcn_raw_buffer_store_b128(v, yr, voff, 0, kNonTemporal);
+    voff += rstep;
   }
-  // The next tile's loads refill these buffers.
-  __syncthreads();
+  // The next tile's loads refill these buffers once every wave's reads of
+  // them are done; the stores drain meanwhile.
+  lds_barrier();
 }
 
 // Epilogue of a tile.  acc[i][j][r] holds tile column (weight row within
@@ -743,12 +797,15 @@ gemm_tile(const GemmBatch& B, char* const (&ring)[RING], int item)
   const int nst_pad = (t.nst + RING - 1) / RING * RING;
 #pragma unroll
   for (int r = 0; r < RING; ++r) { issue_loads(ring[r], r); }
+  // Stage 0 has landed once at most the later stages' loads are in flight
+  // (loads complete in issue order; the previous tile's output stores may
+  // still be draining, which only makes the wait longer).
   if constexpr (RING == 2) {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LB) : "memory");
   } else {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * LB) : "memory");
   }
-  __syncthreads();
+  lds_barrier();
   read_frags(ring[0], 0, 0);
   for (int ktl = 0; ktl < nst_pad; ktl += RING) {
 #pragma unroll
@@ -1323,16 +1380,6 @@ f16_to_bf16_kernel(const uint2* __restrict__ src, uint2* __restrict__ dst,
 // fetch the chunk the swizzle puts there.  K and V are read through
 // buffer resources bounded at tk keys: keys past tk read as zeros and are
 // masked to -inf, which adds 0 to every sum.
-__device__ __forceinline__ uint32_t
-pack_bf16x2(float lo, float hi)
-{
-  // v_cvt_pk_bf16_f32: round to nearest even
-  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-  typedef float f32x2_t __attribute__((ext_vector_type(2)));
-  return __builtin_bit_cast(uint32_t,
-                            __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
-}
-
 // max of v over lanes l and l ^ 32
 __device__ __forceinline__ float
 max_halves(float v)
