@@ -264,6 +264,13 @@ def test_invalid_shapes_launch_nothing(ops):
                          ctypes.c_void_p(w.data_ptr()), None,
                          ctypes.c_void_p(y.data_ptr()), 4, 16, 8)
     assert st == u15h.EINVAL                     # misaligned x
+    # N above 2^20: rejected before anything is read (the pointers are the
+    # small buffers above; nothing may touch them)
+    st = lib.u15h_linear(ctx, s, ctypes.c_void_p(x.data_ptr()),
+                         ctypes.c_void_p(w.data_ptr()), None,
+                         ctypes.c_void_p(y.data_ptr()), 4, 16, (1 << 20) + 8)
+    assert st == u15h.EINVAL
+    assert b"too large" in lib.u15h_last_error(ctx)
     torch.cuda.synchronize()
     assert torch.all(y == 7.0)
 
