@@ -19,6 +19,9 @@ attention over the K/V cache at config 2's generation-pass shape and
 (the bf16 grouped GEMM), timed per launch with HIP events on the stream it
 runs on; "cpu_baseline" times the reference's CPU linear (or the oracle's
 restatement) on a bounded sample of config 1 on this host, single thread.
+The int8, attention and norm/RoPE objects carry their own "cpu_baseline"
+(the oracle's exact int8 GEMM, the reference's CPU attention, the oracle's
+norm + RoPE), each on a bounded sample, single thread.
 """
 import argparse
 import json
@@ -390,6 +393,116 @@ def norm_rope_measure(torch, ops, gen, launches):
                          "frac": round(out["q"]["achieved_GBps"] / PEAK_HBM, 4)}}
 
 
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _timed(fn):
+    t = time.perf_counter()
+    fn()
+    return time.perf_counter() - t
+
+
+def cpu_baseline_i8(target_s):
+    """The exact int8 GEMM on the CPU (the oracle's restatement: int8 x int8
+    -> int32, one thread; the reference's int8 arithmetic lives in an absent
+    dependency), on a bounded sample of config 1: 256 rows through the
+    layer's 14 GEMMs, the first `frac` of each weight's output channels."""
+    import numpy as np
+
+    import oracle
+    rng = np.random.default_rng(8)
+    rows = 256
+    shapes = [(NQ, HIDDEN), (NKV, HIDDEN), (NKV, HIDDEN), (HIDDEN, NQ),
+              (INTER, HIDDEN), (INTER, HIDDEN), (HIDDEN, INTER)]
+    xs = {K: rng.integers(-127, 128, (rows, K), dtype=np.int8) for K in (HIDDEN, INTER)}
+    probe = rng.integers(-127, 128, (16, HIDDEN), dtype=np.int8)
+    rate = 2 * rows * 16 * HIDDEN / max(_timed(lambda: oracle.gemm_i8_i32(xs[HIDDEN], probe)), 1e-6)
+    total = sum(2 * rows * n * k for n, k in shapes) * 2
+    frac = min(1.0, target_s * rate / total)
+    ops_done, dt = 0, 0.0
+    for _set in range(2):
+        for (n, k) in shapes:
+            nn = max(8, int(n * frac) // 8 * 8)
+            w = rng.integers(-127, 128, (nn, k), dtype=np.int8)
+            dt += _timed(lambda: oracle.gemm_i8_i32(xs[k], w))
+            ops_done += 2 * rows * nn * k
+    return {"value": ops_done / dt / 1e12, "unit": "TOPS", "cores": 1,
+            "kind": "port",
+            "sample": (f"config 1 rows (256), the 14 GEMMs of one layer, first "
+                       f"{frac:.4f} of each weight's output channels: "
+                       f"{ops_done / 1e9:.2f} GOP in {dt:.1f} s, exact int32 "
+                       f"accumulation, 1 thread, {_cpu_model()}")}
+
+
+def cpu_baseline_attention(target_s):
+    """The reference's CPU attention (u15::ref::attention, compiled from the
+    reference when oracle/_ref is built; else the oracle's restatement), one
+    thread, on a bounded sample of the generation pass: one GQA group (4 q
+    heads on 1 kv head), the first `tq` of 4096 queries over all 4224 keys,
+    d = 128, no mask."""
+    import numpy as np
+
+    import oracle
+    a = ATTN
+    rng = np.random.default_rng(9)
+    grp = a["hq"] // a["hkv"]
+    k = rng.standard_normal((1, a["tk"], a["d"]), dtype=np.float32)
+    v = rng.standard_normal((1, a["tk"], a["d"]), dtype=np.float32)
+    ref = oracle.ref_lib() is not None
+
+    def run(tq):
+        q = rng.standard_normal((grp, tq, a["d"]), dtype=np.float32) * 0.1
+        if ref:
+            return _timed(lambda: oracle.ref_attention(q, k, v, None, 1))
+        return _timed(lambda: oracle.attention(q, k, v, 1, a["tk"]))
+    rate = 4 * grp * 4 * a["tk"] * a["d"] / max(run(4), 1e-6)
+    tq = int(max(4, min(a["tq"], target_s * rate / (4 * grp * a["tk"] * a["d"]))))
+    dt = run(tq)
+    flop = 4 * grp * tq * a["tk"] * a["d"]
+    return {"value": flop / dt / 1e12, "unit": "TFLOP/s", "cores": 1,
+            "kind": "reference" if ref else "port",
+            "sample": (f"{grp} q heads x {tq} queries over {a['tk']} keys, "
+                       f"d {a['d']}, bidirectional: {flop / 1e9:.2f} GFLOP in "
+                       f"{dt:.1f} s, f32, 1 thread, {_cpu_model()}")}
+
+
+def cpu_baseline_norm_rope(target_s):
+    """The oracle's split q/k norm + split RoPE (its restatement of the
+    reference's split_qk_norm and split_rope; the reference's CPU form
+    exists only fused with the projection), one thread, on the first `T` of
+    config 2's tokens for the 32 q heads."""
+    import numpy as np
+
+    import oracle
+    rng = np.random.default_rng(10)
+    H, D, d_t, d_h = 32, 128, 64, 32
+    w_t = rng.standard_normal(D // 2, dtype=np.float32)     # norm of [0, D/2)
+    w_hw = rng.standard_normal(D // 2, dtype=np.float32)    # norm of [D/2, D)
+
+    def run(T):
+        x = rng.standard_normal((T, H * D), dtype=np.float32)
+        pos = np.arange(T, dtype=np.int32)
+        return _timed(lambda: oracle.split_qk_norm_rope(x, w_t, w_hw, pos, pos, pos,
+                                                        H, D, d_t, d_h))
+    rate = 64 / max(run(64), 1e-6)
+    T = int(max(64, min(4224, target_s * rate)))
+    dt = run(T)
+    nbytes = 2 * T * H * D * 2 + 2 * T * D * 4      # bf16 in + out, f32 tables
+    return {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": 1,
+            "kind": "port",
+            "sample": (f"{T} tokens x {H} heads x {D}, t|h|w = {d_t}|{d_h}|{d_h}: "
+                       f"{dt:.2f} s, counted as the device pass's bytes "
+                       f"(bf16 rows in and out, f32 tables), 1 thread, "
+                       f"{_cpu_model()}")}
+
+
 def cpu_baseline(target_s):
     """Reference CPU linear (u15::ref::linear compiled from the reference,
     or the oracle's restatement when that is not built), single thread, on
@@ -422,14 +535,7 @@ def cpu_baseline(target_s):
             fn(xs[k][:m], w)
             flop += 2 * m * nn * k
     dt = time.perf_counter() - t
-    cpu = "unknown"
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+    cpu = _cpu_model()
     return {"value": flop / dt / 1e12, "unit": "TFLOP/s", "cores": 1,
             "kind": "reference" if ref else "port",
             "sample": (f"config 1 (64 und + 192 gen rows), all 14 GEMMs of one "
@@ -534,6 +640,12 @@ def main():
         result["split_norm_rope"] = norm_rope_measure(torch, ops, gen, args.steps)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        side = args.cpu_seconds / 3
+        if want_i8:
+            result["int8"]["cpu_baseline"] = cpu_baseline_i8(side)
+        if not args.no_attn:
+            result["attention"]["cpu_baseline"] = cpu_baseline_attention(side)
+            result["split_norm_rope"]["cpu_baseline"] = cpu_baseline_norm_rope(side / 2)
     ops.close()
     print(json.dumps(result), flush=True)
 
