@@ -877,8 +877,12 @@ split_reduce_kernel(const GemmBatch B)
   // loop is unrolled, so many loads are in flight; each sum still runs in
   // share order.
   const int q = threadIdx.x & 63;
-  const int mlb = (blockIdx.x % (kBM / kRowsPerBlock)) * kRowsPerBlock +
-                  (threadIdx.x >> 6);
+  const int block_row = (blockIdx.x % (kBM / kRowsPerBlock)) * kRowsPerBlock;
+  // A block whose rows all lie past the problem (the lower half of a
+  // 128-row und tile) has nothing to store; its loads would only cost
+  // bandwidth.
+  if (row0 + block_row >= P.rows) { return; }
+  const int mlb = block_row + (threadIdx.x >> 6);
   const int nl = q * 4;
   constexpr int kCols = E == Epi::kSwiglu ? 2 : 1;   // gate (+ up) columns
   int col[kCols];
