@@ -650,8 +650,10 @@ gemm_tile(const GemmBatch& B, char* const (&ring)[RING], int item)
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave & 1;
-  const int wn = wave >> 1;
+  // Wave w computes tile rows wm*128.. and weight rows wn*NW..; waves w and
+  // w + 4 share a SIMD, so each SIMD holds one upper and one lower half.
+  const int wm = wave / WN;
+  const int wn = wave % WN;
 
   // ---- operand extents and per-wave load parameters (wave-uniform) ------
   // Weight rows are wld bytes apart (kbytes for a plain [N][K] matrix, 2K
@@ -771,12 +773,19 @@ gemm_tile(const GemmBatch& B, char* const (&ring)[RING], int item)
   // be read while the last MFMAs run.  The body is branch-free, which keeps
   // the accumulators in registers across the whole loop; past the last
   // stage the extra loads fetch nothing and the extra reads are unused.
-  auto stage = [&](char* cur, const char* nxt, int ktl) {
+  // A wave whose 128 rows all lie past the problem (the lower half of a
+  // 128-row und tile) runs the same loads, waits and barriers without the
+  // fragment reads and MFMAs (`act` false), leaving its SIMD's matrix core
+  // to the partner wave; its accumulators stay zero and are never stored.
+  auto stage = [&](auto act, char* cur, const char* nxt, int ktl) {
+    constexpr bool kAct = decltype(act)::value;
+    if constexpr (kAct) {
 #pragma unroll
-    for (int s = 0; s + 1 < kSub; ++s) {
-      read_frags(cur, s + 1, (s + 1) & 1);
-      mma_step(s & 1);
-      interleave_reads<kMfmaPerStep, kReadsPerStep>();
+      for (int s = 0; s + 1 < kSub; ++s) {
+        read_frags(cur, s + 1, (s + 1) & 1);
+        mma_step(s & 1);
+        interleave_reads<kMfmaPerStep, kReadsPerStep>();
+      }
     }
     if constexpr (RING == 2) {
       asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
@@ -787,9 +796,11 @@ gemm_tile(const GemmBatch& B, char* const (&ring)[RING], int item)
     }
     __syncthreads();
     issue_loads(cur, ktl + RING);
-    read_frags(nxt, 0, 0);
-    mma_step((kSub - 1) & 1);
-    interleave_loads_reads<kMfmaPerStep, LB, kReadsPerStep>();
+    if constexpr (kAct) {
+      read_frags(nxt, 0, 0);
+      mma_step((kSub - 1) & 1);
+      interleave_loads_reads<kMfmaPerStep, LB, kReadsPerStep>();
+    }
   };
 
   // ---- main loop: a multiple of RING stages; a padding stage (K past the
@@ -806,12 +817,19 @@ gemm_tile(const GemmBatch& B, char* const (&ring)[RING], int item)
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * LB) : "memory");
   }
   lds_barrier();
-  read_frags(ring[0], 0, 0);
-  for (int ktl = 0; ktl < nst_pad; ktl += RING) {
+  auto main_loop = [&](auto act) {
+    if constexpr (decltype(act)::value) { read_frags(ring[0], 0, 0); }
+    for (int ktl = 0; ktl < nst_pad; ktl += RING) {
 #pragma unroll
-    for (int r = 0; r < RING; ++r) {
-      stage(ring[r], ring[(r + 1) % RING], ktl + r);
+      for (int r = 0; r < RING; ++r) {
+        stage(act, ring[r], ring[(r + 1) % RING], ktl + r);
+      }
     }
+  };
+  if (t.row0 + wm * 128 < P.rows) {
+    main_loop(std::true_type{});
+  } else {
+    main_loop(std::false_type{});
   }
   // No load may still be writing LDS when the workgroup retires.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
