@@ -9,7 +9,9 @@
 //
 // Tile: 256 activation rows x 256 weight rows.  The default workgroup has
 // 8 waves (2 per SIMD) in a 2x4 grid, each owning 128 activation rows x 64
-// weight rows; the 4-wave workgroup owns 128x128 per wave.  K is staged
+// weight rows (wave w: rows 128*(w/4).., weight rows 64*(w%4)..; the two
+// waves of a SIMD own the two row halves); the 4-wave workgroup owns
+// 128x128 per wave.  K is staged
 // through LDS 128 bytes at a time (64 bf16 or 128 int8): both element types
 // share one byte layout, one load schedule and one swizzle.  The MFMA is a
 // trait (Mma*): v_mfma_f32_32x32x16_bf16 for bf16, v_mfma_i32_16x16x64_i8
@@ -21,9 +23,10 @@
 // stores as one 8-byte (bf16) or 16-byte (int32) write.
 //
 // LDS: two stages of [256 weight rows | 256 activation rows] x 128 bytes.
-// Row r's 16-byte chunk c sits at chunk position c ^ (r & 7), so the eight
-// rows a fragment read touches at one k-chunk land in eight different bank
-// groups, and the 8 lanes that write one row write all eight positions.
+// Row r's 16-byte chunk c sits at chunk position c ^ ((r >> 1) & 7), so
+// the 16 rows a fragment read touches at one k-chunk land in 16 different
+// bank groups, and the 8 lanes that write one row write all eight
+// positions.
 //
 // Global loads use buffer resources sized to the tile's valid rows, so rows
 // past M or N read as zero in hardware; a K tail (K not a multiple of the
