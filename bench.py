@@ -355,6 +355,60 @@ def attention_measure(torch, ops, gen, launches):
                          "frac": round(tf / PEAK_BF16, 4)}}
 
 
+def attention_masks_measure(torch, ops, gen, launches):
+    """The causal and block-causal kernels at the generation pass's shape:
+    4096 queries after a 128-token prefix (q_offset 128) over 4224 keys.
+    Block-causal t: the prefix's tokens distinct (0..127), then four image
+    blocks of 1024 tokens with t = 128..131, so a query sees the prefix and
+    the blocks up to its own.  FLOP counts only the visible (query, key)
+    pairs (4 * d per pair and head)."""
+    import numpy as np
+    a = ATTN
+    pre = a["tk"] - a["tq"]
+    q = torch.randn(a["hq"], a["tq"], a["d"], generator=gen, device="cuda").to(torch.bfloat16)
+    k = torch.randn(a["hkv"], a["tk"], a["d"], generator=gen, device="cuda").to(torch.bfloat16)
+    v = torch.randn(a["hkv"], a["tk"], a["d"], generator=gen, device="cuda").to(torch.bfloat16)
+    out = torch.empty_like(q)
+    t_np = np.concatenate([np.arange(pre), pre + np.arange(a["tq"]) // 1024]).astype(np.int32)
+    t_index = torch.from_numpy(t_np).cuda()
+    qpos = pre + np.arange(a["tq"])
+    pairs = {
+        "causal": int(np.sum(qpos + 1)),
+        # keys j with t[j] <= t[i]; t is non-decreasing, so a searchsorted
+        "block_causal": int(np.sum(np.searchsorted(t_np, t_np[qpos], side="right"))),
+    }
+    calls = {
+        "causal": lambda: ops.sdpa(q, k, v, out, a["hkv"], a["tk"], causal=True,
+                                   q_offset=pre),
+        "block_causal": lambda: ops.sdpa_block_causal(q, k, v, out, t_index, a["hkv"],
+                                                      a["tk"], q_offset=pre),
+    }
+    res = {}
+    for mode, kern in (("causal", "attention_kernel<128, 1>"),
+                       ("block_causal", "attention_kernel<128, 2>")):
+        fn = calls[mode]
+        for _ in range(3):
+            fn()
+        hev = HipEvents()
+        stream = torch.cuda.current_stream()
+        e0, e1 = hev.create(), hev.create()
+        torch.cuda.synchronize()
+        hev.record(e0, stream)
+        for _ in range(launches):
+            fn()
+        hev.record(e1, stream)
+        torch.cuda.synchronize()
+        ms = hev.elapsed(e0, e1) / launches
+        hev.close()
+        flop = 4 * a["hq"] * a["d"] * pairs[mode]
+        tf = flop / (ms * 1e-3) / 1e12
+        res[mode] = {"kernel": kern, "q_offset": pre, "avg_launch_ms": round(ms, 5),
+                     "visible_pairs_per_head": pairs[mode], "flop_per_launch": flop,
+                     "value": round(tf, 2), "unit": "TFLOP/s",
+                     "frac": round(tf / PEAK_BF16, 4)}
+    return res
+
+
 def norm_rope_measure(torch, ops, gen, launches):
     """Average launch time of the fused split q/k norm + split RoPE pass
     over config 2's q (32 heads) and k (8 heads) rows: 4224 tokens,
@@ -563,7 +617,9 @@ def main():
     ops = u15h.Ops(0)
     gen = torch.Generator(device="cuda").manual_seed(args.seed)
     if args.attn_only:
-        print(json.dumps(attention_measure(torch, ops, gen, args.steps)), flush=True)
+        res = attention_measure(torch, ops, gen, args.steps)
+        res["masks"] = attention_masks_measure(torch, ops, gen, args.steps)
+        print(json.dumps(res), flush=True)
         ops.close()
         return
     want_i8 = not args.no_int8
@@ -637,6 +693,7 @@ def main():
         }
     if not args.no_attn:
         result["attention"] = attention_measure(torch, ops, gen, args.steps)
+        result["attention"]["masks"] = attention_masks_measure(torch, ops, gen, args.steps)
         result["split_norm_rope"] = norm_rope_measure(torch, ops, gen, args.steps)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

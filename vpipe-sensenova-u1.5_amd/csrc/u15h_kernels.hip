@@ -1462,7 +1462,9 @@ attention_kernel(const AttnArgs A)
   const int b = blockIdx.x;
   const int item = (items % 8 == 0) ? (b % 8) * (items / 8) + b / 8 : b;
   const int h = item / ntq;
-  const int qt = item % ntq;
+  // With a mask, later query tiles see more keys: they are dealt first, so
+  // the long workgroups start early instead of forming the tail.
+  const int qt = MODE == 0 ? item % ntq : ntq - 1 - item % ntq;
   const int kvh = h / (A.hq / A.hkv);
 
   const int tid = threadIdx.x;
@@ -1551,8 +1553,47 @@ attention_kernel(const AttnArgs A)
   f32x16_t sc[2];           // scores of the current tile
   float mb = -INFINITY;     // their max over the row (both halves)
 
-  const int ntiles = (A.tk + BK - 1) / BK;
   const int q_first = A.q_offset + qt * 128;      // workgroup's first query
+  // One past the last key any of the workgroup's queries sees; the tiles
+  // after it are fully masked and would add exactly 0.
+  int kend = A.tk;
+  if constexpr (MODE != 0) {
+    const int q_last = A.q_offset + min(A.tq, qt * 128 + 128) - 1;
+    kend = min(A.tk, q_last + 1);
+  }
+  if constexpr (MODE == 2) {
+    // Keys past q_last are visible only through an equal t.  Bound them by
+    // the t range of the workgroup's queries: the last key whose t lies in
+    // [tmin, tmax] (a superset of the visible keys; the mask is exact).
+    __shared__ int kred[3][4];
+    int tmin = INT_MAX, tmax = INT_MIN;
+    if (tid < 128 && qt * 128 + tid < A.tq) {
+      const int tv = A.t_index[q_first + tid];
+      tmin = tv;
+      tmax = tv;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      tmin = min(tmin, __shfl_xor(tmin, o));
+      tmax = max(tmax, __shfl_xor(tmax, o));
+    }
+    if (lane == 0) { kred[0][wave] = tmin; kred[1][wave] = tmax; }
+    __syncthreads();
+    tmin = min(min(kred[0][0], kred[0][1]), min(kred[0][2], kred[0][3]));
+    tmax = max(max(kred[1][0], kred[1][1]), max(kred[1][2], kred[1][3]));
+    int jm = kend - 1;
+#pragma unroll 8
+    for (int j = kend + tid; j < A.tk; j += 256) {
+      const int tv = A.t_index[j];
+      if (tv >= tmin && tv <= tmax) { jm = j; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) { jm = max(jm, __shfl_xor(jm, o)); }
+    if (lane == 0) { kred[2][wave] = jm; }
+    __syncthreads();
+    kend = max(max(kred[2][0], kred[2][1]), max(kred[2][2], kred[2][3])) + 1;
+  }
+  const int ntiles = (kend + BK - 1) / BK;
 
   // -inf for the scores of tile j0 that the mode hides; a no-op for a tile
   // whose keys are all below tk and (causal masks) the first query
