@@ -213,12 +213,19 @@ store_dequant4(const GemmProblem& P, int m, int n, int a0, int a1, int a2,
 
 // SwiGLU: gate and up are rounded to bf16 first (the unfused GEMMs' output
 // precision), then silu(gate) * up in fp32, rounded to bf16.
+// silu(g) = g / (1 + e^-g) as g * rcp(1 + 2^(-g log2 e)) with the hardware
+// exp2 and reciprocal (v_exp_f32, v_rcp_f32, ~1 ulp each): 6 VALU
+// operations instead of the ~25 of libm's expf and an IEEE division.  The
+// result is rounded to bf16 (8 significant bits) afterwards.  Every SwiGLU
+// here (the elementwise kernel, the fused epilogue, the split reduction)
+// uses this one helper, so they agree bit for bit.
 __device__ __forceinline__ float
 swiglu_f(float g, float u)
 {
   const float gv = bf16_round(g);
   const float uv = bf16_round(u);
-  return (gv / (1.0f + expf(-gv))) * uv;
+  const float e = __builtin_amdgcn_exp2f(gv * -1.4426950408889634f);
+  return (gv * __builtin_amdgcn_rcpf(1.0f + e)) * uv;
 }
 
 __device__ __forceinline__ uint32_t
@@ -1091,9 +1098,7 @@ swiglu_kernel(const uint4* __restrict__ g, const uint4* __restrict__ u,
     for (int e = 0; e < 4; ++e) {
       const float g0 = bf16_to_f32(gw[e] & 0xffffu), g1 = bf16_to_f32(gw[e] >> 16);
       const float u0 = bf16_to_f32(uw[e] & 0xffffu), u1 = bf16_to_f32(uw[e] >> 16);
-      const float h0 = (g0 / (1.0f + expf(-g0))) * u0;
-      const float h1 = (g1 / (1.0f + expf(-g1))) * u1;
-      ow[e] = bf16_bits(h0) | (bf16_bits(h1) << 16);
+      ow[e] = pack_bf16x2(swiglu_f(g0, u0), swiglu_f(g1, u1));
     }
     o[i] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
   }
