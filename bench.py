@@ -662,7 +662,7 @@ def main():
                      "peak": PEAK_BF16, "unit": "TFLOP/s",
                      "frac": round(kern_tflops / PEAK_BF16, 4),
                      "traffic": measured_traffic(),
-                     "kernel": "mot_gemm_kernel<MmaBf16, kBf16, 4>",
+                     "kernel": "mot_gemm_kernel<MmaBf16x16, kBf16, 4>",
                      "avg_launch_ms": round(kern_ms, 5),
                      "flop_per_launch": kern_flop,
                      "alg_bytes_per_launch": int(traffic_alg),

@@ -24,7 +24,7 @@ struct u15h_ctx {
   bool split_on = true;      // env U15H_SPLIT=0 turns the split-K tail off
   // GEMM kernel build: 8 or 4 waves (env U15H_WAVES), four-stage LDS ring
   // or two-stage pipeline (env U15H_RING=1/0).
-  u15h::GemmShape gemm = {8, 0, -1};
+  u15h::GemmShape gemm = {8, 0, 1};
   // One-shot profiling event: recorded after the next GEMM kernel.
   hipEvent_t profile_event = nullptr;
   // Partial-sum workspace of split tiles: at most num_cu K shares of one
@@ -344,7 +344,7 @@ u15h_create(int device, u15h_ctx** out)
   ctx->split_on = env_int("U15H_SPLIT", 1) != 0;
   ctx->gemm.waves = env_int("U15H_WAVES", 8) == 4 ? 4 : 8;
   ctx->gemm.cus = env_int("U15H_PERSIST", 1) != 0 ? ctx->num_cu : 0;
-  ctx->gemm.mfma16 = std::max(-1, std::min(1, env_int("U15H_MFMA16", -1)));
+  ctx->gemm.mfma16 = std::max(-1, std::min(1, env_int("U15H_MFMA16", 1)));
   ctx->i8_min_m = std::max(1, env_int("U15H_I8_MIN_M", 1024));
   *out = ctx;
   return U15H_OK;

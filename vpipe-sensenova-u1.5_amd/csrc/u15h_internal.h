@@ -77,9 +77,9 @@ inline size_t split_ws_bytes(const GemmBatch& b)
 struct GemmShape {
   int waves;
   int cus;
-  // 8-wave workgroup MFMA shape: 1 = 16x16 for both types, 0 = 32x32 for
-  // both, -1 = 16x16 for int8 and 32x32 for bf16 (the measured best).  The
-  // 4-wave workgroup always runs 16x16.
+  // 8-wave workgroup MFMA shape: 1 = 16x16 for both types (the measured
+  // best, the default), 0 = 32x32 for both, -1 = 16x16 for int8 and 32x32
+  // for bf16.  The 4-wave workgroup always runs 16x16.
   int mfma16;
 };
 

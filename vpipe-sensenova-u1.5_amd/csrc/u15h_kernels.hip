@@ -14,8 +14,9 @@
 // 128x128 per wave.  K is staged
 // through LDS 128 bytes at a time (64 bf16 or 128 int8): both element types
 // share one byte layout, one load schedule and one swizzle.  The MFMA is a
-// trait (Mma*): v_mfma_f32_32x32x16_bf16 for bf16, v_mfma_i32_16x16x64_i8
-// for int8 by default, each taking 16 bytes of K per lane.
+// trait (Mma*): by default the 16x16 shapes, v_mfma_f32_16x16x32_bf16 and
+// v_mfma_i32_16x16x64_i8 (the 32x32 ones as an option), each taking 16
+// bytes of K per lane.
 //
 // Operand order: the WEIGHT fragment is the MFMA's first operand, so the
 // accumulator's rows are output columns.  A lane then holds groups of four
