@@ -343,10 +343,11 @@ def ops_4waves():
 
 @pytest.mark.parametrize("Mu,Mg,K,N", [(37, 263, 1032, 264), (128, 4096, 4096, 1024)])
 def test_workgroup_shapes_agree(ops, ops_4waves, Mu, Mg, K, N):
-    """The 8-wave workgroup (32x32x16 MFMAs) and the 4-wave one (16x16x32
-    MFMAs): the f32 sums round at different K chunk boundaries, so the bf16
-    outputs and the fused SwiGLU outputs agree within the bar, and both
-    match the oracle on sampled rows."""
+    """The 8-wave workgroup (128x64 per wave) and the 4-wave one (128x128
+    per wave, accumulators pinned in AGPRs by inline-asm MFMAs): the f32
+    sums may round differently, so the bf16 outputs and the fused SwiGLU
+    outputs agree within the bar, and both match the oracle on sampled
+    rows."""
     M = Mu + Mg
     g = torch.Generator(device="cuda").manual_seed(K + N)
     x = torch.randn(M, K, generator=g, device="cuda").to(torch.bfloat16)

@@ -309,4 +309,18 @@ def test_i32_four_wave_workgroup_bit_exact(Mu, Mg, K, N):
     for r in (0, Mu - 1, Mu, M // 2, M - 1):
         w = wu if r < Mu else wg
         assert np.array_equal(out[r:r + 1], oracle.gemm_i8_i32(xq[r:r + 1], w))
+    # the fused dequant epilogue of the same workgroup, on the checked
+    # accumulators: bit-exact against the oracle's expression
+    sx = (rng.random(M, dtype=np.float32) * 0.01 + 1e-4).astype(np.float32)
+    swu = (rng.random(N, dtype=np.float32) * 0.01 + 1e-4).astype(np.float32)
+    swg = (rng.random(N, dtype=np.float32) * 0.01 + 1e-4).astype(np.float32)
+    yb = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    o4.mot_gemm_i8(torch.from_numpy(xq).cuda(), torch.from_numpy(sx).cuda(), Mu, Mg,
+                   K, [_proj(torch.from_numpy(wu).cuda(), torch.from_numpy(swu).cuda(),
+                             torch.from_numpy(wg).cuda(), torch.from_numpy(swg).cuda(),
+                             yb)])
+    torch.cuda.synchronize()
+    yb_h = host_bits(yb)
+    for lo, hi, sw in ((0, Mu, swu), (Mu, M, swg)):
+        assert np.array_equal(yb_h[lo:hi], oracle.dequant_bf16(out[lo:hi], sx[lo:hi], sw))
     o4.close()

@@ -22,8 +22,8 @@ struct u15h_ctx {
   int device = 0;
   int num_cu = 256;
   bool split_on = true;      // env U15H_SPLIT=0 turns the split-K tail off
-  // GEMM kernel build: 8 or 4 waves (env U15H_WAVES), four-stage LDS ring
-  // or two-stage pipeline (env U15H_RING=1/0).
+  // GEMM kernel build: 8 or 4 waves per workgroup (env U15H_WAVES) and the
+  // 8-wave build's MFMA shape (env U15H_MFMA16).
   u15h::GemmShape gemm = {8, 0, 1};
   // One-shot profiling event: recorded after the next GEMM kernel.
   hipEvent_t profile_event = nullptr;

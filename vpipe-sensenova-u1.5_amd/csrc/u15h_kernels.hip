@@ -11,7 +11,8 @@
 // 8 waves (2 per SIMD) in a 2x4 grid, each owning 128 activation rows x 64
 // weight rows (wave w: rows 128*(w/4).., weight rows 64*(w%4)..; the two
 // waves of a SIMD own the two row halves); the 4-wave workgroup owns
-// 128x128 per wave.  K is staged
+// 128x128 per wave, its 256 accumulator registers pinned in AGPRs by
+// inline-asm MFMAs whose source order is the loop's schedule.  K is staged
 // through LDS 128 bytes at a time (64 bf16 or 128 int8): both element types
 // share one byte layout, one load schedule and one swizzle.  The MFMA is a
 // trait (Mma*): by default the 16x16 shapes, v_mfma_f32_16x16x32_bf16 and
@@ -168,6 +169,29 @@ struct MmaI8x16 {                // v_mfma_i32_16x16x64_i8
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
   }
 };
+
+// A 16x16 MFMA whose accumulator input and result are one AGPR tuple ("+a").
+// The 4-wave workgroup holds 256 accumulator registers per lane; with the
+// builtins the compiler gives the 16x16 MFMAs (which, unlike the 32x32 ones,
+// have no tied-accumulator form) a different result tuple than input and
+// shuffles the accumulators through VGPRs every stage.  Volatile, so these
+// MFMAs keep their source order relative to each other and to the fragment
+// reads and loads written between them: the source order is the schedule.
+// The compiler's hazard tracking does not see inside the asm, so callers
+// cover the two hazards it would: a VALU write of an accumulator (the
+// zeroing) followed by the MFMA's read, and the MFMA's write followed by a
+// VALU read (the epilogue's v_accvgpr_read), each with s_nop wait states.
+template <class Mma>
+__device__ __forceinline__ void
+mfma_pinned(typename Mma::acc_t& c, i32x4_t a, i32x4_t b)
+{
+  static_assert(Mma::kF == 16, "pinned MFMAs are the 16x16 shapes");
+  if constexpr (Mma::kInt) {
+    asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+  } else {
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+  }
+}
 
 // The accumulators of one wave: weight fragments x activation fragments
 // (the wave covers kBN / WN weight rows and 128 activation rows).
@@ -708,22 +732,30 @@ gemm_tile(const GemmBatch& B, char* const (&ring)[RING], int item)
   const int tail_odd =
       ((nk - 1) * KB + (chunk_odd << 4) < kbytes) ? 0 : kOobOffset;
 
-  auto issue_loads = [&](char* stage_base, int ktl) {
+  // A stage's loads: per-stage offsets, then LB blocks of 1 KiB each.
+  struct LoadArgs { int ko, ve, vo; };
+  auto load_args = [&](int ktl) {
     const int kt = t.kbeg + ktl;
-    const int ko = __builtin_amdgcn_readfirstlane(min(kt, nk - 1) * KB);
     const bool last = kt == nk - 1;
     const int oob = ktl >= t.nst ? kOobOffset : 0;
-    const int ve = lane_even + row_base * pitch + (last ? tail_even : 0) + oob;
-    const int vo = lane_odd + row_base * pitch + (last ? tail_odd : 0) + oob;
+    LoadArgs a;
+    a.ko = __builtin_amdgcn_readfirstlane(min(kt, nk - 1) * KB);
+    a.ve = lane_even + row_base * pitch + (last ? tail_even : 0) + oob;
+    a.vo = lane_odd + row_base * pitch + (last ? tail_odd : 0) + oob;
+    return a;
+  };
+  auto load_block = [&](const LoadArgs& a, char* stage_base, int b) {
     char* dst = stage_base + wave * (kRowsPerWave * KB);
+    const int orow = (b & bmask) * kRowsPerBlock;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        b < LB / 2 ? r_lo : r_hi,
+        (__attribute__((address_space(3))) void*)(dst + b * 1024), 16,
+        ((b & 1) ? a.vo : a.ve) + orow * pitch, a.ko, 0, 0);
+  };
+  auto issue_loads = [&](char* stage_base, int ktl) {
+    const LoadArgs a = load_args(ktl);
 #pragma unroll
-    for (int b = 0; b < LB; ++b) {
-      const int orow = (b & bmask) * kRowsPerBlock;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          b < LB / 2 ? r_lo : r_hi,
-          (__attribute__((address_space(3))) void*)(dst + b * 1024), 16,
-          ((b & 1) ? vo : ve) + orow * pitch, ko, 0, 0);
-    }
+    for (int b = 0; b < LB; ++b) { load_block(a, stage_base, b); }
   };
 
   // ---- MFMA fragments ---------------------------------------------------
@@ -746,6 +778,18 @@ gemm_tile(const GemmBatch& B, char* const (&ring)[RING], int item)
   for (int i = 0; i < FI; ++i) {
 #pragma unroll
     for (int j = 0; j < FJ; ++j) { acc[i][j] = typename Mma::acc_t{}; }
+  }
+  // The 4-wave workgroup runs the pinned MFMAs.  The empty asm statements
+  // order the zeroing (VALU writes of the AGPRs) before the s_nop, which
+  // gives the first MFMAs' accumulator reads their wait states.
+  constexpr bool kPin = WN == 2;
+  if constexpr (kPin) {
+#pragma unroll
+    for (int i = 0; i < FI; ++i) {
+#pragma unroll
+      for (int j = 0; j < FJ; ++j) { asm volatile("" : "+a"(acc[i][j])); }
+    }
+    asm volatile("s_nop 4");
   }
 
   i32x4_t fa[2][FI], fb[2][FJ];
@@ -773,6 +817,32 @@ gemm_tile(const GemmBatch& B, char* const (&ring)[RING], int item)
   constexpr int kMfmaPerStep = FI * FJ;
   constexpr int kReadsPerStep = FI + FJ;
 
+  // Pinned schedule (4 waves): fragment read r of a sub-step, in the order
+  // the next sub-step first uses them (a0, b0..b7, a1..a7), so its first
+  // MFMAs wait for two reads, not nine.
+  auto read_one = [&](const char* base, int s, int buf, int r) {
+    const int q = r == 0 ? 0 : (r <= FJ ? FI + r - 1 : r - FJ);
+    if (q < FI) {
+      fa[buf][q] = *reinterpret_cast<const i32x4_t*>(base + wbase + q * Mma::kF * KB +
+                                                     rd[s]);
+    } else {
+      fb[buf][q - FI] = *reinterpret_cast<const i32x4_t*>(
+          base + abase + (q - FI) * Mma::kF * KB + rd[s]);
+    }
+  };
+  // One sub-step's MFMAs with `between(k)` after MFMA k: that is where the
+  // reads and loads issue (the MFMAs are volatile asm, so they stay put).
+  auto pinned_step = [&](int buf, auto&& between) {
+#pragma unroll
+    for (int i = 0; i < FI; ++i) {
+#pragma unroll
+      for (int j = 0; j < FJ; ++j) {
+        mfma_pinned<Mma>(acc[i][j], fa[buf][i], fb[buf][j]);
+        between(i * FJ + j);
+      }
+    }
+  };
+
   // One K stage in ring buffer `cur`; `nxt` holds the next stage.  On entry
   // the fragments of sub-step 0 are in fa/fb[0]; the fragments of sub-step
   // s+1 are read while the MFMAs of sub-step s run.  Before the last
@@ -790,6 +860,31 @@ gemm_tile(const GemmBatch& B, char* const (&ring)[RING], int item)
   // to the partner wave; its accumulators stay zero and are never stored.
   auto stage = [&](auto act, char* cur, const char* nxt, int ktl) {
     constexpr bool kAct = decltype(act)::value;
+    if constexpr (kPin) {
+      // The same hand-off, scheduled in source: one read after every 4th
+      // MFMA (from MFMA 1 in the first sub-step, from MFMA 2 in the last),
+      // and in the last sub-step one 1 KiB load after every 4th MFMA from
+      // MFMA 0 -- spread loads issue without stalling the MFMA stream.
+      static_assert(kSub == 2 && kMfmaPerStep == 4 * kReadsPerStep &&
+                    LB == kReadsPerStep, "pinned schedule: 64 MFMAs, 16 reads, 16 loads");
+      if constexpr (kAct) {
+        pinned_step(0, [&](int k) {
+          if (k % 4 == 1) { read_one(cur, 1, 1, k / 4); }
+        });
+      }
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+      __syncthreads();
+      if constexpr (kAct) {
+        const LoadArgs la = load_args(ktl + RING);
+        pinned_step(1, [&](int k) {
+          if (k % 4 == 0) { load_block(la, cur, k / 4); }
+          if (k % 4 == 2) { read_one(nxt, 0, 0, k / 4); }
+        });
+      } else {
+        issue_loads(cur, ktl + RING);
+      }
+      return;
+    }
     if constexpr (kAct) {
 #pragma unroll
       for (int s = 0; s + 1 < kSub; ++s) {
@@ -829,7 +924,19 @@ gemm_tile(const GemmBatch& B, char* const (&ring)[RING], int item)
   }
   lds_barrier();
   auto main_loop = [&](auto act) {
-    if constexpr (decltype(act)::value) { read_frags(ring[0], 0, 0); }
+    if constexpr (decltype(act)::value) {
+      if constexpr (kPin) {
+        // In the loop's read order (the scheduling barriers keep it), so
+        // the loop's waits are the same from either predecessor.
+#pragma unroll
+        for (int r = 0; r < kReadsPerStep; ++r) {
+          read_one(ring[0], 0, 0, r);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+        read_frags(ring[0], 0, 0);
+      }
+    }
     for (int ktl = 0; ktl < nst_pad; ktl += RING) {
 #pragma unroll
       for (int r = 0; r < RING; ++r) {
@@ -844,6 +951,17 @@ gemm_tile(const GemmBatch& B, char* const (&ring)[RING], int item)
   }
   // No load may still be writing LDS when the workgroup retires.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if constexpr (kPin) {
+    // 32 wait states between the last MFMA's result and the epilogue's
+    // reads of the AGPRs (more than the 16x16 shapes' pass count needs);
+    // the empty asm statements order those reads after them.
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7");
+#pragma unroll
+    for (int i = 0; i < FI; ++i) {
+#pragma unroll
+      for (int j = 0; j < FJ; ++j) { asm volatile("" : "+a"(acc[i][j])); }
+    }
+  }
 
   gemm_epilogue<Mma, E, WN>(B, P, t, wm, wn, lane, acc, ring);
 }
