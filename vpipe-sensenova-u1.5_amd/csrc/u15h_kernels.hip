@@ -498,7 +498,7 @@ gemm_epilogue_staged(const GemmProblem& P, const TileWork& t, int wm, int wn,
   // Read back: wave w stores tile rows [RW w, RW w + RW) (RW = 256 / waves);
   // 64 / CH rows per instruction, CH lanes per row.
   constexpr int RW = kBM / (2 * WN);
-  const int wave = (int)(threadIdx.x >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   constexpr int kRowsPerRead = 64 / CH;
   // The read-back addresses depend on the lane only; computed from an
   // opaque copy of it they stay here instead of being hoisted out of the
@@ -552,8 +552,13 @@ gemm_epilogue(const GemmBatch& B, const GemmProblem& P, const TileWork& t,
   constexpr int FJ = 128 / kF;
   constexpr int kGr = Mma::kE / 4;
   constexpr int kGs = 4 * (64 / kF);
-  const int lr = lane % kF;
-  const int lh = lane / kF;
+  // Lane-derived offsets from an opaque copy of the lane: computed here,
+  // per tile, instead of being hoisted to the kernel's start and spilled
+  // across the main loop (a reload waits for every store in flight).
+  int lane_e = lane;
+  asm volatile("" : "+v"(lane_e));
+  const int lr = lane_e % kF;
+  const int lh = lane_e / kF;
   if (t.is_split) {
     int32_t* wsb = static_cast<int32_t*>(B.ws) +
                    (size_t)((t.tile - B.split_begin) * B.split + t.share) *
@@ -577,7 +582,7 @@ gemm_epilogue(const GemmBatch& B, const GemmProblem& P, const TileWork& t,
     return;
   }
   if constexpr (E != Epi::kI32) {
-    gemm_epilogue_staged<Mma, E, WN>(P, t, wm, wn, lane, acc, ring);
+    gemm_epilogue_staged<Mma, E, WN>(P, t, wm, wn, lane_e, acc, ring);
     return;
   }
 #pragma unroll
@@ -632,8 +637,10 @@ gemm_epilogue(const GemmBatch& B, const GemmProblem& P, const TileWork& t,
 // buffer is free, so a load has RING-1 stages to land.
 //
 // WN = waves along the tile's N (weight-row) extent; 2 waves along M.
-//   WN = 2: 4 waves, each 128 x 128 (4 x 4 accumulators of 32 x 32)
-//   WN = 4: 8 waves, two per SIMD, each 128 x 64 (2 x 4 accumulators); a
+//   WN = 2: 4 waves, each 128 x 128 (8 x 8 accumulators of 16 x 16,
+//           pinned in AGPRs)
+//   WN = 4: 8 waves, two per SIMD, each 128 x 64 (4 x 8 accumulators of
+//           16 x 16, or 2 x 4 of 32 x 32); a
 //           wave waiting on LDS, memory or the barrier leaves the matrix
 //           core to the other wave of its SIMD.
 //
