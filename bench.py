@@ -15,9 +15,12 @@ fused dequant, weights quantised per output channel once, up front.
 Prints ONE JSON line (rank 0).  `value` is bf16 TFLOP/s of the whole step;
 the int8 tier's TOPS ride in "int8"; "attention" times the layer's
 attention over the K/V cache at config 2's generation-pass shape and
-"split_norm_rope" the fused q/k norm + RoPE pass on its q and k rows.  "roofline" is the dominant kernel
-(the bf16 grouped GEMM), timed per launch with HIP events on the stream it
-runs on; "cpu_baseline" times the reference's CPU linear (or the oracle's
+"split_norm_rope" the fused q/k norm + RoPE pass on its q and k rows.
+"roofline" is the dominant kernel (the bf16 grouped GEMM), timed per launch
+with HIP events on the stream it runs on: against the MFMA peak above the
+ridge, against 8 TB/s below it (small M, e.g. --m-und 128 --m-gen 0, where
+the weights dominate the bytes; achieved_GBps is reported either way);
+"cpu_baseline" times the reference's CPU linear (or the oracle's
 restatement) on a bounded sample of config 1 on this host, single thread.
 The int8, attention and norm/RoPE objects carry their own "cpu_baseline"
 (the oracle's exact int8 GEMM, the reference's CPU attention, the oracle's
@@ -92,20 +95,38 @@ def parse():
 
 
 COPY_PROBE_BYTES = 1 << 30
-TRAFFIC_FILE = REPO / "profiles" / "mot_gemm_bf16_c2_traffic.txt"
+# (layers, m_und, m_gen) -> rocprof traffic summary of that token split
+TRAFFIC_FILES = {
+    (1, 128, 4096): REPO / "profiles" / "mot_gemm_bf16_c2_traffic.txt",
+    (1, 128, 0): REPO / "profiles" / "mot_gemm_bf16_und128_traffic.txt",
+}
 
 
-def measured_traffic():
-    """HBM bytes per launch of the bf16 grouped GEMM at config 2, as the
-    committed rocprof FETCH_SIZE / WRITE_SIZE summary records them (scaled
-    by a plain copy of known size), or None if not measured."""
+def measured_traffic(args):
+    """HBM bytes per launch of the bf16 grouped GEMM, as the committed
+    rocprof FETCH_SIZE / WRITE_SIZE summary of this token split records them
+    (scaled by a plain copy of known size), or None if not measured."""
+    f = TRAFFIC_FILES.get((args.layers, args.m_und, args.m_gen))
+    if f is None:
+        return None
     try:
-        for line in TRAFFIC_FILE.read_text().splitlines():
+        for line in f.read_text().splitlines():
             if line.startswith("hbm_bytes_per_launch:"):
                 return int(float(line.split(":", 1)[1]))
     except OSError:
         pass
     return None
+
+
+def _roof(flop, nbytes, achieved, gbps, peak, unit):
+    """The roofline that bounds a launch of `flop` operations over `nbytes`
+    algorithmic bytes: the matrix cores above the ridge (peak / 8 TB/s),
+    HBM below it (small M: the weights dominate the bytes)."""
+    if flop / nbytes < peak * 1e12 / (PEAK_HBM * 1e9):
+        return {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM,
+                "unit": "GB/s", "frac": round(gbps / PEAK_HBM, 4)}
+    return {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak,
+            "unit": unit, "frac": round(achieved / peak, 4)}
 
 
 def copy_probe():
@@ -636,11 +657,14 @@ def main():
     kern_flop = flop / len(runs)
     kern_tflops = kern_flop / (kern_ms * 1e-3) / 1e12
     # HBM bytes the kernel must move per launch (averaged over the step):
-    # each weight read once, activations read once, outputs written once.
-    wbytes = 2 * 2 * FLOP_PER_ROW // 2
+    # each weight set with rows read once (FLOP_PER_ROW bytes of bf16 per
+    # set), activations read once, outputs written once.
+    nsets = (args.m_und > 0) + (args.m_gen > 0)
+    wbytes = nsets * FLOP_PER_ROW
     abytes = 2 * M * (HIDDEN + NQ + HIDDEN + INTER)
     obytes = 2 * M * (NQ + 2 * NKV + HIDDEN + 2 * INTER + HIDDEN)
     traffic_alg = (wbytes + abytes + obytes) * args.layers / len(runs)
+    kern_gbps = traffic_alg / (kern_ms * 1e-3) / 1e9
     _, _, _, wdesc = WORKLOADS[args.workload]
 
     result = {
@@ -658,15 +682,15 @@ def main():
                    "launches_per_step": len(runs),
                    "fused_swiglu": bool(args.fused_swiglu)},
         "pct_of_peak": round(100 * tflops / PEAK_BF16, 2),
-        "roofline": {"bound": "mfma", "achieved": round(kern_tflops, 2),
-                     "peak": PEAK_BF16, "unit": "TFLOP/s",
-                     "frac": round(kern_tflops / PEAK_BF16, 4),
-                     "traffic": measured_traffic(),
-                     "kernel": "mot_gemm_kernel<MmaBf16x16, kBf16, 4>",
-                     "avg_launch_ms": round(kern_ms, 5),
-                     "flop_per_launch": kern_flop,
-                     "alg_bytes_per_launch": int(traffic_alg),
-                     "split_reduce_ms_per_step": round(red_ms / args.steps, 5)},
+        "roofline": dict(
+            _roof(kern_flop, traffic_alg, kern_tflops, kern_gbps, PEAK_BF16,
+                  "TFLOP/s"),
+            traffic=measured_traffic(args),
+            kernel="mot_gemm_kernel<MmaBf16x16, kBf16, 4>",
+            avg_launch_ms=round(kern_ms, 5), flop_per_launch=kern_flop,
+            alg_bytes_per_launch=int(traffic_alg),
+            achieved_GBps=round(kern_gbps, 1),
+            split_reduce_ms_per_step=round(red_ms / args.steps, 5)),
     }
     if want_i8:
         runs8 = i8_launches(ops, layers, A)
@@ -677,16 +701,24 @@ def main():
         g_tops = (flop / 4) / (g_ms * 1e-3) / 1e12
         q_ms = per8["quant"][0] / per8["quant"][1]
         q_bytes = (3 * M * (HIDDEN + NQ + HIDDEN + INTER) + 4 * 4 * M) / 4
+        # int8 GEMM launch bytes: int8 weights (half the bf16 bytes) and
+        # per-channel scales, int8 activations and per-token scales, bf16
+        # outputs
+        i8_bytes = (wbytes / 2 + abytes / 2 + obytes
+                    + 4 * (nsets * (NQ + 2 * NKV + HIDDEN + 2 * INTER + HIDDEN)
+                           + 4 * M)) * args.layers / len(runs8)
+        g_gbps = i8_bytes / (g_ms * 1e-3) / 1e9
         result["int8"] = {
             "value": round(tops, 2), "unit": "TOPS",
             "pct_of_peak": round(100 * tops / PEAK_I8, 2),
             "ms_per_step": round(ms8, 4),
-            "roofline": {"bound": "mfma", "achieved": round(g_tops, 2),
-                         "peak": PEAK_I8, "unit": "TOPS",
-                         "frac": round(g_tops / PEAK_I8, 4),
-                         "kernel": "mot_gemm_kernel<MmaI8x16, kDequantBf16, 4>",
-                         "avg_launch_ms": round(g_ms, 5),
-                         "split_reduce_ms_per_step": round(red8 / args.steps, 5)},
+            "roofline": dict(
+                _roof(flop / 4, i8_bytes, g_tops, g_gbps, PEAK_I8, "TOPS"),
+                kernel="mot_gemm_kernel<MmaI8x16, kDequantBf16, 4>",
+                avg_launch_ms=round(g_ms, 5),
+                alg_bytes_per_launch=int(i8_bytes),
+                achieved_GBps=round(g_gbps, 1),
+                split_reduce_ms_per_step=round(red8 / args.steps, 5)),
             "quant_kernel": {"bound": "hbm", "avg_launch_ms": round(q_ms, 5),
                              "achieved_GBps": round(q_bytes / (q_ms * 1e-3) / 1e9, 1),
                              "peak": PEAK_HBM},
