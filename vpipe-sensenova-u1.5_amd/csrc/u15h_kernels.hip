@@ -340,6 +340,22 @@ tile_work(const GemmBatch& B, int nk, int w)
 // Scheduling masks of __builtin_amdgcn_sched_group_barrier.
 constexpr int kSchedMfma = 0x008, kSchedVmem = 0x010, kSchedDsRead = 0x100;
 
+// Fragment read r goes after MFMA kReadEvery*r + kReadEvery-1: every
+// second MFMA when a sub-step has at least twice as many MFMAs as reads
+// (the 16x16 builds: 32 MFMAs, 12 reads), which measured 2.9% (bf16) and
+// 1.4% (int8) faster than one read after each of the first MFMAs; every
+// MFMA otherwise (the 32x32 builds: 8 MFMAs, 6 reads).
+template <int kMfmas, int kReads>
+constexpr int kReadEvery = kMfmas >= 2 * kReads ? 2 : 1;
+
+template <int kMfmas, int kReads>
+__device__ __forceinline__ bool
+read_after(int k)
+{
+  constexpr int E = kReadEvery<kMfmas, kReads>;
+  return k % E == E - 1 && k / E < kReads;
+}
+
 // `reads` fragment reads spread over `mfmas` MFMAs.
 template <int kMfmas, int kReads>
 __device__ __forceinline__ void
@@ -348,7 +364,9 @@ interleave_reads()
 #pragma unroll
   for (int k = 0; k < kMfmas; ++k) {
     __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-    if (k < kReads) { __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0); }
+    if (read_after<kMfmas, kReads>(k)) {
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    }
   }
 }
 
@@ -367,7 +385,9 @@ interleave_loads_reads()
         __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
       }
     }
-    if (k < kReads) { __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0); }
+    if (read_after<kMfmas, kReads>(k)) {
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    }
   }
 }
 
