@@ -371,18 +371,28 @@ interleave_reads()
 }
 
 // `loads` direct loads and `reads` fragment reads spread over `mfmas` MFMAs.
+// With at least two MFMAs per load (the 16x16 builds: 8 loads, 32 MFMAs) a
+// load goes after every second MFMA from the first: int8 +0.8%, bf16 the
+// same, against one load after each of the first MFMAs.
 template <int kMfmas, int kLoads, int kReads>
 __device__ __forceinline__ void
 interleave_loads_reads()
 {
   constexpr int kLoadsPerMfma = (kLoads + kMfmas - 1) / kMfmas;
+  constexpr int kLoadEvery = kMfmas >= 2 * kLoads ? 2 : 1;
 #pragma unroll
   for (int k = 0; k < kMfmas; ++k) {
     __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-#pragma unroll
-    for (int l = 0; l < kLoadsPerMfma; ++l) {
-      if (k * kLoadsPerMfma + l < kLoads) {
+    if constexpr (kLoadEvery == 2) {
+      if (k % 2 == 0 && k / 2 < kLoads) {
         __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
+      }
+    } else {
+#pragma unroll
+      for (int l = 0; l < kLoadsPerMfma; ++l) {
+        if (k * kLoadsPerMfma + l < kLoads) {
+          __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
+        }
       }
     }
     if (read_after<kMfmas, kReads>(k)) {
