@@ -340,20 +340,26 @@ tile_work(const GemmBatch& B, int nk, int w)
 // Scheduling masks of __builtin_amdgcn_sched_group_barrier.
 constexpr int kSchedMfma = 0x008, kSchedVmem = 0x010, kSchedDsRead = 0x100;
 
-// Fragment read r goes after MFMA kReadEvery*r + kReadEvery-1: every
-// second MFMA when a sub-step has at least twice as many MFMAs as reads
-// (the 16x16 builds: 32 MFMAs, 12 reads), which measured 2.9% (bf16) and
-// 1.4% (int8) faster than one read after each of the first MFMAs; every
-// MFMA otherwise (the 32x32 builds: 8 MFMAs, 6 reads).
-template <int kMfmas, int kReads>
-constexpr int kReadEvery = kMfmas >= 2 * kReads ? 2 : 1;
-
+// Where the fragment reads of a sub-step go.  When a sub-step has at least
+// twice as many MFMAs as reads (the 16x16 builds: 32 MFMAs, 12 reads), read
+// r goes after MFMA r * kMfmas / kReads + 1, spread over the whole
+// sub-step: measured +4.6% (bf16) and +1.8% (int8) on the kernel against
+// one read after each of the first 12 MFMAs, and +1.6% (bf16) against one
+// after every second MFMA.  Otherwise (the 32x32 builds: 8 MFMAs, 6
+// reads) one read after each of the first MFMAs.
 template <int kMfmas, int kReads>
 __device__ __forceinline__ bool
 read_after(int k)
 {
-  constexpr int E = kReadEvery<kMfmas, kReads>;
-  return k % E == E - 1 && k / E < kReads;
+  if constexpr (kMfmas >= 2 * kReads) {
+#pragma unroll
+    for (int r = 0; r < kReads; ++r) {
+      if (k == r * kMfmas / kReads + 1) { return true; }
+    }
+    return false;
+  } else {
+    return k < kReads;
+  }
 }
 
 // `reads` fragment reads spread over `mfmas` MFMAs.
