@@ -1162,8 +1162,15 @@ split_reduce_kernel(const GemmBatch B)
 // division.  |x/s| < 127.5, so the fast path needs no clamp; the bytes are
 // packed biased (v_cvt_pk_u8_f32) and unbiased by flipping bit 7.  The
 // codes are the division's, bit for bit.
+//
+// The bound needs inv to be a finite, correctly rounded reciprocal.  For a
+// row whose absmax is below ~127 * 2^-128 (3.7e-37), s is so small that
+// 1/s overflows to +inf; the caller then passes fast = false and every
+// chunk of the row takes the division.  The redo test is written so that
+// a NaN deviation (an inf or NaN product) also selects the division:
+// fmaxf would drop a NaN, and `dev > limit` is false for one.
 __device__ __forceinline__ uint2
-quant8(const uint4 v, float s, float inv)
+quant8(const uint4 v, float s, float inv, bool fast)
 {
   if (s == 0.0f) { return make_uint2(0u, 0u); }       // row of zeros
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -1174,15 +1181,15 @@ quant8(const uint4 v, float s, float inv)
     x[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
   }
   uint32_t packed[2] = {0u, 0u};
-  float dev = 0.0f;
+  bool redo = !fast;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const float u = fmaf(x[e], inv, 128.0f);
     const float n = rintf(u);
-    dev = fmaxf(dev, fabsf(u - n));
+    redo |= !(fabsf(u - n) <= 0.5f - 5e-5f);
     packed[e >> 2] = __builtin_amdgcn_cvt_pk_u8_f32(n, e & 3, packed[e >> 2]);
   }
-  if (dev > 0.5f - 5e-5f) {
+  if (redo) {
     packed[0] = packed[1] = 0u;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -1232,15 +1239,17 @@ quant_rows_i8_kernel(const uint16_t* __restrict__ x, int K,
   amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float s = amax / 127.0f;
   const float inv = s != 0.0f ? 1.0f / s : 0.0f;
+  // 1/s overflows for rows with absmax below ~3.7e-37: division only.
+  const bool fast = inv <= 3.4028234663852886e38f;
   if (threadIdx.x == 0) { sc[r] = s; }
   uint2* qr = reinterpret_cast<uint2*>(q + (size_t)r * K);
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
     const int c = threadIdx.x + i * 256;
-    if (c < nchunk) { qr[c] = quant8(v[i], s, inv); }
+    if (c < nchunk) { qr[c] = quant8(v[i], s, inv, fast); }
   }
   for (int c = threadIdx.x + CPT * 256; c < nchunk; c += 256) {
-    qr[c] = quant8(xr[c], s, inv);
+    qr[c] = quant8(xr[c], s, inv, fast);
   }
 }
 
@@ -2001,16 +2010,19 @@ gather_rows_kernel(const uint16_t* __restrict__ src,
 
 template <class Mma, Epi E, int WN>
 hipError_t
-launch_gemm(const GemmBatch& b, int cus, hipStream_t s, hipEvent_t after_gemm)
+launch_gemm(const GemmBatch& b, int cus, hipStream_t s, const GemmEvents& ev)
 {
   if (b.total_tiles <= 0) { return hipSuccess; }
   const int items = grid_blocks(b);
   const int grid = (cus > 0 && cus < items) ? cus : items;
+  hipError_t e = hipSuccess;
+  if (ev.before != nullptr) { e = hipEventRecord(ev.before, s); }
+  if (e != hipSuccess) { return e; }
   hipLaunchKernelGGL((mot_gemm_kernel<Mma, E, WN>), dim3(grid), dim3(128 * WN),
                      0, s, b);
-  hipError_t e = hipGetLastError();
-  if (e == hipSuccess && after_gemm != nullptr) {
-    e = hipEventRecord(after_gemm, s);
+  e = hipGetLastError();
+  if (e == hipSuccess && ev.after != nullptr) {
+    e = hipEventRecord(ev.after, s);
   }
   if (e != hipSuccess || b.split_begin >= b.total_tiles) { return e; }
   constexpr bool kInt = Mma::kInt;
@@ -2023,7 +2035,7 @@ launch_gemm(const GemmBatch& b, int cus, hipStream_t s, hipEvent_t after_gemm)
 template <class Mma, Epi E>
 hipError_t
 launch_gemm_waves(const GemmBatch& b, const GemmShape& g, hipStream_t s,
-                  hipEvent_t ev)
+                  const GemmEvents& ev)
 {
   // the 4-wave workgroup (one wave per SIMD, 512 registers) runs the 16x16
   // MFMAs; the 8-wave one the 32x32 MFMAs, whose fragments fit 256
@@ -2037,26 +2049,26 @@ launch_gemm_waves(const GemmBatch& b, const GemmShape& g, hipStream_t s,
 
 hipError_t
 launch_gemm_bf16(const GemmBatch& b, Epi epi, const GemmShape& g,
-                 hipStream_t s, hipEvent_t after_gemm)
+                 hipStream_t s, const GemmEvents& ev)
 {
   switch (epi) {
     case Epi::kBf16:
-      return launch_gemm_waves<MmaBf16, Epi::kBf16>(b, g, s, after_gemm);
+      return launch_gemm_waves<MmaBf16, Epi::kBf16>(b, g, s, ev);
     case Epi::kSwiglu:
-      return launch_gemm_waves<MmaBf16, Epi::kSwiglu>(b, g, s, after_gemm);
+      return launch_gemm_waves<MmaBf16, Epi::kSwiglu>(b, g, s, ev);
     default: return hipErrorInvalidValue;
   }
 }
 
 hipError_t
 launch_gemm_i8(const GemmBatch& b, Epi epi, const GemmShape& g, hipStream_t s,
-               hipEvent_t after_gemm)
+               const GemmEvents& ev)
 {
   switch (epi) {
     case Epi::kI32:
-      return launch_gemm_waves<MmaI8, Epi::kI32>(b, g, s, after_gemm);
+      return launch_gemm_waves<MmaI8, Epi::kI32>(b, g, s, ev);
     case Epi::kDequantBf16:
-      return launch_gemm_waves<MmaI8, Epi::kDequantBf16>(b, g, s, after_gemm);
+      return launch_gemm_waves<MmaI8, Epi::kDequantBf16>(b, g, s, ev);
     default: return hipErrorInvalidValue;
   }
 }
