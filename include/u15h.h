@@ -29,7 +29,12 @@
  *
  * Ordering: every call enqueues on the caller's hipStream_t and returns
  * without synchronising.  A context is not thread-safe: use one per host
- * thread, or serialise.
+ * thread, or serialise.  A context owns scratch memory that its GEMM calls
+ * write and read on the device (the split-K partial sums, the int8 route's
+ * codes and scales, the dequant expansion), so ALL calls on one context
+ * must be ordered on ONE stream (or otherwise ordered by the caller, e.g.
+ * with events): two calls on one context queued on unordered streams race
+ * on that scratch.  Use one context per stream for concurrent work.
  *
  * Errors: every call returns a u15h_status.  On any non-OK status from a
  * shape / argument check NOTHING has been launched (the reference's
@@ -138,8 +143,11 @@ u15h_status u15h_dequant_affine(u15h_ctx* ctx, u15h_stream stream,
                                 u15h_bf16* w_out);
 
 /* Replaces MetalOps::linear(enc, x, QWeight, bias, y, M, K, N) for a
- * quantized pack (src/u15-metal-ops.cc:402-433): dequant once into the
- * context's grow-only scratch, then the dense path (u15h_linear). */
+ * quantized pack (src/u15-metal-ops.cc:359-433): dequant once into the
+ * context's grow-only scratch, then u15h_linear's route on the expansion
+ * -- including its int8 interception when the tier is on and the shape
+ * qualifies (the reference's linear_mma_q_ re-enters linear_mma_,
+ * src/u15-metal-ops.cc:291-300, 393-399). */
 u15h_status u15h_linear_q(u15h_ctx* ctx, u15h_stream stream,
                           const u15h_bf16* x, const u15h_qweight* w,
                           const u15h_bf16* bias, u15h_bf16* y,
@@ -389,6 +397,120 @@ u15h_status u15h_mot_gemm_i8(u15h_ctx* ctx, u15h_stream stream,
                              int nproj);
 
 /* ------------------------------------------------------------------ */
+/* The resident MoT layer stack                                        */
+/* ------------------------------------------------------------------ */
+
+/* The seven projections of an expert layer, in the order
+ * U15Backbone::layer_step_ issues them (src/u15-backbone.cc:197-254), and
+ * the two experts of a MotLayer (src/u15-weights.h:113-116). */
+typedef enum {
+  U15H_PROJ_Q = 0, U15H_PROJ_K = 1, U15H_PROJ_V = 2, U15H_PROJ_O = 3,
+  U15H_PROJ_GATE = 4, U15H_PROJ_UP = 5, U15H_PROJ_DOWN = 6, U15H_NPROJ = 7
+} u15h_proj_id;
+typedef enum { U15H_UND = 0, U15H_GEN = 1 } u15h_expert;
+
+/* A host-side table of device pointers: n_layers MotLayers, each with the
+ * seven projection matrices of both experts (the reference's
+ * MotLayer{und, gen} of ExpertLayer, src/u15-weights.h:97-117), bf16
+ * [N][K] and optionally their int8-tier copies (per-output-channel codes
+ * [N][K] + f32 scales [N], as u15h_quant_rows_i8 makes them).  The
+ * caller owns the weight memory and keeps it resident; the stack holds
+ * pointers only.  Shapes follow LlmConfig (src/u15-config.h:40-63):
+ * q [heads*head_dim][hidden], k/v [kv_heads*head_dim][hidden],
+ * o [hidden][heads*head_dim], gate/up [inter][hidden], down [hidden][inter]. */
+typedef struct u15h_stack u15h_stack;
+
+u15h_status u15h_stack_create(int n_layers, int hidden, int heads,
+                              int kv_heads, int head_dim, int inter,
+                              u15h_stack** out);
+void        u15h_stack_destroy(u15h_stack* st);
+
+/* Maps one of the reference's tensor names to its slot, by the rule of
+ * U15Weights' layer binder (src/u15-weights.cc:539-578):
+ *   language_model.model.layers.<i>.self_attn.{q,k,v,o}_proj[_mot_gen]
+ *   language_model.model.layers.<i>.mlp[_mot_gen].{gate,up,down}_proj
+ * each optionally followed by ".weight".  The attention matrices suffix
+ * the TENSOR (q_proj_mot_gen), the MLP suffixes the MODULE
+ * (mlp_mot_gen.gate_proj).  Host only.  EINVAL for any other name (norms,
+ * embeddings, a malformed layer index). */
+u15h_status u15h_weight_slot(const char* name, int* layer, int* expert,
+                             int* proj);
+
+/* Binds a bf16 matrix [N][K] (device memory, 16-byte aligned) to the slot
+ * a reference tensor name maps to.  EINVAL for an unknown name or a layer
+ * index outside the stack. */
+u15h_status u15h_stack_bind(u15h_stack* st, const char* name,
+                            const u15h_bf16* w);
+/* Binds the int8-tier copy of a slot: wq [N][K] int8, sw [N] f32. */
+u15h_status u15h_stack_bind_i8(u15h_stack* st, const char* name,
+                               const int8_t* wq, const float* sw);
+/* The same two bindings by index (either pointer group may be NULL to
+ * leave it unchanged). */
+u15h_status u15h_stack_set(u15h_stack* st, int layer, int expert, int proj,
+                           const u15h_bf16* w, const int8_t* wq,
+                           const float* sw);
+
+/* The matrices a pass needs are bound (the projection half of
+ * ExpertLayer::complete, src/u15-weights.cc:333-339): every layer's seven
+ * matrices of the und expert (need_und) and/or the gen expert (need_gen),
+ * bf16 (tier 0) or int8 (tier 1).  On EINVAL, `missing` (if not NULL)
+ * receives the reference name of the first unbound matrix. */
+u15h_status u15h_stack_check(const u15h_stack* st, int need_und,
+                             int need_gen, int tier, char* missing,
+                             size_t missing_cap);
+
+/* The activations of one layer's projections: the reference's layer
+ * scratch (_normed, _q, _k, _v, _attn_t, _gate, _up, _ff, _proj;
+ * src/u15-backbone.cc:197-254), rows [0, M_und) und, then M_gen gen. */
+typedef struct {
+  const u15h_bf16* x;     /* [M][hidden]          q|k|v input            */
+  u15h_bf16*       q;     /* [M][heads*head_dim]                         */
+  u15h_bf16*       k;     /* [M][kv_heads*head_dim]                      */
+  u15h_bf16*       v;     /* [M][kv_heads*head_dim]                      */
+  const u15h_bf16* attn;  /* [M][heads*head_dim]  o input                */
+  u15h_bf16*       o;     /* [M][hidden]                                 */
+  const u15h_bf16* x2;    /* [M][hidden]          gate|up input          */
+  u15h_bf16*       gate;  /* [M][inter] (unused with U15H_FUSED_SWIGLU)  */
+  u15h_bf16*       up;    /* [M][inter] (unused with U15H_FUSED_SWIGLU)  */
+  u15h_bf16*       h;     /* [M][inter] down input; written by the fused
+                             gate|up step                                */
+  u15h_bf16*       down;  /* [M][hidden]                                 */
+  int8_t*          xq;    /* int8 tier: [M][max(hidden, heads*head_dim,
+                             inter)] activation codes (caller scratch)   */
+  float*           sx;    /* int8 tier: [M] per-token scales            */
+} u15h_layer_io;
+
+/* Steps of a layer (bit mask) and options. */
+#define U15H_STEP_QKV      1   /* q|k|v = x . {Wq|Wk|Wv}^T, one launch  */
+#define U15H_STEP_O        2   /* o = attn . Wo^T                        */
+#define U15H_STEP_GATE_UP  4   /* gate|up = x2 . {Wg|Wu}^T, one launch   */
+#define U15H_STEP_DOWN     8   /* down = h . Wd^T                        */
+#define U15H_STEP_ALL     15
+#define U15H_TIER_BF16     0
+#define U15H_TIER_I8       1   /* per-token quantisation of each step's
+                                  input into xq/sx, then the int8 GEMM
+                                  with the fused dequant                 */
+#define U15H_FUSED_SWIGLU  1   /* flag: the gate|up step writes h =
+                                  silu(gate) * up (fused epilogue; bf16
+                                  tier) instead of gate and up           */
+
+/* One layer's projection steps, both experts per launch: the projection
+ * half of U15Backbone::layer_step_ (src/u15-backbone.cc:174-257), whose
+ * norms, attention and residual adds stay with the caller between the
+ * steps.  Each step is one grouped launch over both weight sets. */
+u15h_status u15h_stack_layer(u15h_ctx* ctx, u15h_stream stream,
+                             const u15h_stack* st, int layer,
+                             const u15h_layer_io* io, int M_und, int M_gen,
+                             int steps, int tier, int flags);
+
+/* Every layer's projection steps in order, layer after layer, on the
+ * same io buffers: forward_many's layer loop (src/u15-backbone.cc:
+ * 386-426) with the non-projection ops of layer_step_ left out. */
+u15h_status u15h_stack_forward(u15h_ctx* ctx, u15h_stream stream,
+                               const u15h_stack* st, const u15h_layer_io* io,
+                               int M_und, int M_gen, int tier, int flags);
+
+/* ------------------------------------------------------------------ */
 /* profiling                                                           */
 /* ------------------------------------------------------------------ */
 
@@ -399,6 +521,12 @@ u15h_status u15h_mot_gemm_i8(u15h_ctx* ctx, u15h_stream stream,
  * reduction kernel, then forgets it -- so a caller brackets the GEMM
  * kernel alone between its own event and this one.  NULL cancels. */
 u15h_status u15h_profile_next_gemm(u15h_ctx* ctx, void* event);
+/* The same with a second event recorded right BEFORE the next GEMM kernel
+ * (after any quantisation the same call launches first), so the pair
+ * brackets exactly that kernel.  Either may be NULL.  No reference
+ * counterpart. */
+u15h_status u15h_profile_bracket_next_gemm(u15h_ctx* ctx, void* before,
+                                           void* after);
 
 /* ------------------------------------------------------------------ */
 /* per-token routing                                                   */

@@ -91,3 +91,81 @@ def test_qweight_geometry_rule():
                       (4096, 128, 768)):
         with pytest.raises(u15h.U15hError):
             u15h.qweight_geometry(K, sc, cc)
+
+
+# ---- the resident layer stack: host logic ---------------------------------
+
+def test_weight_slot_reference_names():
+    """Literal names from the reference's own tests and docs: the attention
+    suffixes the tensor, the MLP the module (src/u15-weights.cc:539-578;
+    tests/u15-weights-test.cc:200, tests/u15-config-test.cc:98;
+    ARCHITECTURE.md:77-78)."""
+    ws = u15h.weight_slot
+    assert ws("language_model.model.layers.0.self_attn.q_proj_mot_gen.weight") == (0, u15h.GEN, 0)
+    assert ws("language_model.model.layers.0.mlp_mot_gen.gate_proj.weight") == (0, u15h.GEN, 4)
+    assert ws("language_model.model.layers.41.mlp.down_proj.weight") == (41, u15h.UND, 6)
+    assert ws("language_model.model.layers.7.self_attn.o_proj") == (7, u15h.UND, 3)
+    assert ws("language_model.model.layers.12.self_attn.v_proj_mot_gen") == (12, u15h.GEN, 2)
+    assert ws("language_model.model.layers.5.mlp.up_proj") == (5, u15h.UND, 5)
+
+
+@pytest.mark.parametrize("bad", [
+    "language_model.model.layers.03.self_attn.q_proj",          # leading zero
+    "language_model.model.layers.-1.self_attn.q_proj",
+    "language_model.model.layers..mlp.up_proj",
+    "language_model.model.layers.3.self_attn.q_norm.weight",    # a norm
+    "language_model.model.layers.3.self_attn.q_norm_hw_mot_gen.weight",
+    "language_model.model.layers.3.input_layernorm.weight",
+    "language_model.model.layers.3.mlp.gate_proj_mot_gen",      # wrong suffix place
+    "language_model.model.layers.3.self_attn_mot_gen.q_proj",   # wrong suffix place
+    "language_model.model.layers.3.self_attn.q_proj.weightx",
+    "language_model.model.layers.3.self_attn.q_proj.bias",
+    "language_model.model.norm_mot_gen.weight",
+    "model.layers.3.mlp.up_proj.weight",
+    "language_model.model.layers.1234567890.mlp.up_proj",
+    "",
+])
+def test_weight_slot_refuses_other_names(bad):
+    with pytest.raises(u15h.U15hError):
+        u15h.weight_slot(bad)
+
+
+def test_weight_slot_round_trip_over_the_stack():
+    for layer in (0, 1, 9, 10, 41):
+        for e in (u15h.UND, u15h.GEN):
+            for p in range(7):
+                assert u15h.weight_slot(u15h.slot_name(layer, e, p)) == (layer, e, p)
+
+
+def test_stack_check_names_the_first_missing_matrix():
+    st = u15h.Stack(3)
+    assert st.check() == "language_model.model.layers.0.self_attn.q_proj.weight"
+    assert st.check(need_und=False) == \
+        "language_model.model.layers.0.self_attn.q_proj_mot_gen.weight"
+    assert st.check(tier=u15h.TIER_I8).endswith("(int8)")
+    assert st.check(need_und=False, need_gen=False) is None   # nothing needed
+    st.close()
+
+
+def test_stack_refusals_without_a_device():
+    lib = u15h.load_library()
+    h = ctypes.c_void_p()
+    # shapes: heads must be a multiple of kv_heads, widths multiples of 8
+    assert lib.u15h_stack_create(2, 4096, 32, 5, 128, 12288, ctypes.byref(h)) == u15h.EINVAL
+    assert lib.u15h_stack_create(2, 4100, 32, 8, 128, 12288, ctypes.byref(h)) == u15h.EINVAL
+    assert lib.u15h_stack_create(0, 4096, 32, 8, 128, 12288, ctypes.byref(h)) == u15h.EINVAL
+    assert lib.u15h_stack_create(2, 4096, 32, 8, 128, 12288, ctypes.byref(h)) == u15h.OK
+    # by index: layer, expert and projection ranges; a half-given int8 pair
+    assert lib.u15h_stack_set(h, 2, 0, 0, None, None, None) == u15h.EINVAL
+    assert lib.u15h_stack_set(h, 0, 2, 0, None, None, None) == u15h.EINVAL
+    assert lib.u15h_stack_set(h, 0, 0, 7, None, None, None) == u15h.EINVAL
+    assert lib.u15h_stack_set(h, 0, 0, 0, None, ctypes.c_void_p(256), None) == u15h.EINVAL
+    assert lib.u15h_stack_set(h, 0, 0, 0, ctypes.c_void_p(8), None, None) == u15h.EINVAL
+    # a name whose layer lies outside the stack
+    assert lib.u15h_stack_bind(h, b"language_model.model.layers.2.mlp.up_proj",
+                               ctypes.c_void_p(256)) == u15h.EINVAL
+    # calls need a context
+    io = u15h.layer_io()
+    assert lib.u15h_stack_layer(None, None, h, 0, ctypes.byref(io), 0, 1, 15, 0, 0) == u15h.EINVAL
+    assert lib.u15h_stack_forward(None, None, h, ctypes.byref(io), 0, 1, 0, 0) == u15h.EINVAL
+    lib.u15h_stack_destroy(h)

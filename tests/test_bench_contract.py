@@ -78,3 +78,83 @@ def test_more_than_one_gpu_is_refused():
     assert p.returncode == 2
     assert "one GPU only" in p.stderr
     assert p.stdout == ""
+
+
+# ---- per-launch arithmetic of a step (both tiers) ---------------------------
+
+@pytest.mark.parametrize("layers", [1, 42])
+def test_step_work_per_launch(layers):
+    """FLOP and algorithmic bytes per GEMM launch do not depend on how many
+    layers a step holds, and the int8 figures count int8 operands."""
+    w = bench.step_work(128, 4096, layers)
+    M = 4224
+    assert w["gemm_launches"] == 4 * layers and w["quant_launches"] == 4 * layers
+    assert w["flop"] / w["gemm_launches"] == bench.FLOP_PER_ROW * M / 4
+    # bf16: both weight sets, inputs and outputs, 2 bytes each
+    assert w["bf16_bytes"] / w["gemm_launches"] == _layer_bytes(128, 4096) / 4
+    # int8: int8 weights (half the bf16 bytes) + f32 channel scales of both
+    # sets, int8 inputs + one f32 scale per row per launch, bf16 outputs
+    H, I, NQ, NKV = bench.HIDDEN, bench.INTER, bench.NQ, bench.NKV
+    cols = NQ + 2 * NKV + H + 2 * I + H
+    i8_layer = (2 * bench.FLOP_PER_ROW // 2 + 4 * 2 * cols
+                + M * (H + NQ + H + I) + 16 * M + 2 * M * cols)
+    assert w["i8_bytes"] / w["gemm_launches"] == i8_layer / 4
+    assert 204e6 < w["i8_bytes"] / w["gemm_launches"] < 206e6
+    # the quantiser reads bf16 and writes int8 + a scale per row
+    assert w["quant_bytes"] / w["quant_launches"] == \
+        (3 * M * (H + NQ + H + I) + 16 * M) / 4
+
+
+def test_tier_result_divides_by_launches():
+    """The int8 roofline uses the measured launch count: a 42-layer step's
+    per-launch figures equal a 1-layer step's at the same kernel speed."""
+    outs = []
+    for layers in (1, 42):
+        w = bench.step_work(128, 4096, layers)
+        steps = 3
+        k = {"gemm_ms": 0.17 * w["gemm_launches"] * steps,
+             "pre_ms": 0.02 * w["quant_launches"] * steps,
+             "post_ms": 0.05 * layers * steps, "calls": w["gemm_launches"] * steps}
+        outs.append(bench.tier_result(w, 0.8 * layers, k, steps, True, None))
+    a, b = outs
+    for key in ("achieved", "frac", "avg_launch_ms", "alg_bytes_per_launch",
+                "achieved_GBps", "split_reduce_ms_per_step"):
+        if key == "split_reduce_ms_per_step":
+            assert b["roofline"][key] == pytest.approx(42 * a["roofline"][key])
+        else:
+            assert b["roofline"][key] == pytest.approx(a["roofline"][key])
+    assert a["roofline"]["frac"] < 1.0
+    assert a["quant_kernel"]["achieved_GBps"] == b["quant_kernel"]["achieved_GBps"]
+    assert a["value"] == b["value"]
+
+
+def test_kernel_label_follows_the_knobs(monkeypatch):
+    for k in ("U15H_WAVES", "U15H_MFMA16"):
+        monkeypatch.delenv(k, raising=False)
+    assert bench.kernel_label(False) == "mot_gemm_kernel<MmaBf16x16, kBf16, 4>"
+    assert bench.kernel_label(True) == "mot_gemm_kernel<MmaI8x16, kDequantBf16, 4>"
+    monkeypatch.setenv("U15H_WAVES", "4")
+    assert bench.kernel_label(False) == "mot_gemm_kernel<MmaBf16x16, kBf16, 2>"
+    monkeypatch.setenv("U15H_WAVES", "8")
+    monkeypatch.setenv("U15H_MFMA16", "0")
+    assert bench.kernel_label(False) == "mot_gemm_kernel<MmaBf16, kBf16, 4>"
+    assert bench.kernel_label(True) == "mot_gemm_kernel<MmaI8, kDequantBf16, 4>"
+    monkeypatch.setenv("U15H_MFMA16", "-1")
+    assert bench.kernel_label(False) == "mot_gemm_kernel<MmaBf16, kBf16, 4>"
+    assert bench.kernel_label(True) == "mot_gemm_kernel<MmaI8x16, kDequantBf16, 4>"
+
+
+def test_small_m_rotates_past_the_cache():
+    """Below the ridge a pass cycles more than twice the 256 MB Infinity
+    Cache of weights; above it one layer is the step."""
+    assert bench.rotation_layers(128, 4096) == 1
+    assert bench.rotation_layers(4352, 12288) == 1
+    for mu, mg in ((128, 0), (0, 128), (64, 192), (1, 0)):
+        n = bench.rotation_layers(mu, mg)
+        sets = (mu > 0) + (mg > 0)
+        assert n * sets * bench.LAYER_WEIGHT_BYTES >= 2 * bench.MALL_BYTES
+        assert (n - 1) * sets * bench.LAYER_WEIGHT_BYTES < 2 * bench.MALL_BYTES
+    a = bench.parse(["--m-und", "128", "--m-gen", "0"])
+    assert a.layers == 2
+    assert bench.parse([]).layers == 1
+    assert bench.parse(["--workload", "c5"]).layers == 42

@@ -64,6 +64,54 @@ def test_quant_rows_every_tie(ops):
                           np.tile(want.astype(np.int8), (3, 1)))
 
 
+def test_quant_rows_tiny_absmax(ops):
+    """Rows whose scale is subnormal, including rows whose 1/s overflows
+    to +inf (absmax below ~3.7e-37), down to the smallest bf16 subnormal:
+    codes and scales bit-exact against the oracle's division."""
+    rng = np.random.default_rng(21)
+    K = 4096
+    rows = []
+    for amax in (1e-36, 5e-37, 3.7e-37, 1e-37, 1e-38, 2.0 ** -126, 2.0 ** -130):
+        r = rng.uniform(-amax, amax, K).astype(np.float32)
+        r[int(rng.integers(K))] = -amax
+        rows.append(r)
+    sub = np.zeros(K, np.float32)
+    sub[::7] = np.float32(2.0 ** -133)              # smallest bf16 subnormal
+    sub[3::7] = -np.float32(2.0 ** -133)
+    rows.append(sub)
+    tie = np.zeros(K, np.float32)                   # exact ties at a tiny scale
+    tie[0] = 127.0 * 2.0 ** -120
+    tie[1:254] = np.arange(-126.5, 127.0, 1.0) * 2.0 ** -120
+    rows.append(tie)
+    xb = oracle.f32_to_bf16(np.stack(rows))
+    q, s = quant_gpu(ops, xb)
+    qo, so = oracle.quant_rows_i8(xb)
+    with np.errstate(divide="ignore", over="ignore"):
+        assert not np.all(np.isfinite(np.float32(1.0) / so))     # the case is present
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
+    assert np.array_equal(q.cpu().numpy(), qo)
+
+
+def test_quant_rows_codes_stay_in_range(ops):
+    """A NaN element (no oracle value) still gives a code in [-127, 127]:
+    the redo test selects the division for it, and the row's other codes
+    are the oracle's for the same row with the NaN set to zero."""
+    rng = np.random.default_rng(22)
+    x = rng.standard_normal((2, 512)).astype(np.float32)
+    x[0, 5] = np.nan
+    xb = oracle.f32_to_bf16(x)
+    q, _ = quant_gpu(ops, xb)
+    qh = q.cpu().numpy()
+    assert qh.min() >= -127 and qh.max() <= 127
+    clean = x.copy()
+    clean[0, 5] = 0.0
+    qo, _ = oracle.quant_rows_i8(oracle.f32_to_bf16(clean))
+    keep = np.ones(512, bool)
+    keep[5] = False
+    assert np.array_equal(qh[0, keep], qo[0, keep])
+    assert np.array_equal(qh[1], qo[1])
+
+
 @pytest.mark.parametrize("K", [8, 136, 12288])
 def test_quant_rows_other_widths(ops, K):
     rng = np.random.default_rng(K)
@@ -213,6 +261,61 @@ def test_linear_int8_route_on_and_decline(ops):
         assert not torch.equal(y_i8.cpu(), y_bf16.cpu())
         assert torch.equal(small.cpu(), y_bf16[:8].cpu())   # declined
         assert rel_l2(host_f32(y_i8), host_f32(y_bf16)) < 0.03
+    finally:
+        ops.enable_i8_gemm(False)
+        ops.release_i8_scratch()
+
+
+def test_linear_q_int8_interception(ops):
+    """u15h_linear_q with the tier ON: the dequant-once expansion takes
+    u15h_linear's route, so at M >= the row floor the result equals
+    quantise(x) + quantise(expansion) + int8 GEMM + dequant bit for bit
+    (the reference's linear_mma_q_ re-enters linear_mma_'s interception,
+    src/u15-metal-ops.cc:291-300, 393-399); below the floor it is the dense
+    bf16 result on the expansion."""
+    import os
+    rng = np.random.default_rng(27)
+    K, N, G = 1024, 264, 64
+    Mbig = max(ops.i8_min_m(), 1024)
+    w = oracle.randn_mt(91, N * K, 0.05).reshape(N, K)
+    codes, sc, bi, _ = oracle.pack_affine(w, 8, G)
+    wd = oracle.dequant_affine(codes, sc, bi, 8, G, K)
+    qw = (torch.from_numpy(codes.view(np.int32)).cuda(), dev_bf16(sc), dev_bf16(bi), 8, G)
+    xb = rand_bf16_bits(rng, (Mbig, K))
+    x, wd_dev = dev_bf16(xb), dev_bf16(wd)
+    y_dense = torch.empty(Mbig, N, dtype=torch.bfloat16, device="cuda")
+    ops.enable_i8_gemm(False)
+    ops.linear_q(x, qw, None, y_dense, Mbig, K, N)
+    try:
+        on = ops.enable_i8_gemm(True)
+        if os.environ.get("U15H_I8_GEMM", "") == "0":
+            assert not on
+            return
+        assert on
+        y_q = torch.empty_like(y_dense)
+        ops.linear_q(x, qw, None, y_q, Mbig, K, N)
+        small = torch.empty(8, N, dtype=torch.bfloat16, device="cuda")
+        ops.linear_q(x[:8], qw, None, small, 8, K, N)
+        torch.cuda.synchronize()
+        xq, sx = quant_gpu(ops, xb)
+        wq, sw = quant_gpu(ops, wd)
+        y_ref = torch.empty_like(y_dense)
+        ops.mot_gemm_i8(xq, sx, 0, Mbig, K, [_proj(None, None, wq, sw, y_ref)])
+        y_lin = torch.empty_like(y_dense)
+        ops.linear(x, wd_dev, None, y_lin, Mbig, K, N)     # the same route
+        torch.cuda.synchronize()
+        assert torch.equal(y_q.cpu(), y_ref.cpu())
+        assert torch.equal(y_q.cpu(), y_lin.cpu())
+        assert not torch.equal(y_q.cpu(), y_dense.cpu())
+        assert torch.equal(small.cpu(), y_dense[:8].cpu())   # declined: dense
+        # the int32 accumulators behind it are the oracle's, exactly
+        qo, so = oracle.quant_rows_i8(wd)
+        assert np.array_equal(wq.cpu().numpy(), qo)
+        rows = np.array([0, 511, Mbig - 1], np.int32)
+        xq_h = xq.cpu().numpy()
+        acc = oracle.gemm_i8_i32(xq_h, qo, row_ids=rows)
+        exp = oracle.dequant_bf16(acc, sx.cpu().numpy()[rows], so)
+        assert np.array_equal(host_bits(y_q)[rows], exp)
     finally:
         ops.enable_i8_gemm(False)
         ops.release_i8_scratch()

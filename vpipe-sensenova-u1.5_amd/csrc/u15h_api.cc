@@ -25,7 +25,9 @@ struct u15h_ctx {
   // GEMM kernel build: 8 or 4 waves per workgroup (env U15H_WAVES) and the
   // 8-wave build's MFMA shape (env U15H_MFMA16).
   u15h::GemmShape gemm = {8, 0, 1};
-  // One-shot profiling event: recorded after the next GEMM kernel.
+  // One-shot profiling events: recorded right before and right after the
+  // next GEMM kernel.
+  hipEvent_t profile_before = nullptr;
   hipEvent_t profile_event = nullptr;
   // Partial-sum workspace of split tiles: at most num_cu K shares of one
   // 256x256 tile each (allocated on first use, kept until destroy).
@@ -83,11 +85,12 @@ bind_device(u15h_ctx* ctx)
   return U15H_OK;
 }
 
-// The profiling event of the next GEMM launch (one-shot).
-hipEvent_t
+// The profiling events of the next GEMM launch (one-shot).
+u15h::GemmEvents
 take_profile_event(u15h_ctx* ctx)
 {
-  hipEvent_t e = ctx->profile_event;
+  const u15h::GemmEvents e = {ctx->profile_before, ctx->profile_event};
+  ctx->profile_before = nullptr;
   ctx->profile_event = nullptr;
   return e;
 }
@@ -290,6 +293,12 @@ linear_i8_route(u15h_ctx* ctx, hipStream_t s, const u15h_bf16* x,
 }
 
 }  // namespace
+
+u15h_status
+u15h::set_error(u15h_ctx* ctx, u15h_status st, const char* msg)
+{
+  return fail(ctx, st, "%s", msg);
+}
 
 extern "C" {
 
@@ -558,8 +567,15 @@ u15h_release_i8_scratch(u15h_ctx* ctx)
 u15h_status
 u15h_profile_next_gemm(u15h_ctx* ctx, void* event)
 {
+  return u15h_profile_bracket_next_gemm(ctx, nullptr, event);
+}
+
+u15h_status
+u15h_profile_bracket_next_gemm(u15h_ctx* ctx, void* before, void* after)
+{
   if (ctx == nullptr) { return U15H_EINVAL; }
-  ctx->profile_event = static_cast<hipEvent_t>(event);
+  ctx->profile_before = static_cast<hipEvent_t>(before);
+  ctx->profile_event = static_cast<hipEvent_t>(after);
   return U15H_OK;
 }
 
@@ -756,10 +772,15 @@ u15h_linear_q(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
   if ((st = u15h_dequant_affine(ctx, stream, w, N, K, wd)) != U15H_OK) {
     return st;
   }
-  // From here it is the dense bf16 path, never the int8 tier: the
-  // reference re-enters linear_mma_'s matmul the same way
-  // (u15-metal-ops.cc:393-399).
-  return dense_bf16(ctx, as_stream(stream), x, wd, bias, y, M, K, N);
+  // From here the expansion is a dense weight and takes u15h_linear's
+  // route: the reference's linear_mma_q_ re-enters linear_mma_, whose
+  // first step is the int8 interception (u15-metal-ops.cc:291-300,
+  // 393-399: a quantized weight arrives there as the _w_deq expansion).
+  hipStream_t s = as_stream(stream);
+  if (ctx->i8_on && M >= ctx->i8_min_m && K % 128 == 0) {
+    return linear_i8_route(ctx, s, x, wd, bias, y, M, K, N);
+  }
+  return dense_bf16(ctx, s, x, wd, bias, y, M, K, N);
 }
 
 u15h_status

@@ -6,6 +6,8 @@
 #include <hip/hip_runtime_api.h>
 #include <stdint.h>
 
+#include "u15h.h"
+
 namespace u15h {
 
 // Output tile of one workgroup and the K bytes staged per LDS stage.
@@ -83,12 +85,17 @@ struct GemmShape {
   int mfma16;
 };
 
-// `after_gemm`, when not null, is recorded on `s` right after the GEMM
-// kernel and before any split-K reduction kernel.
+// Profiling events of one GEMM launch: `before`, when not null, is
+// recorded on the launch stream right before the GEMM kernel, `after`
+// right after it and before any split-K reduction kernel.
+struct GemmEvents {
+  hipEvent_t before;
+  hipEvent_t after;
+};
 hipError_t launch_gemm_bf16(const GemmBatch& b, Epi epi, const GemmShape& g,
-                            hipStream_t s, hipEvent_t after_gemm);
+                            hipStream_t s, const GemmEvents& ev);
 hipError_t launch_gemm_i8(const GemmBatch& b, Epi epi, const GemmShape& g,
-                          hipStream_t s, hipEvent_t after_gemm);
+                          hipStream_t s, const GemmEvents& ev);
 hipError_t launch_quant_rows_i8(const uint16_t* x, int rows, int K,
                                 int8_t* q, float* sc, hipStream_t s);
 hipError_t launch_swiglu(const uint16_t* g, const uint16_t* u, uint16_t* o,
@@ -130,6 +137,10 @@ hipError_t launch_gather_rows(const uint16_t* src, const int32_t* perm,
                               hipStream_t s);
 // Forces every kernel's code object to load; false if any cannot.
 bool kernels_loadable();
+
+// Sets the context's last-error text (u15h_last_error) and returns `st`;
+// for host code of the library outside u15h_api.cc.
+u15h_status set_error(u15h_ctx* ctx, u15h_status st, const char* msg);
 
 // Tile columns per tile for an epilogue (kSwiglu tiles produce half).
 constexpr int tile_cols(Epi e) { return e == Epi::kSwiglu ? kBN / 2 : kBN; }

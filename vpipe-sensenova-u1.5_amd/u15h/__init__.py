@@ -52,6 +52,12 @@ class _MotProjI8(ctypes.Structure):
                 ("y", ctypes.c_void_p), ("N", ctypes.c_int)]
 
 
+class _LayerIO(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in
+                ("x", "q", "k", "v", "attn", "o", "x2", "gate", "up", "h",
+                 "down", "xq", "sx")]
+
+
 class _QWeight(ctypes.Structure):
     _fields_ = [("codes", ctypes.c_void_p), ("scales", ctypes.c_void_p),
                 ("biases", ctypes.c_void_p), ("bits", ctypes.c_int),
@@ -90,6 +96,7 @@ def load_library() -> ctypes.CDLL:
         "u15h_release_i8_scratch": (None, [vp]),
         "u15h_i8_min_m": (i, [vp]),
         "u15h_profile_next_gemm": (i, [vp, vp]),
+        "u15h_profile_bracket_next_gemm": (i, [vp, vp, vp]),
         "u15h_quant_rows_i8": (i, [vp, vp, vp, i, i, vp, vp]),
         "u15h_mot_gemm_i8_i32": (i, [vp, vp, vp, i, i, i,
                                      ctypes.POINTER(_MotProjI8), i]),
@@ -125,6 +132,18 @@ def load_library() -> ctypes.CDLL:
         "u15h_transpose_thd": (i, [vp, vp, vp, vp, i, i, i]),
         "u15h_transpose_htd": (i, [vp, vp, vp, vp, i, i, i]),
         "u15h_transpose_into_cache": (i, [vp, vp, vp, vp, i, i, i, i, i]),
+        "u15h_stack_create": (i, [i, i, i, i, i, i, ctypes.POINTER(vp)]),
+        "u15h_stack_destroy": (None, [vp]),
+        "u15h_weight_slot": (i, [ctypes.c_char_p, ctypes.POINTER(i),
+                                 ctypes.POINTER(i), ctypes.POINTER(i)]),
+        "u15h_stack_bind": (i, [vp, ctypes.c_char_p, vp]),
+        "u15h_stack_bind_i8": (i, [vp, ctypes.c_char_p, vp, vp]),
+        "u15h_stack_set": (i, [vp, i, i, i, vp, vp, vp]),
+        "u15h_stack_check": (i, [vp, i, i, i, ctypes.c_char_p, ctypes.c_size_t]),
+        "u15h_stack_layer": (i, [vp, vp, vp, i, ctypes.POINTER(_LayerIO), i,
+                                 i, i, i, i]),
+        "u15h_stack_forward": (i, [vp, vp, vp, ctypes.POINTER(_LayerIO), i,
+                                   i, i, i]),
         "u15h_gather_rows": (i, [vp, vp, vp, vp, i, i, vp]),
         "u15h_scatter_rows": (i, [vp, vp, vp, vp, i, i, vp]),
     }
@@ -153,6 +172,110 @@ def route_rows(expert) -> tuple[list[int], int, int]:
     if st != OK:
         raise U15hError(st, "u15h_route_rows: invalid expert ids")
     return perm[:M], mu.value, mg.value
+
+
+PROJ_NAMES = ("q", "k", "v", "o", "gate", "up", "down")
+UND, GEN = 0, 1
+STEP_QKV, STEP_O, STEP_GATE_UP, STEP_DOWN, STEP_ALL = 1, 2, 4, 8, 15
+TIER_BF16, TIER_I8 = 0, 1
+FUSED_SWIGLU = 1
+
+
+def weight_slot(name: str) -> tuple[int, int, int]:
+    """(layer, expert, projection index) of a reference tensor name, by the
+    layer binder's rule (src/u15-weights.cc:539-578); U15hError otherwise."""
+    lib = load_library()
+    l, e, p = ctypes.c_int(0), ctypes.c_int(0), ctypes.c_int(0)
+    st = lib.u15h_weight_slot(name.encode(), ctypes.byref(l), ctypes.byref(e),
+                              ctypes.byref(p))
+    if st != OK:
+        raise U15hError(st, f"not a projection matrix name: {name!r}")
+    return l.value, e.value, p.value
+
+
+def slot_name(layer: int, expert: int, proj: int) -> str:
+    """The reference's tensor name of a slot (the inverse of weight_slot)."""
+    pre = f"language_model.model.layers.{layer}."
+    sfx = "_mot_gen" if expert == GEN else ""
+    n = PROJ_NAMES[proj]
+    if proj <= 3:
+        return f"{pre}self_attn.{n}_proj{sfx}.weight"
+    return f"{pre}mlp{sfx}.{n}_proj.weight"
+
+
+class Stack:
+    """u15h_stack: n_layers MotLayers of device-pointer bindings (the
+    reference's MotLayer{und, gen}, src/u15-weights.h:97-117).  Holds a
+    reference to every bound tensor so the memory stays alive."""
+
+    def __init__(self, n_layers, hidden=4096, heads=32, kv_heads=8,
+                 head_dim=128, inter=12288):
+        self._lib = load_library()
+        h = ctypes.c_void_p()
+        st = self._lib.u15h_stack_create(n_layers, hidden, heads, kv_heads,
+                                         head_dim, inter, ctypes.byref(h))
+        if st != OK:
+            raise U15hError(st, "u15h_stack_create: invalid shape")
+        self._h = h
+        self.n_layers = n_layers
+        self.hidden, self.qdim = hidden, heads * head_dim
+        self.kvdim, self.inter = kv_heads * head_dim, inter
+        self._keep = {}
+
+    def shape(self, proj):
+        """(N, K) of a projection."""
+        return {0: (self.qdim, self.hidden), 1: (self.kvdim, self.hidden),
+                2: (self.kvdim, self.hidden), 3: (self.hidden, self.qdim),
+                4: (self.inter, self.hidden), 5: (self.inter, self.hidden),
+                6: (self.hidden, self.inter)}[proj]
+
+    def bind(self, name, w):
+        l, e, p = weight_slot(name)
+        _need(w, torch.bfloat16, self.shape(p), name)
+        st = self._lib.u15h_stack_bind(self._h, name.encode(), _ptr(w))
+        if st != OK:
+            raise U15hError(st, f"u15h_stack_bind({name})")
+        self._keep[(l, e, p, "w")] = w
+
+    def bind_i8(self, name, wq, sw):
+        l, e, p = weight_slot(name)
+        N, K = self.shape(p)
+        _need(wq, torch.int8, (N, K), name)
+        _need(sw, torch.float32, (N,), name + " scales")
+        st = self._lib.u15h_stack_bind_i8(self._h, name.encode(), _ptr(wq),
+                                          _ptr(sw))
+        if st != OK:
+            raise U15hError(st, f"u15h_stack_bind_i8({name})")
+        self._keep[(l, e, p, "q")] = (wq, sw)
+
+    def check(self, need_und=True, need_gen=True, tier=TIER_BF16):
+        """None if the pass's matrices are bound, else the first missing
+        reference name."""
+        buf = ctypes.create_string_buffer(256)
+        st = self._lib.u15h_stack_check(self._h, int(need_und), int(need_gen),
+                                        tier, buf, 256)
+        return None if st == OK else buf.value.decode()
+
+    def close(self):
+        if getattr(self, "_h", None):
+            self._lib.u15h_stack_destroy(self._h)
+            self._h = None
+        self._keep = {}
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def layer_io(**bufs):
+    """A u15h_layer_io from torch tensors (missing entries are NULL)."""
+    io = _LayerIO()
+    for name, _ in _LayerIO._fields_:
+        t = bufs.get(name)
+        setattr(io, name, None if t is None else t.data_ptr())
+    return io
 
 
 def build_rope_tables(pos_t, pos_h, pos_w, head_dim, d_t, d_h,
@@ -505,6 +628,17 @@ class Ops:
         self._check(self._lib.u15h_profile_next_gemm(self._ctx, h),
                     "u15h_profile_next_gemm")
 
+    def profile_bracket_next_gemm(self, before, after):
+        """Record raw hipEvent_t handles right before and right after the
+        next GEMM kernel (either may be None)."""
+        def h(e):
+            if e is None or isinstance(e, ctypes.c_void_p):
+                return e
+            return ctypes.c_void_p(e)
+        self._check(self._lib.u15h_profile_bracket_next_gemm(self._ctx, h(before),
+                                                             h(after)),
+                    "u15h_profile_bracket_next_gemm")
+
     # ---- the step after the q/k projections -------------------------------
     def _head(self, x, heads, head_dim):
         tokens = x.shape[0]
@@ -621,6 +755,24 @@ class Ops:
         st = self._lib.u15h_scatter_rows(self._ctx, _stream(stream), _ptr(src),
                                          _ptr(perm), M, cols, _ptr(dst))
         self._check(st, "u15h_scatter_rows")
+
+    # ---- the resident layer stack -----------------------------------------
+    def stack_layer(self, stack, layer, io, M_und, M_gen, steps=STEP_ALL,
+                    tier=TIER_BF16, flags=0, stream=None):
+        """One layer's projection steps (u15h_stack_layer); `io` from
+        layer_io()."""
+        st = self._lib.u15h_stack_layer(self._ctx, _stream(stream), stack._h,
+                                        layer, ctypes.byref(io), M_und, M_gen,
+                                        steps, tier, flags)
+        self._check(st, "u15h_stack_layer")
+
+    def stack_forward(self, stack, io, M_und, M_gen, tier=TIER_BF16, flags=0,
+                      stream=None):
+        """Every layer's projection steps in order (u15h_stack_forward)."""
+        st = self._lib.u15h_stack_forward(self._ctx, _stream(stream), stack._h,
+                                          ctypes.byref(io), M_und, M_gen, tier,
+                                          flags)
+        self._check(st, "u15h_stack_forward")
 
     # ---- raw access for tests of argument checking ----------------------
     @property
