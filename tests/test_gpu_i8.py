@@ -81,7 +81,7 @@ def test_quant_rows_tiny_absmax(ops):
     rows.append(sub)
     tie = np.zeros(K, np.float32)                   # exact ties at a tiny scale
     tie[0] = 127.0 * 2.0 ** -120
-    tie[1:254] = np.arange(-126.5, 127.0, 1.0) * 2.0 ** -120
+    tie[1:255] = np.arange(-126.5, 127.0, 1.0) * 2.0 ** -120
     rows.append(tie)
     xb = oracle.f32_to_bf16(np.stack(rows))
     q, s = quant_gpu(ops, xb)
