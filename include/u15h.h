@@ -121,6 +121,25 @@ u15h_status u15h_mot_linear(u15h_ctx* ctx, u15h_stream stream,
                             const u15h_bf16* x, int M_und, int M_gen, int K,
                             const u15h_mot_proj* proj, int nproj);
 
+/* u15h_mot_linear without any device allocation.  No counterpart in the
+ * reference; it is for callers that cannot call hipMalloc: code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation.
+ * Same arguments, kernels and results (bit for bit) as u15h_mot_linear,
+ * but the split-K partial sums go to a static device array of the
+ * library (64 MiB per GPU, one 256x256 tile of 4-byte sums for each of up
+ * to 256 compute units; every GPU the library runs on holds it until the
+ * process ends) instead of the context's workspace.  Nothing in it needs
+ * clearing between calls.  EINVAL if a launch would need more partial sums
+ * than the array holds (a GPU with more than 256 CUs); ENODEV if the
+ * array's address could not be looked up at u15h_create.  All calls of
+ * this entry point on one GPU share the one array -- from any context and
+ * any stream -- so calls that can overlap on one GPU race: order them
+ * (one stream, or events). */
+u15h_status u15h_mot_linear_noalloc(u15h_ctx* ctx, u15h_stream stream,
+                                    const u15h_bf16* x, int M_und, int M_gen,
+                                    int K, const u15h_mot_proj* proj,
+                                    int nproj);
+
 /* Affine-quantized weight pack: the reference's QWeight
  * (src/u15-metal-ops.h:39-57; shape rules src/u15-weights.cc:248-325).
  *   codes  uint32 [N][K*bits/32], code k of a row at bits

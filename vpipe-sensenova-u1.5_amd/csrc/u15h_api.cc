@@ -32,6 +32,11 @@ struct u15h_ctx {
   // Partial-sum workspace of split tiles: at most num_cu K shares of one
   // 256x256 tile each (allocated on first use, kept until destroy).
   void* split_ws = nullptr;
+  // The device address of the static split-K scratch that
+  // u15h_mot_linear_noalloc uses instead (looked up at create; null if the
+  // lookup failed, with the HIP error kept for the message).
+  void* noalloc_ws = nullptr;
+  hipError_t noalloc_err = hipSuccess;
   bool i8_on = false;
   int i8_min_m = 1024;
   // Grow-only scratch of the int8 route of u15h_linear: activation and
@@ -154,9 +159,11 @@ split_ws_capacity(const u15h_ctx* ctx)
 // tiles on C compute units, the last T % C tiles would run as a last,
 // partial round that leaves most units idle; instead each is cut into
 // S = C / (T % C) shares of its K stages (so the shares fill about one
-// round), at least kMinStagesPerShare stages each.
+// round), at least kMinStagesPerShare stages each.  The partial sums go to
+// the context's workspace (allocated on first use), or with `noalloc` to
+// the static scratch, which allocates nothing.
 u15h_status
-plan_split(u15h_ctx* ctx, GemmBatch& b)
+plan_split(u15h_ctx* ctx, GemmBatch& b, bool noalloc = false)
 {
   b.split = 1;
   b.split_begin = b.total_tiles;
@@ -168,6 +175,21 @@ plan_split(u15h_ctx* ctx, GemmBatch& b)
   const int nk = (b.kbytes + u15h::kKB - 1) / u15h::kKB;
   const int S = std::min(C / rem, nk / kMinStagesPerShare);
   if (S < 2) { return U15H_OK; }
+  b.split = S;
+  b.split_begin = T - rem;
+  if (noalloc) {
+    if (ctx->noalloc_ws == nullptr) {
+      return fail(ctx, U15H_ENODEV, "static split-K scratch unavailable: %s",
+                  hipGetErrorString(ctx->noalloc_err));
+    }
+    if (split_ws_bytes(b) > u15h::kNoAllocScratchBytes) {
+      return fail(ctx, U15H_EINVAL, "split-K partial sums of %zu bytes exceed "
+                  "the static scratch of %zu bytes", split_ws_bytes(b),
+                  u15h::kNoAllocScratchBytes);
+    }
+    b.ws = ctx->noalloc_ws;
+    return U15H_OK;
+  }
   if (ctx->split_ws == nullptr) {
     if (hipMalloc(&ctx->split_ws, split_ws_capacity(ctx)) != hipSuccess) {
       ctx->split_ws = nullptr;
@@ -175,8 +197,6 @@ plan_split(u15h_ctx* ctx, GemmBatch& b)
                   split_ws_capacity(ctx));
     }
   }
-  b.split = S;
-  b.split_begin = T - rem;
   b.ws = ctx->split_ws;
   return split_ws_bytes(b) <= split_ws_capacity(ctx)
              ? U15H_OK
@@ -345,10 +365,17 @@ u15h_create(int device, u15h_ctx** out)
   // (the reference validates every function at init,
   // src/u15-metal-ops.cc:205-243).
   const bool ok = u15h::kernels_loadable();
+  // The static scratch's address on this device, looked up once per
+  // device while it is current.
+  void* noalloc_ws = nullptr;
+  const hipError_t noalloc_err = ok ? u15h::noalloc_scratch(device, &noalloc_ws)
+                                    : hipErrorNotReady;
   if (prev >= 0 && prev != device) { (void)hipSetDevice(prev); }
   if (!ok) { return U15H_ENODEV; }
   u15h_ctx* ctx = new u15h_ctx;
   ctx->device = device;
+  ctx->noalloc_ws = noalloc_ws;
+  ctx->noalloc_err = noalloc_err;
   ctx->num_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
   ctx->split_on = env_int("U15H_SPLIT", 1) != 0;
   ctx->gemm.waves = env_int("U15H_WAVES", 8) == 4 ? 4 : 8;
@@ -425,10 +452,10 @@ u15h_linear(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
   return dense_bf16(ctx, s, x, w, bias, y, M, K, N);
 }
 
-u15h_status
-u15h_mot_linear(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
+static u15h_status
+mot_linear_impl(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
                 int M_und, int M_gen, int K, const u15h_mot_proj* proj,
-                int nproj)
+                int nproj, bool noalloc)
 {
   if (ctx == nullptr) { return U15H_EINVAL; }
   u15h_status st = check_k(ctx, K, 2, 8);
@@ -475,9 +502,25 @@ u15h_mot_linear(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
                 M_und, p.N, p.N, tc);
   }
   if ((st = check_tiles(ctx, b)) != U15H_OK) { return st; }
-  if ((st = plan_split(ctx, b)) != U15H_OK) { return st; }
+  if ((st = plan_split(ctx, b, noalloc)) != U15H_OK) { return st; }
   return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kBf16, ctx->gemm, as_stream(stream), take_profile_event(ctx)),
                   "mot_gemm_bf16");
+}
+
+u15h_status
+u15h_mot_linear(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
+                int M_und, int M_gen, int K, const u15h_mot_proj* proj,
+                int nproj)
+{
+  return mot_linear_impl(ctx, stream, x, M_und, M_gen, K, proj, nproj, false);
+}
+
+u15h_status
+u15h_mot_linear_noalloc(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
+                        int M_und, int M_gen, int K, const u15h_mot_proj* proj,
+                        int nproj)
+{
+  return mot_linear_impl(ctx, stream, x, M_und, M_gen, K, proj, nproj, true);
 }
 
 u15h_status

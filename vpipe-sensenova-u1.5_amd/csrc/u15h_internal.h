@@ -138,6 +138,15 @@ hipError_t launch_gather_rows(const uint16_t* src, const int32_t* perm,
 // Forces every kernel's code object to load; false if any cannot.
 bool kernels_loadable();
 
+// The allocation-free entry point's split-K scratch: a static device array
+// of this many bytes (one 256 x 256 tile of 4-byte sums per CU, up to 256
+// CUs), looked up per device (at most kMaxScratchDevices of them).
+constexpr size_t kNoAllocScratchBytes = (size_t)256 * kBM * kBN * 4;
+constexpr int kMaxScratchDevices = 64;
+// Device address of that array on `device`, which must be current on the
+// first call for it; the result is kept per device.
+hipError_t noalloc_scratch(int device, void** out);
+
 // Sets the context's last-error text (u15h_last_error) and returns `st`;
 // for host code of the library outside u15h_api.cc.
 u15h_status set_error(u15h_ctx* ctx, u15h_status st, const char* msg);

@@ -35,6 +35,7 @@
 // stage) is zero-filled by pushing the invalid chunks' offsets out of range.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "u15h_internal.h"
@@ -2263,6 +2264,45 @@ launch_gather_rows(const uint16_t* src, const int32_t* perm, int M, int cols,
   return hipGetLastError();
 }
 
+}  // namespace u15h
+
+// ---- the allocation-free entry point's scratch ----------------------------
+// Split-K partial sums for u15h_mot_linear_noalloc: one 256 x 256 tile of
+// 4-byte partial sums per compute unit of a GPU with up to 256 CUs (the
+// planner never asks for more than one per CU), 64 MiB per device, held
+// by every device the library runs on until the process ends.  Host code
+// must not pass `scratch` itself to a kernel: in host code the name is a
+// host-side stand-in, not a device address.  Its per-device address comes
+// from hipGetSymbolAddress below and is the only handle host code uses.
+static __device__ __align__(256) char scratch[u15h::kNoAllocScratchBytes];
+
+namespace u15h {
+
+hipError_t
+noalloc_scratch(int device, void** out)
+{
+  // Looked up once per device (with that device current: u15h_create
+  // calls this right after binding it) and kept; each GPU holds its own
+  // copy of the array at its own address.
+  static std::mutex mu;
+  static bool done[kMaxScratchDevices];
+  static hipError_t res[kMaxScratchDevices];
+  static void* ptr[kMaxScratchDevices];
+  *out = nullptr;
+  if (device < 0 || device >= kMaxScratchDevices) { return hipErrorInvalidDevice; }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!done[device]) {
+    void* p = nullptr;
+    res[device] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    ptr[device] = res[device] == hipSuccess ? p : nullptr;
+    done[device] = true;
+  }
+  *out = ptr[device];
+  return res[device];
+}
+
+namespace {
+
 template <class MB, class MI, int WN>
 bool
 gemm_kernels_loadable()
@@ -2283,6 +2323,8 @@ gemm_kernels_loadable()
   }
   return true;
 }
+
+}  // namespace
 
 bool
 kernels_loadable()

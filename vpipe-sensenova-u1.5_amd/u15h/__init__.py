@@ -89,6 +89,8 @@ def load_library() -> ctypes.CDLL:
         "u15h_linear": (i, [vp, vp, vp, vp, vp, vp, i, i, i]),
         "u15h_mot_linear": (i, [vp, vp, vp, i, i, i,
                                 ctypes.POINTER(_MotProj), i]),
+        "u15h_mot_linear_noalloc": (i, [vp, vp, vp, i, i, i,
+                                        ctypes.POINTER(_MotProj), i]),
         "u15h_swiglu": (i, [vp, vp, vp, vp, vp, i64]),
         "u15h_mot_gate_up_swiglu": (i, [vp, vp, vp, i, i, i, vp, vp, vp, vp,
                                         vp, i]),
@@ -429,9 +431,12 @@ class Ops:
                                    _ptr(w), _ptr(bias), _ptr(y), M, K, N)
         self._check(st, "u15h_linear")
 
-    def mot_linear(self, x, M_und, M_gen, K, projs, stream=None):
+    def mot_linear(self, x, M_und, M_gen, K, projs, stream=None,
+                   noalloc=False):
         """Grouped MoT GEMM.  projs: list of dicts with keys
-        w_und, w_gen, y and optionally bias_und, bias_gen."""
+        w_und, w_gen, y and optionally bias_und, bias_gen.  noalloc=True
+        calls u15h_mot_linear_noalloc (split-K sums in the library's static
+        scratch; no device allocation)."""
         M = M_und + M_gen
         _need(x, torch.bfloat16, (M, K), "x")
         if not 1 <= len(projs) <= MAX_PROJ:
@@ -453,9 +458,10 @@ class Ops:
                 p["bias_und"].data_ptr() if p.get("bias_und") is not None else None,
                 p["bias_gen"].data_ptr() if p.get("bias_gen") is not None else None,
                 p["y"].data_ptr(), N)
-        st = self._lib.u15h_mot_linear(self._ctx, _stream(stream), _ptr(x),
-                                       M_und, M_gen, K, arr, len(projs))
-        self._check(st, "u15h_mot_linear")
+        fn = self._lib.u15h_mot_linear_noalloc if noalloc else self._lib.u15h_mot_linear
+        st = fn(self._ctx, _stream(stream), _ptr(x), M_und, M_gen, K, arr,
+                len(projs))
+        self._check(st, "u15h_mot_linear_noalloc" if noalloc else "u15h_mot_linear")
 
     # ---- affine-quantized weights ---------------------------------------
     @staticmethod
