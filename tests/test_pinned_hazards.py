@@ -120,11 +120,18 @@ def test_no_valu_write_just_before_an_mfma_read(kernels):
         assert not _valu_hazards(body), (name, _valu_hazards(body)[:3])
 
 
+def _touches_agpr(s):
+    return re.search(r"\ba\d+\b|\ba\[", s) is not None
+
+
 def test_loop_keeps_accumulators_in_place(kernels):
     for name, body in kernels.items():
         idx = [i for i, s in enumerate(body) if s.startswith("v_mfma")]
         between = body[idx[0]:idx[-1]]
         assert not any(s.startswith("v_accvgpr") for s in between), name
+        # nor any other access (a spill or reload) of an AGPR
+        assert not any(_touches_agpr(s) for s in between
+                       if not s.startswith("v_mfma")), name
         # tied: every MFMA's result tuple is its accumulator input
         for i in idx:
             ops = [o.strip() for o in body[i].split(None, 1)[1].split(",")]
@@ -134,3 +141,27 @@ def test_loop_keeps_accumulators_in_place(kernels):
 def test_results_settle_before_agpr_reads(kernels):
     for name, body in kernels.items():
         assert _unsettled_agpr_read(body) is None, (name, _unsettled_agpr_read(body))
+
+
+def _unsettled_agpr_write(body):
+    """The last AGPR write before the first MFMA, with fewer than 2 wait
+    states between it and the MFMA, or None."""
+    first = min(i for i, s in enumerate(body) if s.startswith("v_mfma"))
+    ws = 0
+    for s in reversed(body[:first]):
+        op = s.split()[0]
+        if _touches_agpr(s) and (op.startswith("v_accvgpr_write") or
+                                 op.startswith("v_mov")):
+            return None if ws >= 2 else (s, ws)
+        ws += _wait_states(s)
+    return None
+
+
+def test_checker_catches_planted_early_write():
+    assert _unsettled_agpr_write(["v_accvgpr_write_b32 a0, 0", MF])
+    assert not _unsettled_agpr_write(["v_accvgpr_write_b32 a0, 0", "s_nop 4", MF])
+
+
+def test_accumulators_settle_before_the_first_mfma(kernels):
+    for name, body in kernels.items():
+        assert _unsettled_agpr_write(body) is None, (name, _unsettled_agpr_write(body))
