@@ -1,13 +1,14 @@
 """The 4-wave GEMM issues its MFMAs as inline asm with the accumulator
-tied in AGPRs, which the compiler's hazard tracking does not see into.
-This compiles the kernels to gfx950 assembly (no GPU needed) and checks,
-for every 4-wave GEMM kernel, what that tracking would otherwise
-guarantee:
+tied in AGPRs, and the skinny GEMM with the accumulator tied in VGPRs;
+the compiler's hazard tracking does not see into either.  This compiles
+the kernels to gfx950 assembly (no GPU needed) and checks, for every such
+kernel, what that tracking would otherwise guarantee:
   - no VALU instruction writes an MFMA source register within the
     2 wait states before the MFMA reads it;
-  - the main loop moves no accumulator (no v_accvgpr_* between MFMAs);
+  - the main loop moves no accumulator (no copy between MFMAs);
   - every MFMA result is followed by at least 19 wait states (s_nop) before
-    anything outside the MFMAs touches an AGPR."""
+    anything outside the MFMAs touches an accumulator, and the zeroing of
+    the accumulators precedes the first MFMA by at least 2."""
 import pathlib
 import re
 import shutil
@@ -46,7 +47,7 @@ def kernels():
     found = {}
     name = None
     for raw in out.splitlines():
-        if re.match(r"^_Z\S*mot_gemm_kernel\S*Li2E\S*:", raw):
+        if re.match(r"^_Z\S*(mot_gemm_kernel\S*Li2E|skinny_(?:reg|lds)_kernel)\S*:", raw):
             name = raw.split(":")[0]
             found[name] = []
             continue
@@ -57,15 +58,41 @@ def kernels():
             s = raw.strip()
             if s and not s.startswith(";") and not s.startswith(".") and not s.endswith(":"):
                 found[name].append(s)
-    assert found, "no 4-wave GEMM kernels in the assembly"
+    assert found, "no pinned-MFMA kernels in the assembly"
     return found
 
 
 def test_every_epilogue_has_a_pinned_kernel(kernels):
-    # bf16, SwiGLU, int32 and dequant epilogues, 256 MFMAs each
-    assert len(kernels) == 4
-    for body in kernels.values():
-        assert sum(1 for s in body if s.startswith("v_mfma")) == 256
+    # 4-wave GEMM: bf16, SwiGLU, int32 and dequant epilogues, 256 MFMAs
+    # each; skinny GEMM: the four row-group builds (register kernel for 16
+    # rows, LDS kernel for 32, 64 and 128), 16 MFMAs per 16 rows and
+    # unrolled K-block (2 k-steps), 8 blocks unrolled but 4 at 128 rows
+    four = [n for n in kernels if "mot_gemm_kernel" in n]
+    skinny = [n for n in kernels if "skinny_" in n]
+    assert len(four) == 4 and len(skinny) == 4
+    for n in four:
+        assert sum(1 for s in kernels[n] if s.startswith("v_mfma")) == 256
+    for n in skinny:
+        mt = int(re.search(r"skinny_(?:reg|lds)_kernelILi(\d+)E", n).group(1))
+        depth = 4 if mt == 8 else 8
+        assert sum(1 for s in kernels[n] if s.startswith("v_mfma")) == 2 * mt * depth
+
+
+def _operands(s):
+    return [o.strip() for o in s.split(None, 1)[1].split(",")] if " " in s else []
+
+
+def _acc_regs(body):
+    """Every register an MFMA of the body accumulates in."""
+    regs = set()
+    for s in body:
+        if s.startswith("v_mfma"):
+            regs |= _regs(_operands(s)[0])
+    return regs
+
+
+def _touches(s, regs):
+    return any(_regs(o) & regs for o in _operands(s))
 
 
 def _valu_hazards(body):
@@ -74,32 +101,34 @@ def _valu_hazards(body):
     for i, s in enumerate(body):
         if not s.startswith("v_mfma"):
             continue
-        srcs = set().union(*(_regs(o.strip()) for o in s.split(None, 1)[1].split(",")[1:]))
+        srcs = set().union(*(_regs(o) for o in _operands(s)[1:]))
         ws, k = 0, i - 1
         while k >= 0 and ws < 2:
             p = body[k]
             op = p.split()[0]
             if op.startswith("v_") and not op.startswith("v_mfma"):
-                if _regs(p.split(None, 1)[1].split(",")[0].strip()) & srcs:
+                if _regs(_operands(p)[0]) & srcs:
                     bad.append((p, ws, s))
             ws += _wait_states(p)
             k -= 1
     return bad
 
 
-def _unsettled_agpr_read(body):
-    """The first AGPR access after the last MFMA with fewer than 19 wait
-    states between them, or None."""
+def _unsettled_acc_read(body):
+    """The first access of an accumulator register after the last MFMA
+    with fewer than 19 wait states between them, or None."""
+    acc = _acc_regs(body)
     last = max(i for i, s in enumerate(body) if s.startswith("v_mfma"))
     ws = 0
     for s in body[last + 1:]:
-        if re.search(r"\ba\d+\b|\ba\[", s):
+        if _touches(s, acc):
             return None if ws >= 19 else (s, ws)
         ws += _wait_states(s)
     return None
 
 
 MF = "v_mfma_f32_16x16x32_bf16 a[0:3], v[10:13], v[14:17], a[0:3]"
+MFV = "v_mfma_f32_16x16x32_bf16 v[20:23], v[10:13], v[14:17], v[20:23]"
 
 
 def test_checkers_catch_planted_mistakes():
@@ -109,10 +138,15 @@ def test_checkers_catch_planted_mistakes():
     assert _valu_hazards(["v_mov_b32_e32 v15, v1", "s_nop 0", MF])
     assert not _valu_hazards(["v_mov_b32_e32 v11, v1", "s_nop 1", MF])
     assert not _valu_hazards(["v_mov_b32_e32 v20, v1", MF])
+    # a VGPR accumulator written just before the MFMA reads it
+    assert _valu_hazards(["v_mov_b32_e32 v21, 0", MFV])
     # an accumulator read 8 wait states after the last MFMA: caught
-    assert _unsettled_agpr_read([MF, "s_nop 7", "v_accvgpr_read_b32 v0, a0"])
-    assert not _unsettled_agpr_read([MF, "s_nop 7", "s_nop 7", "s_nop 7",
-                                     "v_accvgpr_read_b32 v0, a0"])
+    assert _unsettled_acc_read([MF, "s_nop 7", "v_accvgpr_read_b32 v0, a0"])
+    assert not _unsettled_acc_read([MF, "s_nop 7", "s_nop 7", "s_nop 7",
+                                    "v_accvgpr_read_b32 v0, a0"])
+    assert _unsettled_acc_read([MFV, "s_nop 7", "v_add_f32_e32 v0, v22, v1"])
+    assert not _unsettled_acc_read([MFV, "s_nop 7", "s_nop 7", "s_nop 7",
+                                    "v_add_f32_e32 v0, v22, v1"])
 
 
 def test_no_valu_write_just_before_an_mfma_read(kernels):
@@ -120,48 +154,51 @@ def test_no_valu_write_just_before_an_mfma_read(kernels):
         assert not _valu_hazards(body), (name, _valu_hazards(body)[:3])
 
 
-def _touches_agpr(s):
-    return re.search(r"\ba\d+\b|\ba\[", s) is not None
-
-
 def test_loop_keeps_accumulators_in_place(kernels):
     for name, body in kernels.items():
+        acc = _acc_regs(body)
         idx = [i for i, s in enumerate(body) if s.startswith("v_mfma")]
         between = body[idx[0]:idx[-1]]
-        assert not any(s.startswith("v_accvgpr") for s in between), name
-        # nor any other access (a spill or reload) of an AGPR
-        assert not any(_touches_agpr(s) for s in between
+        if any(reg[0] == "a" for reg in acc):
+            # AGPR accumulators: no accumulator move at all (in VGPR
+            # kernels the compiler may park other values in AGPRs)
+            assert not any(s.startswith("v_accvgpr") for s in between), name
+        # nor any other access (a copy, spill or reload) of an accumulator
+        assert not any(_touches(s, acc) for s in between
                        if not s.startswith("v_mfma")), name
-        # tied: every MFMA's result tuple is its accumulator input
+        # tied: every MFMA's result tuple is its accumulator input (AGPRs
+        # in the 4-wave GEMM)
         for i in idx:
-            ops = [o.strip() for o in body[i].split(None, 1)[1].split(",")]
-            assert ops[0] == ops[3] and ops[0].startswith("a["), body[i]
+            ops = _operands(body[i])
+            assert ops[0] == ops[3], body[i]
+            assert ops[0].startswith("a[") or "skinny" in name, body[i]
 
 
-def test_results_settle_before_agpr_reads(kernels):
+def test_results_settle_before_accumulator_reads(kernels):
     for name, body in kernels.items():
-        assert _unsettled_agpr_read(body) is None, (name, _unsettled_agpr_read(body))
+        assert _unsettled_acc_read(body) is None, (name, _unsettled_acc_read(body))
 
 
-def _unsettled_agpr_write(body):
-    """The last AGPR write before the first MFMA, with fewer than 2 wait
-    states between it and the MFMA, or None."""
+def _unsettled_acc_write(body):
+    """The last write of an accumulator register before the first MFMA,
+    with fewer than 2 wait states between it and the MFMA, or None."""
+    acc = _acc_regs(body)
     first = min(i for i, s in enumerate(body) if s.startswith("v_mfma"))
     ws = 0
     for s in reversed(body[:first]):
-        op = s.split()[0]
-        if _touches_agpr(s) and (op.startswith("v_accvgpr_write") or
-                                 op.startswith("v_mov")):
+        ops = _operands(s)
+        if s.startswith("v_") and ops and _regs(ops[0]) & acc:
             return None if ws >= 2 else (s, ws)
         ws += _wait_states(s)
     return None
 
 
 def test_checker_catches_planted_early_write():
-    assert _unsettled_agpr_write(["v_accvgpr_write_b32 a0, 0", MF])
-    assert not _unsettled_agpr_write(["v_accvgpr_write_b32 a0, 0", "s_nop 4", MF])
+    assert _unsettled_acc_write(["v_accvgpr_write_b32 a0, 0", MF])
+    assert not _unsettled_acc_write(["v_accvgpr_write_b32 a0, 0", "s_nop 4", MF])
+    assert _unsettled_acc_write(["v_mov_b32_e32 v23, 0", MFV])
 
 
 def test_accumulators_settle_before_the_first_mfma(kernels):
     for name, body in kernels.items():
-        assert _unsettled_agpr_write(body) is None, (name, _unsettled_agpr_write(body))
+        assert _unsettled_acc_write(body) is None, (name, _unsettled_acc_write(body))

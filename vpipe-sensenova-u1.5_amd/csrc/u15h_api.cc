@@ -22,6 +22,8 @@ struct u15h_ctx {
   int device = 0;
   int num_cu = 256;
   bool split_on = true;      // env U15H_SPLIT=0 turns the split-K tail off
+  // env U15H_SKINNY=0 keeps batches of <= 128-row problems on the tiled GEMM
+  bool skinny_on = true;
   // GEMM kernel build: 8 or 4 waves per workgroup (env U15H_WAVES) and the
   // 8-wave build's MFMA shape (env U15H_MFMA16).
   u15h::GemmShape gemm = {8, 0, 1};
@@ -203,6 +205,96 @@ plan_split(u15h_ctx* ctx, GemmBatch& b, bool noalloc = false)
              : fail(ctx, U15H_EINVAL, "split workspace overflow");
 }
 
+// The skinny route: a bf16 batch whose problems all have at most 128 rows
+// (und prefill, small decode-like steps) and plain [N][K] weights.  There
+// the weights are the traffic; the tiled GEMM would run its 256-row tiles
+// mostly empty.
+bool
+skinny_fits(const u15h_ctx* ctx, const GemmBatch& b)
+{
+  if (!ctx->skinny_on || b.nprob <= 0 || b.kbytes % 128 != 0) { return false; }
+  for (int i = 0; i < b.nprob; ++i) {
+    const GemmProblem& p = b.p[i];
+    if (p.rows > u15h::kSkinnyMaxRows || p.wld != b.kbytes || p.n % 4 != 0) {
+      return false;
+    }
+  }
+  return true;
+}
+
+// Launches a batch that skinny_fits on the skinny kernels.  K shares S
+// (a power of two) are added while the workgroups stay within what the
+// CUs hold at once, each share keeps enough K-blocks to fill its waves'
+// prefetch, and the fp32 partial sums (written and read once) stay at most
+// half the weight bytes: S * rows * 8 <= K.
+// The partials go to the split-K workspace (or, with `noalloc`, the static
+// scratch); a batch whose partials would not fit takes fewer shares.
+u15h_status
+skinny_launch(u15h_ctx* ctx, const GemmBatch& b, hipStream_t s, bool noalloc,
+              const u15h::GemmEvents& ev)
+{
+  u15h::SkinnyBatch k;
+  std::memset(&k, 0, sizeof k);
+  k.kbytes = b.kbytes;
+  k.nprob = b.nprob;
+  for (int i = 0; i < b.nprob; ++i) { k.max_rows = std::max(k.max_rows, b.p[i].rows); }
+  k.cols = u15h::skinny_cols(k.max_rows);
+  for (int i = 0; i < b.nprob; ++i) {
+    const GemmProblem& p = b.p[i];
+    u15h::SkinnyProblem& q = k.p[i];
+    q.a = p.a;
+    q.w = p.w;
+    q.y = p.y;
+    q.bias = p.bias;
+    q.rows = p.rows;
+    q.n = p.n;
+    q.ldy = p.ldy;
+    q.cb_begin = k.total_cb;
+    k.total_cb += (p.n + k.cols - 1) / k.cols;
+  }
+  const int K = b.kbytes / 2;
+  const int nkb = b.kbytes / 128;
+  // two resident workgroups per CU (64 KiB of LDS each in the LDS
+  // kernels); a share keeps 32 K-blocks (8 per wave) in the register
+  // kernel, 16 in the LDS kernels
+  const int per_cu = 2;
+  const int min_kb = k.cols == 16 ? 32 : 16;
+  int S = 1;
+  while (S < 16 && 2 * S * k.total_cb <= per_cu * ctx->num_cu &&
+         nkb / (2 * S) >= min_kb && 2 * S * k.max_rows * 8 <= K) {
+    S *= 2;
+  }
+  const size_t cap = noalloc ? u15h::kNoAllocScratchBytes : split_ws_capacity(ctx);
+  for (;;) {
+    k.split = S;
+    if (S == 1 || u15h::skinny_ws_floats(k) * 4 <= cap) { break; }
+    S /= 2;
+  }
+  if (S > 1) {
+    if (noalloc) {
+      if (ctx->noalloc_ws == nullptr) {
+        return fail(ctx, U15H_ENODEV, "static split-K scratch unavailable: %s",
+                    hipGetErrorString(ctx->noalloc_err));
+      }
+      k.ws = static_cast<float*>(ctx->noalloc_ws);
+    } else {
+      if (ctx->split_ws == nullptr &&
+          hipMalloc(&ctx->split_ws, split_ws_capacity(ctx)) != hipSuccess) {
+        ctx->split_ws = nullptr;
+        return fail(ctx, U15H_ENOMEM, "split-K workspace of %zu bytes",
+                    split_ws_capacity(ctx));
+      }
+      k.ws = static_cast<float*>(ctx->split_ws);
+    }
+    size_t off = 0;
+    for (int i = 0; i < k.nprob; ++i) {
+      k.p[i].ws_off = off;
+      off += (size_t)S * k.p[i].rows * k.p[i].n;
+    }
+  }
+  return launched(ctx, u15h::launch_skinny_bf16(k, s, ev), "skinny_gemm_bf16");
+}
+
 // Shape limits shared by every GEMM entry point.  Byte offsets inside a
 // tile are 32-bit, so one row of K may be at most 2^31 / 256 / 2 bytes.
 u15h_status
@@ -378,6 +470,7 @@ u15h_create(int device, u15h_ctx** out)
   ctx->noalloc_err = noalloc_err;
   ctx->num_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
   ctx->split_on = env_int("U15H_SPLIT", 1) != 0;
+  ctx->skinny_on = env_int("U15H_SKINNY", 1) != 0;
   ctx->gemm.waves = env_int("U15H_WAVES", 8) == 4 ? 4 : 8;
   ctx->gemm.cus = env_int("U15H_PERSIST", 1) != 0 ? ctx->num_cu : 0;
   ctx->gemm.mfma16 = std::max(-1, std::min(1, env_int("U15H_MFMA16", 1)));
@@ -417,6 +510,9 @@ dense_bf16(u15h_ctx* ctx, hipStream_t s, const u15h_bf16* x,
   GemmBatch b = empty_batch(K * 2);
   add_problem(b, x, w, nullptr, y, bias, nullptr, nullptr, M, N, N,
               u15h::tile_cols(Epi::kBf16));
+  if (skinny_fits(ctx, b)) {
+    return skinny_launch(ctx, b, s, false, take_profile_event(ctx));
+  }
   u15h_status st = plan_split(ctx, b);
   if (st != U15H_OK) { return st; }
   return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kBf16, ctx->gemm, s, take_profile_event(ctx)), "gemm_bf16");
@@ -502,6 +598,9 @@ mot_linear_impl(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
                 M_und, p.N, p.N, tc);
   }
   if ((st = check_tiles(ctx, b)) != U15H_OK) { return st; }
+  if (skinny_fits(ctx, b)) {
+    return skinny_launch(ctx, b, as_stream(stream), noalloc, take_profile_event(ctx));
+  }
   if ((st = plan_split(ctx, b, noalloc)) != U15H_OK) { return st; }
   return launched(ctx, u15h::launch_gemm_bf16(b, Epi::kBf16, ctx->gemm, as_stream(stream), take_profile_event(ctx)),
                   "mot_gemm_bf16");

@@ -94,6 +94,48 @@ struct GemmEvents {
 };
 hipError_t launch_gemm_bf16(const GemmBatch& b, Epi epi, const GemmShape& g,
                             hipStream_t s, const GemmEvents& ev);
+
+// The skinny bf16 GEMM for problems of at most kSkinnyMaxRows rows: one
+// workgroup per column block (skinny_cols(max_rows) output columns: 16 up
+// to 16 rows, 64 above) and K share.  Problem p's column blocks are
+// [cb_begin, cb_begin + ceil(n / cols)); with S > 1 the shares' fp32
+// partial sums go to ws + ws_off as [S][rows][n] and a second kernel adds
+// them in share order, the bias, and rounds to bf16.
+constexpr int kSkinnyMaxRows = 128;
+constexpr int skinny_cols(int max_rows) { return max_rows <= 16 ? 16 : 64; }
+struct SkinnyProblem {
+  const void*     a;      // activation rows [rows][K] (bf16)
+  const void*     w;      // weight rows [n][K] (bf16)
+  void*           y;      // output rows [rows][ldy] (bf16)
+  const uint16_t* bias;   // bf16 [n] or null
+  int rows;
+  int n;
+  int ldy;
+  int cb_begin;           // first column block of this problem
+  size_t ws_off;          // floats from ws to this problem's partial sums
+};
+struct SkinnyBatch {
+  SkinnyProblem p[kMaxProb];
+  int nprob;
+  int kbytes;             // bytes per row of K (K * 2; a multiple of 128)
+  int split;              // K shares per column block (S)
+  int cols;               // output columns per block (skinny_cols)
+  int total_cb;           // column blocks over all problems
+  int max_rows;           // largest problem (picks the kernel build)
+  float* ws;              // partial sums when split > 1
+};
+// Floats of partial-sum workspace a skinny batch needs.
+inline size_t skinny_ws_floats(const SkinnyBatch& b)
+{
+  if (b.split <= 1) { return 0; }
+  size_t f = 0;
+  for (int i = 0; i < b.nprob; ++i) {
+    f += (size_t)b.split * b.p[i].rows * b.p[i].n;
+  }
+  return f;
+}
+hipError_t launch_skinny_bf16(const SkinnyBatch& b, hipStream_t s,
+                              const GemmEvents& ev);
 hipError_t launch_gemm_i8(const GemmBatch& b, Epi epi, const GemmShape& g,
                           hipStream_t s, const GemmEvents& ev);
 hipError_t launch_quant_rows_i8(const uint16_t* x, int rows, int K,

@@ -35,6 +35,7 @@
 // stage) is zero-filled by pushing the invalid chunks' offsets out of range.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 
@@ -2041,6 +2042,358 @@ transpose_rows_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ d
   }
 }
 
+// ---- skinny GEMM: problems of at most 128 rows --------------------------
+// Below a few hundred rows per weight set a projection streams its weights
+// (N x K bf16) and little else; the tiled GEMM's 256-row tiles then run
+// mostly empty, and its split-K tail sends 256 x 256 fp32 partial tiles
+// through memory.  Two kernels cover this regime, both built on the same
+// fragment layout:
+//
+// K order inside a 64-element K-block: lane group g (lanes 16g .. 16g+15)
+// holds elements [16g, 16g + 16) of its row for both operands, the first
+// eight as MFMA k-step 0 and the rest as k-step 1.  The products summed
+// are exactly the block's, in another order, and each lane's bytes of a
+// row are one 32-byte run (a row's 128 bytes in four lanes).
+// v_mfma_f32_16x16x32_bf16 takes the weight fragment as A (16 output
+// columns) and the activation fragment as B (16 rows): lane (g, r) ends
+// with columns 4g .. 4g + 3 of its 16 for row r of each 16-row group.
+//
+// Loads of one wave return in issue order, so a wave can only run as far
+// ahead of its data as its earliest outstanding load allows; both kernels
+// keep every operand kSkDepth K-blocks ahead.
+//
+// The accumulators are tied to their MFMAs (inline asm "+v"): the
+// builtin's untied 16x16 result makes the compiler rotate them through
+// copies.  The asm is volatile and writes no memory, so the loads and
+// reads around it keep their place; the hazards the compiler's tracking
+// would cover are covered with wait states (the zeroing before the first
+// MFMA, the last results before the epilogue reads them).
+constexpr int kSkDepth = 8;    // K-blocks in flight per wave
+
+// Bias, rounding and store of 4 output columns n..n+3 of row m.
+__device__ __forceinline__ void
+skinny_store(const SkinnyProblem& P, int m, int n, f32x4_t v, uint2 bb)
+{
+  const float v0 = v[0] + bf16_to_f32(bb.x & 0xffffu);
+  const float v1 = v[1] + bf16_to_f32(bb.x >> 16);
+  const float v2 = v[2] + bf16_to_f32(bb.y & 0xffffu);
+  const float v3 = v[3] + bf16_to_f32(bb.y >> 16);
+  *reinterpret_cast<uint2*>(static_cast<uint16_t*>(P.y) + (size_t)m * P.ldy + n) =
+      make_uint2(pack_bf16x2(v0, v1), pack_bf16x2(v2, v3));
+}
+
+// Problem of a column block (uniform over the workgroup).
+__device__ __forceinline__ int
+skinny_problem(const SkinnyBatch& B, int cbg)
+{
+  int pi = 0;
+#pragma unroll
+  for (int q = 1; q < kMaxProb; ++q) {
+    if (q < B.nprob && cbg >= B.p[q].cb_begin) { pi = q; }
+  }
+  return pi;
+}
+
+// Rows <= 16: a workgroup computes 16 output columns
+// over a K share; its four waves take every fourth K-block each and load
+// both operands straight into registers (the activation rows are few and
+// L2-resident), with no barrier until the four partial sums meet in LDS,
+// where wave 0 adds them in wave order.
+template <int MT>
+__global__ __launch_bounds__(256) void
+skinny_reg_kernel(const SkinnyBatch B)
+{
+  __shared__ f32x4_t red[4][MT][64];
+  const int S = B.split;
+  const int cbg = blockIdx.x / S;
+  const int share = blockIdx.x - cbg * S;
+  const SkinnyProblem& P = B.p[skinny_problem(B, cbg)];
+  const int kbytes = B.kbytes;
+  const int nkb = kbytes / 128;
+  const int kb0 = share * nkb / S;
+  const int nk = (share + 1) * nkb / S - kb0;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4, r = lane & 15;
+  const int n0 = (cbg - P.cb_begin) * 16;
+  const int nw = (nk - wave + 3) / 4;              // this wave's K-blocks
+
+  // weight rows [n0, n0 + 16) and activation rows [0, rows); rows past
+  // either read as zero
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(
+      static_cast<const char*>(P.w) + (size_t)n0 * kbytes,
+      max(0, min(16, P.n - n0)) * kbytes);
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(P.a, P.rows * kbytes);
+  const int lv = r * kbytes + g * 32;               // row r, bytes 32g..
+
+  i32x4_t wreg[kSkDepth][2];
+  i32x4_t xreg[kSkDepth][MT][2];
+  auto issue = [&](int slot, int j) {
+    const int oob = j < nw ? 0 : kOobOffset;        // past the share: zeros
+    const int ko = __builtin_amdgcn_readfirstlane(
+        (kb0 + wave + 4 * min(j, max(nw - 1, 0))) * 128);
+    wreg[slot][0] = __builtin_amdgcn_raw_buffer_load_b128(wr, lv + oob, ko, 0);
+    wreg[slot][1] = __builtin_amdgcn_raw_buffer_load_b128(wr, lv + 16 + oob, ko, 0);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int v = lv + mt * 16 * kbytes + oob;
+      xreg[slot][mt][0] = __builtin_amdgcn_raw_buffer_load_b128(xr, v, ko, 0);
+      xreg[slot][mt][1] = __builtin_amdgcn_raw_buffer_load_b128(xr, v + 16, ko, 0);
+    }
+  };
+
+  f32x4_t acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    acc[mt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    asm volatile("" : "+v"(acc[mt]));
+  }
+  asm volatile("s_nop 4");
+  // the loads in K order (compiler fences between the blocks)
+#pragma unroll
+  for (int d = 0; d < kSkDepth; ++d) {
+    asm volatile("" ::: "memory");
+    issue(d, d);
+  }
+  const int nw_pad = (nw + kSkDepth - 1) / kSkDepth * kSkDepth;
+  for (int j0 = 0; j0 < nw_pad; j0 += kSkDepth) {
+#pragma unroll
+    for (int d = 0; d < kSkDepth; ++d) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
+                       : "+v"(acc[mt]) : "v"(wreg[d][ks]), "v"(xreg[d][mt][ks]));
+        }
+      }
+      asm volatile("" ::: "memory");
+      issue(d, j0 + d + kSkDepth);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
+               ::: "memory");
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    asm volatile("" : "+v"(acc[mt]));
+    red[wave][mt][lane] = acc[mt];
+  }
+  __syncthreads();
+  if (wave != 0) { return; }
+  const int n = n0 + 4 * g;
+  if (n >= P.n) { return; }
+  uint2 bb = make_uint2(0u, 0u);
+  if (S == 1 && P.bias != nullptr) { bb = *reinterpret_cast<const uint2*>(P.bias + n); }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = mt * 16 + r;
+    if (m >= P.rows) { continue; }
+    const f32x4_t v = ((red[0][mt][lane] + red[1][mt][lane]) + red[2][mt][lane]) +
+                      red[3][mt][lane];
+    if (S == 1) {
+      skinny_store(P, m, n, v, bb);
+    } else {
+      float* ws = B.ws + P.ws_off + (size_t)share * P.rows * P.n;
+      *reinterpret_cast<f32x4_t*>(ws + (size_t)m * P.n + n) = v;
+    }
+  }
+}
+
+// Rows 17..128: a workgroup computes 64 output columns over a K share.
+// Wave w streams weight rows [16w, 16w + 16) of the block into registers,
+// while the activation rows' K-block, which all four waves use, goes to
+// LDS by DMA through a ring of D stages (one __shared__ object each, so
+// the compiler can tell a stage's DMA from another stage's reads), as
+// deep as the weight lead, which a shallower ring would cut short: 8
+// stages (64 KiB) up to 64 rows, 4 (64 KiB) up to 128, so that two
+// workgroups fit a CU either way.
+template <int MT, int D>
+__device__ __forceinline__ void
+skinny_lds_tile(const SkinnyBatch& B, char* const (&xs)[D])
+{
+  constexpr int kXInst = MT / 2;                    // DMA loads per wave
+  const int S = B.split;
+  const int cbg = blockIdx.x / S;
+  const int share = blockIdx.x - cbg * S;
+  const SkinnyProblem& P = B.p[skinny_problem(B, cbg)];
+  const int kbytes = B.kbytes;
+  const int nkb = kbytes / 128;
+  const int kb0 = share * nkb / S;
+  const int nk = (share + 1) * nkb / S - kb0;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4, r = lane & 15;
+  const int n0 = (cbg - P.cb_begin) * 64 + wave * 16;
+
+  // weight rows [n0, n0 + 16) clipped to n: rows past it read as zero
+  const int wrows = max(0, min(16, P.n - n0));
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(
+      static_cast<const char*>(P.w) + (size_t)min(n0, P.n) * kbytes,
+      wrows * kbytes);
+  const int wv = r * kbytes + g * 32;
+  // activation rows [0, rows): rows past them read as zero
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(P.a, P.rows * kbytes);
+  // DMA: instruction j of wave w fills 16-byte stage slots
+  // p = 32 MT w + 64 j + lane, slot p of row p / 8 holding chunk
+  // (p % 8) ^ (row % 8) of the row's K-block
+  int xv[kXInst];
+#pragma unroll
+  for (int j = 0; j < kXInst; ++j) {
+    const int p = 32 * MT * wave + 64 * j + lane;
+    const int m = p >> 3;
+    xv[j] = m * kbytes + ((((p & 7) ^ (m & 7))) << 4);
+  }
+  // fragment reads: row r of a 16-row group, chunk 2g + ks
+  int xo[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    xo[ks] = r * 128 + (((2 * g + ks) ^ (r & 7)) << 4);
+  }
+
+  auto issue_x = [&](char* st, int i) {
+    const int oob = i < nk ? 0 : kOobOffset;       // past the share: zeros
+    const int ko = __builtin_amdgcn_readfirstlane((kb0 + min(i, nk - 1)) * 128);
+#pragma unroll
+    for (int j = 0; j < kXInst; ++j) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          xr, (__attribute__((address_space(3))) void*)(st + 32 * MT * 16 * wave + 1024 * j),
+          16, xv[j] + oob, ko, 0, 0);
+    }
+  };
+  i32x4_t wreg[D][2];
+  auto issue_w = [&](int slot, int i) {
+    const int oob = i < nk ? 0 : kOobOffset;
+    const int ko = __builtin_amdgcn_readfirstlane((kb0 + min(i, nk - 1)) * 128);
+    wreg[slot][0] = __builtin_amdgcn_raw_buffer_load_b128(wr, wv + oob, ko, 0);
+    wreg[slot][1] = __builtin_amdgcn_raw_buffer_load_b128(wr, wv + 16 + oob, ko, 0);
+  };
+
+  f32x4_t acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    acc[mt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    asm volatile("" : "+v"(acc[mt]));
+  }
+  asm volatile("s_nop 4");
+
+  // The wait before each barrier counts loads in issue order, so the order
+  // is pinned with compiler fences: the prologue's x stages, then its
+  // weight blocks in K order; in each block the x refill, then the weight
+  // refill.
+#pragma unroll
+  for (int i = 0; i + 1 < D; ++i) { issue_x(xs[i], i); }
+#pragma unroll
+  for (int i = 0; i < D; ++i) {
+    asm volatile("" ::: "memory");
+    issue_w(i, i);
+  }
+  // Before block i's barrier this wave's DMA of x stage i has landed: at
+  // most the loads issued after it may be in flight -- the weight loads
+  // of its own iteration and D - 2 later iterations' x and weight
+  // loads (earlier in the prologue, where more follow it).
+  constexpr int kAfterX = 2 + (D - 2) * (kXInst + 2);
+  static_assert(kAfterX < 64, "vmcnt holds at most 63");
+  const int nk_pad = (nk + D - 1) / D * D;
+  for (int i0 = 0; i0 < nk_pad; i0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int i = i0 + d;
+      // (a bare s_barrier: __syncthreads' fence would wait for every
+      // weight load in flight)
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kAfterX) : "memory");
+      // every wave is past its reads of stage i - 1: refill it
+      issue_x(xs[(d + D - 1) % D], i + D - 1);
+      asm volatile("" ::: "memory");
+      const char* st = xs[d];
+      i32x4_t xf[MT][2];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          xf[mt][ks] = *reinterpret_cast<const i32x4_t*>(st + mt * 2048 + xo[ks]);
+        }
+      }
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
+                       : "+v"(acc[mt]) : "v"(wreg[d][ks]), "v"(xf[mt][ks]));
+        }
+      }
+      issue_w(d, i + D);
+    }
+  }
+  // no DMA may still be writing LDS when the workgroup retires; wait
+  // states between the last MFMA results and the epilogue's reads
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
+               ::: "memory");
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) { asm volatile("" : "+v"(acc[mt])); }
+
+  const int n = n0 + 4 * g;
+  if (n >= P.n) { return; }
+  uint2 bb = make_uint2(0u, 0u);
+  if (S == 1 && P.bias != nullptr) { bb = *reinterpret_cast<const uint2*>(P.bias + n); }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = mt * 16 + r;
+    if (m >= P.rows) { continue; }
+    if (S == 1) {
+      skinny_store(P, m, n, acc[mt], bb);
+    } else {
+      float* ws = B.ws + P.ws_off + (size_t)share * P.rows * P.n;
+      *reinterpret_cast<f32x4_t*>(ws + (size_t)m * P.n + n) = acc[mt];
+    }
+  }
+}
+
+template <int MT, int D>
+__global__ __launch_bounds__(256) void
+skinny_lds_kernel(const SkinnyBatch B)
+{
+  constexpr int kStage = MT * 16 * 128;
+  __shared__ __attribute__((aligned(1024))) char xs0[kStage];
+  __shared__ __attribute__((aligned(1024))) char xs1[kStage];
+  __shared__ __attribute__((aligned(1024))) char xs2[kStage];
+  __shared__ __attribute__((aligned(1024))) char xs3[kStage];
+  if constexpr (D == 4) {
+    char* const xs[4] = {xs0, xs1, xs2, xs3};
+    skinny_lds_tile<MT, 4>(B, xs);
+  } else {
+    static_assert(D == 8, "ring of 4 or 8 stages");
+    __shared__ __attribute__((aligned(1024))) char xs4[kStage];
+    __shared__ __attribute__((aligned(1024))) char xs5[kStage];
+    __shared__ __attribute__((aligned(1024))) char xs6[kStage];
+    __shared__ __attribute__((aligned(1024))) char xs7[kStage];
+    char* const xs[8] = {xs0, xs1, xs2, xs3, xs4, xs5, xs6, xs7};
+    skinny_lds_tile<MT, 8>(B, xs);
+  }
+}
+
+// Sums the S partial sums of every output in share order, adds the bias
+// and rounds to bf16: one thread per 4 columns of a row; blockIdx.y is the
+// problem.
+__global__ __launch_bounds__(256) void
+skinny_reduce_kernel(const SkinnyBatch B)
+{
+  const SkinnyProblem& P = B.p[blockIdx.y];
+  const int q = P.n / 4;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)P.rows * q) { return; }
+  const int m = (int)(idx / q);
+  const int n = (int)(idx - (int64_t)m * q) * 4;
+  const size_t plane = (size_t)P.rows * P.n;
+  const float* ws = B.ws + P.ws_off + (size_t)m * P.n + n;
+  f32x4_t v = *reinterpret_cast<const f32x4_t*>(ws);
+  for (int sh = 1; sh < B.split; ++sh) {
+    v += *reinterpret_cast<const f32x4_t*>(ws + sh * plane);
+  }
+  uint2 bb = make_uint2(0u, 0u);
+  if (P.bias != nullptr) { bb = *reinterpret_cast<const uint2*>(P.bias + n); }
+  skinny_store(P, m, n, v, bb);
+}
+
 // ---- row gather / scatter for per-token routing ------------------------
 template <bool kScatter>
 __global__ __launch_bounds__(256) void
@@ -2083,6 +2436,44 @@ launch_gemm(const GemmBatch& b, int cus, hipStream_t s, const GemmEvents& ev)
                      dim3(256), 0, s, b);
   return hipGetLastError();
 }
+
+template <class F>
+hipError_t
+launch_skinny(F kernel, const SkinnyBatch& b, hipStream_t s, const GemmEvents& ev)
+{
+  hipError_t e = hipSuccess;
+  if (ev.before != nullptr) { e = hipEventRecord(ev.before, s); }
+  if (e != hipSuccess) { return e; }
+  hipLaunchKernelGGL(kernel, dim3(b.total_cb * b.split), dim3(256), 0, s, b);
+  e = hipGetLastError();
+  if (e == hipSuccess && ev.after != nullptr) { e = hipEventRecord(ev.after, s); }
+  if (e != hipSuccess || b.split <= 1) { return e; }
+  int64_t most = 0;
+  for (int i = 0; i < b.nprob; ++i) {
+    most = std::max<int64_t>(most, (int64_t)b.p[i].rows * (b.p[i].n / 4));
+  }
+  hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)((most + 255) / 256), b.nprob),
+                     dim3(256), 0, s, b);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t
+launch_skinny_bf16(const SkinnyBatch& b, hipStream_t s, const GemmEvents& ev)
+{
+  if (b.total_cb <= 0 || b.max_rows <= 0) { return hipSuccess; }
+  if (b.max_rows > kSkinnyMaxRows || b.kbytes % 128 != 0 ||
+      b.cols != skinny_cols(b.max_rows)) {
+    return hipErrorInvalidValue;
+  }
+  if (b.max_rows <= 16) { return launch_skinny(skinny_reg_kernel<1>, b, s, ev); }
+  if (b.max_rows <= 32) { return launch_skinny(skinny_lds_kernel<2, 8>, b, s, ev); }
+  if (b.max_rows <= 64) { return launch_skinny(skinny_lds_kernel<4, 8>, b, s, ev); }
+  return launch_skinny(skinny_lds_kernel<8, 4>, b, s, ev);
+}
+
+namespace {
 
 template <class Mma, Epi E>
 hipError_t
@@ -2411,6 +2802,11 @@ kernels_loadable()
       reinterpret_cast<const void*>(&f32_to_bf16_kernel),
       reinterpret_cast<const void*>(&gather_rows_kernel<true>),
       reinterpret_cast<const void*>(&gather_rows_kernel<false>),
+      reinterpret_cast<const void*>(&skinny_reg_kernel<1>),
+      reinterpret_cast<const void*>(&skinny_lds_kernel<2, 8>),
+      reinterpret_cast<const void*>(&skinny_lds_kernel<4, 8>),
+      reinterpret_cast<const void*>(&skinny_lds_kernel<8, 4>),
+      reinterpret_cast<const void*>(&skinny_reduce_kernel),
   };
   for (const void* f : fns) {
     hipFuncAttributes a;
