@@ -483,11 +483,13 @@ def ab_compare(torch, u15h, ops, spec, model, io, args, want_i8):
 def m_sweep(torch, u15h, ops, gen, rounds):
     """The three routes of one projection (K=4096, N=6144, the reference's
     sweep shape, src/u15-metal-ops.h:436-448, 486-502) over row counts:
-    dense bf16 (u15h_linear), the w8g64 pack dequantised once then the
-    dense GEMM (u15h_linear_q), and the int8 GEMM on pre-quantised weights
-    (activation quantiser included).  Each route rotates enough weight
-    copies to exceed twice the Infinity Cache; medians of interleaved
-    rounds."""
+    dense bf16 (u15h_linear), the w8g64 pack through u15h_linear_q (read
+    directly below the 96-row floor, dequantised once then the dense GEMM
+    from it on), and the int8 GEMM on pre-quantised weights (activation
+    quantiser included).  Each route rotates enough weight copies to exceed
+    twice the Infinity Cache; medians of interleaved rounds.  GB/s counts
+    the bf16 weight bytes (N x K x 2; N x K for int8) whatever the route
+    reads."""
     K, N, G = 4096, 6144, 64
     copies = math.ceil(2 * MALL_BYTES / (N * K * 2)) + 1
     ws, packs, q8 = [], [], []
@@ -518,7 +520,7 @@ def m_sweep(torch, u15h, ops, gen, rounds):
         def dense():
             ops.linear(x, ws[nxt()], None, y, M, K, N)
 
-        def deq_once():
+        def lin_q():
             ops.linear_q(x, packs[nxt()], None, y, M, K, N)
 
         def int8():
@@ -526,7 +528,7 @@ def m_sweep(torch, u15h, ops, gen, rounds):
             ops.quant_rows_i8(x, xq, sx)
             ops.mot_gemm_i8(xq, sx, 0, M, K, [dict(wq_gen=wq, sw_gen=sw, y=y)])
         got = interleaved(torch, {"dense": [dense] * copies,
-                                  "dequant_once": [deq_once] * copies,
+                                  "linear_q": [lin_q] * copies,
                                   "int8": [int8] * copies}, 1, rounds)
         row = {"M": M}
         for name, g in got.items():
@@ -534,8 +536,9 @@ def m_sweep(torch, u15h, ops, gen, rounds):
             wbytes = N * K * (1 if name == "int8" else 2)
             row[name] = {"us_per_call": round(us, 2),
                          "weight_GBps": round(wbytes / (us * 1e-6) / 1e9, 1)}
-        row["dequant_once_over_dense"] = round(row["dequant_once"]["us_per_call"]
-                                               / row["dense"]["us_per_call"], 3)
+        row["linear_q_route"] = "direct" if M < 96 else "dequant_once"
+        row["linear_q_over_dense"] = round(row["linear_q"]["us_per_call"]
+                                           / row["dense"]["us_per_call"], 3)
         rows.append(row)
     return {"m_sweep": {"K": K, "N": N, "pack": "w8g64", "weight_copies": copies,
                         "rows": rows}}

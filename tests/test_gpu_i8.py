@@ -300,6 +300,8 @@ def test_linear_q_int8_interception(ops):
         ops.linear_q(x, qw, None, y_q, Mbig, K, N)
         small = torch.empty(8, N, dtype=torch.bfloat16, device="cuda")
         ops.linear_q(x[:8], qw, None, small, 8, K, N)
+        small_dense = torch.empty_like(small)
+        ops.linear(x[:8], wd_dev, None, small_dense, 8, K, N)
         torch.cuda.synchronize()
         xq, sx = quant_gpu(ops, xb)
         wq, sw = quant_gpu(ops, wd)
@@ -311,7 +313,8 @@ def test_linear_q_int8_interception(ops):
         assert torch.equal(y_q.cpu(), y_ref.cpu())
         assert torch.equal(y_q.cpu(), y_lin.cpu())
         assert not torch.equal(y_q.cpu(), y_dense.cpu())
-        assert torch.equal(small.cpu(), y_dense[:8].cpu())   # declined: dense
+        # declined (below the int8 floor): the dense route on the expansion
+        assert torch.equal(small.cpu(), small_dense.cpu())
         # the int32 accumulators behind it are the oracle's, exactly
         qo, so = oracle.quant_rows_i8(wd)
         assert np.array_equal(wq.cpu().numpy(), qo)

@@ -1,12 +1,14 @@
 """The skinny GEMM route: a bf16 batch whose problems all have at most 128
-rows and K a multiple of 64 runs on skinny_gemm_kernel (64 output columns
-per workgroup, weights streamed into registers, K shares summed in order
-by skinny_reduce_kernel).  Checked against the oracle at the reference's
-bars (max-rel <= 1e-2, rel-L2 < 4e-3, tests/u15-kernels-test.cc:55) and
-against the tiled GEMM of a context built with U15H_SKINNY=0, over the
-share counts the planner picks (1 to 16), the four row-group builds
-(<= 16, 32, 64, 128 rows), column counts that leave waves or lanes of a
-block past N, bias, and grouped und + gen batches."""
+rows and K a multiple of 64 runs on skinny_reg_kernel (<= 16 rows, 16
+output columns per workgroup) or skinny_lds_kernel (64 columns), weights
+streamed into registers, K shares summed in order by skinny_reduce_kernel.
+Checked against the oracle at the reference's bars (max-rel <= 1e-2,
+rel-L2 < 4e-3, tests/u15-kernels-test.cc:55) and against the tiled GEMM of
+a context built with U15H_SKINNY=0, over the share counts the planner
+picks (1 to 16), the four row-group builds (<= 16, 32, 64, 128 rows),
+column counts that leave waves or lanes of a block past N, bias, and
+grouped und + gen batches; and u15h_linear_q's direct route below the row
+floor, which reads 4- and 8-bit affine packs in the same kernels."""
 import os
 
 import numpy as np
@@ -149,3 +151,37 @@ def test_skinny_repeat_is_bit_identical(ops):
     ops.linear(x, w, None, y2, M, K, N)
     torch.cuda.synchronize()
     assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+
+
+def _pack_dev(codes, sc, bi, bits, group):
+    return (torch.from_numpy(np.ascontiguousarray(codes, np.uint32).view(np.int32)).cuda(),
+            dev_bf16(sc), dev_bf16(bi), bits, group)
+
+
+@pytest.mark.parametrize("bits,group", [(8, 64), (8, 32), (4, 64), (4, 32)])
+@pytest.mark.parametrize("M", [1, 16, 17, 64, 95, 96])
+def test_linear_q_direct_route(ops, bits, group, M):
+    """Below the row floor (96, the reference's _mma_q_min_m) u15h_linear_q
+    reads the affine pack directly (the reference's steel qmm route,
+    src/u15-metal-ops.cc:402-431), dequantising in registers to the
+    expansion's bf16 weights: bit-equal to u15h_linear on the expansion
+    (which at these rows runs the same skinny kernel), and within the bars
+    of the oracle.  At 96 rows it is dequant-once + the dense route."""
+    K, N = 2048, 328
+    w = oracle.randn_mt(bits * 100 + group + M, N * K, 0.05).reshape(N, K)
+    codes, sc, bi, _ = oracle.pack_affine(w, bits, group)
+    wd = oracle.dequant_affine(codes, sc, bi, bits, group, K)
+    rng = np.random.default_rng(M * 11 + bits)
+    xb = rand_bf16_bits(rng, (M, K))
+    bb = rand_bf16_bits(rng, (N,), 0.5)
+    x, b = dev_bf16(xb), dev_bf16(bb)
+    y = torch.full((M, N), 7.0, dtype=torch.bfloat16, device="cuda")
+    y2 = torch.empty_like(y)
+    ops.linear_q(x, _pack_dev(codes, sc, bi, bits, group), b, y, M, K, N)
+    ops.linear(x, dev_bf16(wd), b, y2, M, K, N)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
+    rows = np.unique(np.array([0, M // 2, M - 1], np.int32))
+    ref = oracle.linear_bf16(xb, wd, bb, row_ids=rows)
+    a = host_f32(y)[rows]
+    assert max_rel(a, ref) <= MAX_REL and rel_l2(a, ref) < REF_BAR

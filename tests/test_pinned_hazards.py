@@ -65,11 +65,12 @@ def kernels():
 def test_every_epilogue_has_a_pinned_kernel(kernels):
     # 4-wave GEMM: bf16, SwiGLU, int32 and dequant epilogues, 256 MFMAs
     # each; skinny GEMM: the four row-group builds (register kernel for 16
-    # rows, LDS kernel for 32, 64 and 128), 16 MFMAs per 16 rows and
-    # unrolled K-block (2 k-steps), 8 blocks unrolled but 4 at 128 rows
+    # rows, LDS kernel for 32, 64 and 128) for bf16 weights and 4- and
+    # 8-bit packs, 16 MFMAs per 16 rows and unrolled K-block (2 k-steps),
+    # 8 blocks unrolled but 4 at 128 rows
     four = [n for n in kernels if "mot_gemm_kernel" in n]
     skinny = [n for n in kernels if "skinny_" in n]
-    assert len(four) == 4 and len(skinny) == 4
+    assert len(four) == 4 and len(skinny) == 12
     for n in four:
         assert sum(1 for s in kernels[n] if s.startswith("v_mfma")) == 256
     for n in skinny:

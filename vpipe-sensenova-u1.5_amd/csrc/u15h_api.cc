@@ -24,6 +24,9 @@ struct u15h_ctx {
   bool split_on = true;      // env U15H_SPLIT=0 turns the split-K tail off
   // env U15H_SKINNY=0 keeps batches of <= 128-row problems on the tiled GEMM
   bool skinny_on = true;
+  // u15h_linear_q below this many rows reads the pack directly (the
+  // reference's _mma_q_min_m, u15-metal-ops.h:502; env U15H_Q_MIN_M)
+  int q_min_m = 96;
   // GEMM kernel build: 8 or 4 waves per workgroup (env U15H_WAVES) and the
   // 8-wave build's MFMA shape (env U15H_MFMA16).
   u15h::GemmShape gemm = {8, 0, 1};
@@ -231,12 +234,18 @@ skinny_fits(const u15h_ctx* ctx, const GemmBatch& b)
 // scratch); a batch whose partials would not fit takes fewer shares.
 u15h_status
 skinny_launch(u15h_ctx* ctx, const GemmBatch& b, hipStream_t s, bool noalloc,
-              const u15h::GemmEvents& ev)
+              const u15h::GemmEvents& ev, const u15h_qweight* q = nullptr)
 {
   u15h::SkinnyBatch k;
   std::memset(&k, 0, sizeof k);
   k.kbytes = b.kbytes;
   k.nprob = b.nprob;
+  if (q != nullptr) {         // one problem whose w is the pack's codes
+    k.qbits = q->bits;
+    k.qgroup = q->group;
+    k.p[0].qs = static_cast<const uint16_t*>(q->scales);
+    k.p[0].qb = static_cast<const uint16_t*>(q->biases);
+  }
   for (int i = 0; i < b.nprob; ++i) { k.max_rows = std::max(k.max_rows, b.p[i].rows); }
   k.cols = u15h::skinny_cols(k.max_rows);
   for (int i = 0; i < b.nprob; ++i) {
@@ -471,6 +480,7 @@ u15h_create(int device, u15h_ctx** out)
   ctx->num_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
   ctx->split_on = env_int("U15H_SPLIT", 1) != 0;
   ctx->skinny_on = env_int("U15H_SKINNY", 1) != 0;
+  ctx->q_min_m = std::max(0, std::min(u15h::kSkinnyMaxRows + 1, env_int("U15H_Q_MIN_M", 96)));
   ctx->gemm.waves = env_int("U15H_WAVES", 8) == 4 ? 4 : 8;
   ctx->gemm.cus = env_int("U15H_PERSIST", 1) != 0 ? ctx->num_cu : 0;
   ctx->gemm.mfma16 = std::max(-1, std::min(1, env_int("U15H_MFMA16", 1)));
@@ -906,6 +916,19 @@ u15h_linear_q(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
   if (x == nullptr || y == nullptr || !aligned16(x) || !aligned16(y) ||
       (bias != nullptr && !aligned16(bias))) {
     return fail(ctx, U15H_EINVAL, "x/y null, or x/y/bias misaligned");
+  }
+  if ((st = bind_device(ctx)) != U15H_OK) { return st; }
+  // Below the row floor the pack is read directly, as the reference's
+  // steel qmm does (u15-metal-ops.cc:402-431): the skinny kernel
+  // dequantises each weight in registers to exactly the expansion's bf16
+  // value, so the product equals u15h_linear on the expansion bit for bit.
+  if (M < ctx->q_min_m) {
+    GemmBatch b = empty_batch(K * 2);
+    add_problem(b, x, w->codes, nullptr, y, bias, nullptr, nullptr, M, N, N,
+                u15h::tile_cols(Epi::kBf16));
+    if (skinny_fits(ctx, b)) {
+      return skinny_launch(ctx, b, as_stream(stream), false, take_profile_event(ctx), w);
+    }
   }
   if ((st = ensure_deq_scratch(ctx, stream, (size_t)N * K * 2)) != U15H_OK) {
     return st;

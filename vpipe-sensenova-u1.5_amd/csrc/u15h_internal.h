@@ -105,7 +105,9 @@ constexpr int kSkinnyMaxRows = 128;
 constexpr int skinny_cols(int max_rows) { return max_rows <= 16 ? 16 : 64; }
 struct SkinnyProblem {
   const void*     a;      // activation rows [rows][K] (bf16)
-  const void*     w;      // weight rows [n][K] (bf16)
+  const void*     w;      // weight rows [n][K] (bf16), or the pack's codes
+  const uint16_t* qs;     // affine pack: scales bf16 [n][K / group]
+  const uint16_t* qb;     // affine pack: biases bf16 [n][K / group]
   void*           y;      // output rows [rows][ldy] (bf16)
   const uint16_t* bias;   // bf16 [n] or null
   int rows;
@@ -122,6 +124,8 @@ struct SkinnyBatch {
   int cols;               // output columns per block (skinny_cols)
   int total_cb;           // column blocks over all problems
   int max_rows;           // largest problem (picks the kernel build)
+  int qbits;              // 0: bf16 weights; 4 or 8: affine-quantized pack
+  int qgroup;             // the pack's group (32 or 64)
   float* ws;              // partial sums when split > 1
 };
 // Floats of partial-sum workspace a skinny batch needs.
@@ -134,6 +138,8 @@ inline size_t skinny_ws_floats(const SkinnyBatch& b)
   }
   return f;
 }
+// The skinny kernels: bf16 weights, or (qbits 4 / 8) an affine-quantized
+// pack dequantised in registers to the expansion's bf16 weights.
 hipError_t launch_skinny_bf16(const SkinnyBatch& b, hipStream_t s,
                               const GemmEvents& ev);
 hipError_t launch_gemm_i8(const GemmBatch& b, Epi epi, const GemmShape& g,

@@ -2070,6 +2070,132 @@ transpose_rows_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ d
 // MFMA, the last results before the epilogue reads them).
 constexpr int kSkDepth = 8;    // K-blocks in flight per wave
 
+// One wave's weight fragments of a K-block: lane (g, r) holds row r,
+// elements [16g, 16g + 16).  QB = 0: bf16 rows, two 16-byte loads.  QB = 4
+// or 8: an affine-quantized pack (codes [n][K * QB / 32] u32, scale and
+// bias bf16 [n][K / group]): the lane's 16 codes (one 16- or 8-byte load)
+// and its group's scale and bias, dequantised when the MFMA takes them as
+// w = bf16_rne(scale * code + bias) (a multiply, then an add) -- the
+// bf16 weight the dequant-once expansion writes, bit for bit.
+template <int QB>
+struct SkW {
+  i32x4_t c;
+  uint32_t s, b;
+};
+template <>
+struct SkW<0> {
+  i32x4_t v[2];
+};
+
+// Per-lane load parameters of a wave's 16 weight rows.
+struct SkWSrc {
+  __amdgpu_buffer_rsrc_t w;     // bf16 rows or codes, rows [n0, n0 + 16)
+  __amdgpu_buffer_rsrc_t qs;    // scales of those rows (QB > 0)
+  __amdgpu_buffer_rsrc_t qb;    // biases of those rows (QB > 0)
+  int wv;                       // the lane's byte offset in w (K-block 0)
+  int sv;                       // the lane's byte offset in qs / qb
+};
+
+template <int QB>
+__device__ __forceinline__ SkWSrc
+sk_wsrc(const SkinnyBatch& B, const SkinnyProblem& P, int n0, int lane)
+{
+  const int g = lane >> 4, r = lane & 15;
+  const int rows = max(0, min(16, P.n - n0));       // rows past n read zero
+  const int nr = min(n0, P.n);
+  SkWSrc d;
+  if constexpr (QB == 0) {
+    d.w = make_rsrc(static_cast<const char*>(P.w) + (size_t)nr * B.kbytes,
+                    rows * B.kbytes);
+    d.wv = r * B.kbytes + g * 32;
+    d.qs = d.qb = d.w;
+    d.sv = 0;
+  } else {
+    const int K = B.kbytes / 2;
+    const int cpitch = K * QB / 8;                   // code bytes per row
+    const int spitch = K / B.qgroup * 2;             // scale bytes per row
+    d.w = make_rsrc(static_cast<const char*>(P.w) + (size_t)nr * cpitch, rows * cpitch);
+    d.qs = make_rsrc(reinterpret_cast<const char*>(P.qs) + (size_t)nr * spitch, rows * spitch);
+    d.qb = make_rsrc(reinterpret_cast<const char*>(P.qb) + (size_t)nr * spitch, rows * spitch);
+    d.wv = r * cpitch + g * 16 * QB / 8;
+    d.sv = r * spitch + (B.qgroup == 32 ? (g >> 1) * 2 : 0);
+  }
+  return d;
+}
+
+// Loads K-block kb (oob: an offset past every row, zeros).
+template <int QB>
+__device__ __forceinline__ void
+sk_load_w(SkW<QB>& d, const SkWSrc& src, int kb, int oob, int qgroup)
+{
+  if constexpr (QB == 0) {
+    const int ko = __builtin_amdgcn_readfirstlane(kb * 128);
+    d.v[0] = __builtin_amdgcn_raw_buffer_load_b128(src.w, src.wv + oob, ko, 0);
+    d.v[1] = __builtin_amdgcn_raw_buffer_load_b128(src.w, src.wv + 16 + oob, ko, 0);
+  } else {
+    const int ko = __builtin_amdgcn_readfirstlane(kb * 64 * QB / 8);
+    if constexpr (QB == 8) {
+      d.c = __builtin_amdgcn_raw_buffer_load_b128(src.w, src.wv + oob, ko, 0);
+    } else {
+      const auto c2 = __builtin_amdgcn_raw_buffer_load_b64(src.w, src.wv + oob, ko, 0);
+      d.c = i32x4_t{(int)c2[0], (int)c2[1], 0, 0};
+    }
+    const int so = __builtin_amdgcn_readfirstlane(kb * (64 / qgroup) * 2);
+    d.s = __builtin_amdgcn_raw_buffer_load_b16(src.qs, src.sv + oob, so, 0);
+    d.b = __builtin_amdgcn_raw_buffer_load_b16(src.qb, src.sv + oob, so, 0);
+  }
+}
+
+// The bf16 A fragment of k-step ks (elements [16g + 8ks, 16g + 8ks + 8)).
+template <int QB>
+__device__ __forceinline__ i32x4_t
+sk_frag(const SkW<QB>& d, int ks)
+{
+  if constexpr (QB == 0) {
+    return d.v[ks];
+  } else {
+    const float sc = bf16_to_f32(d.s & 0xffffu);
+    const float bi = bf16_to_f32(d.b & 0xffffu);
+    constexpr uint32_t kMask = (1u << QB) - 1u;
+    uint32_t codes[2];
+    if constexpr (QB == 8) {
+      codes[0] = (uint32_t)d.c[2 * ks];
+      codes[1] = (uint32_t)d.c[2 * ks + 1];
+    }
+    i32x4_t f;
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      uint32_t c0, c1;
+      if constexpr (QB == 8) {
+        c0 = (codes[e >> 2] >> ((e & 3) * 8)) & kMask;
+        c1 = (codes[e >> 2] >> (((e & 3) + 1) * 8)) & kMask;
+      } else {
+        c0 = ((uint32_t)d.c[ks] >> (e * 4)) & kMask;
+        c1 = ((uint32_t)d.c[ks] >> ((e + 1) * 4)) & kMask;
+      }
+      const float v0 = __fadd_rn(__fmul_rn(sc, (float)c0), bi);
+      const float v1 = __fadd_rn(__fmul_rn(sc, (float)c1), bi);
+      f[e >> 1] = (int)(bf16_bits(v0) | (bf16_bits(v1) << 16));
+    }
+    return f;
+  }
+}
+
+// A 16x16x32 bf16 MFMA with its accumulator tied ("+v").  With QB > 0 the
+// A fragment comes from VALU arithmetic just before: two wait states
+// separate that write from the MFMA's read.
+template <int QB>
+__device__ __forceinline__ void
+sk_mfma(f32x4_t& acc, i32x4_t a, i32x4_t b)
+{
+  if constexpr (QB == 0) {
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
+  } else {
+    asm volatile("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
+                 : "+v"(acc) : "v"(a), "v"(b));
+  }
+}
+
 // Bias, rounding and store of 4 output columns n..n+3 of row m.
 __device__ __forceinline__ void
 skinny_store(const SkinnyProblem& P, int m, int n, f32x4_t v, uint2 bb)
@@ -2099,7 +2225,7 @@ skinny_problem(const SkinnyBatch& B, int cbg)
 // both operands straight into registers (the activation rows are few and
 // L2-resident), with no barrier until the four partial sums meet in LDS,
 // where wave 0 adds them in wave order.
-template <int MT>
+template <int MT, int QB>
 __global__ __launch_bounds__(256) void
 skinny_reg_kernel(const SkinnyBatch B)
 {
@@ -2120,20 +2246,17 @@ skinny_reg_kernel(const SkinnyBatch B)
 
   // weight rows [n0, n0 + 16) and activation rows [0, rows); rows past
   // either read as zero
-  const __amdgpu_buffer_rsrc_t wr = make_rsrc(
-      static_cast<const char*>(P.w) + (size_t)n0 * kbytes,
-      max(0, min(16, P.n - n0)) * kbytes);
+  const SkWSrc wsrc = sk_wsrc<QB>(B, P, n0, lane);
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(P.a, P.rows * kbytes);
   const int lv = r * kbytes + g * 32;               // row r, bytes 32g..
 
-  i32x4_t wreg[kSkDepth][2];
+  SkW<QB> wreg[kSkDepth];
   i32x4_t xreg[kSkDepth][MT][2];
   auto issue = [&](int slot, int j) {
     const int oob = j < nw ? 0 : kOobOffset;        // past the share: zeros
-    const int ko = __builtin_amdgcn_readfirstlane(
-        (kb0 + wave + 4 * min(j, max(nw - 1, 0))) * 128);
-    wreg[slot][0] = __builtin_amdgcn_raw_buffer_load_b128(wr, lv + oob, ko, 0);
-    wreg[slot][1] = __builtin_amdgcn_raw_buffer_load_b128(wr, lv + 16 + oob, ko, 0);
+    const int kb = kb0 + wave + 4 * min(j, max(nw - 1, 0));
+    const int ko = __builtin_amdgcn_readfirstlane(kb * 128);
+    sk_load_w<QB>(wreg[slot], wsrc, kb, oob, B.qgroup);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int v = lv + mt * 16 * kbytes + oob;
@@ -2161,11 +2284,9 @@ skinny_reg_kernel(const SkinnyBatch B)
     for (int d = 0; d < kSkDepth; ++d) {
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
+        const i32x4_t wf = sk_frag<QB>(wreg[d], ks);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
-                       : "+v"(acc[mt]) : "v"(wreg[d][ks]), "v"(xreg[d][mt][ks]));
-        }
+        for (int mt = 0; mt < MT; ++mt) { sk_mfma<QB>(acc[mt], wf, xreg[d][mt][ks]); }
       }
       asm volatile("" ::: "memory");
       issue(d, j0 + d + kSkDepth);
@@ -2207,7 +2328,7 @@ skinny_reg_kernel(const SkinnyBatch B)
 // deep as the weight lead, which a shallower ring would cut short: 8
 // stages (64 KiB) up to 64 rows, 4 (64 KiB) up to 128, so that two
 // workgroups fit a CU either way.
-template <int MT, int D>
+template <int MT, int D, int QB>
 __device__ __forceinline__ void
 skinny_lds_tile(const SkinnyBatch& B, char* const (&xs)[D])
 {
@@ -2226,11 +2347,7 @@ skinny_lds_tile(const SkinnyBatch& B, char* const (&xs)[D])
   const int n0 = (cbg - P.cb_begin) * 64 + wave * 16;
 
   // weight rows [n0, n0 + 16) clipped to n: rows past it read as zero
-  const int wrows = max(0, min(16, P.n - n0));
-  const __amdgpu_buffer_rsrc_t wr = make_rsrc(
-      static_cast<const char*>(P.w) + (size_t)min(n0, P.n) * kbytes,
-      wrows * kbytes);
-  const int wv = r * kbytes + g * 32;
+  const SkWSrc wsrc = sk_wsrc<QB>(B, P, n0, lane);
   // activation rows [0, rows): rows past them read as zero
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(P.a, P.rows * kbytes);
   // DMA: instruction j of wave w fills 16-byte stage slots
@@ -2260,12 +2377,10 @@ skinny_lds_tile(const SkinnyBatch& B, char* const (&xs)[D])
           16, xv[j] + oob, ko, 0, 0);
     }
   };
-  i32x4_t wreg[D][2];
+  SkW<QB> wreg[D];
   auto issue_w = [&](int slot, int i) {
     const int oob = i < nk ? 0 : kOobOffset;
-    const int ko = __builtin_amdgcn_readfirstlane((kb0 + min(i, nk - 1)) * 128);
-    wreg[slot][0] = __builtin_amdgcn_raw_buffer_load_b128(wr, wv + oob, ko, 0);
-    wreg[slot][1] = __builtin_amdgcn_raw_buffer_load_b128(wr, wv + 16 + oob, ko, 0);
+    sk_load_w<QB>(wreg[slot], wsrc, kb0 + min(i, nk - 1), oob, B.qgroup);
   };
 
   f32x4_t acc[MT];
@@ -2291,7 +2406,8 @@ skinny_lds_tile(const SkinnyBatch& B, char* const (&xs)[D])
   // most the loads issued after it may be in flight -- the weight loads
   // of its own iteration and D - 2 later iterations' x and weight
   // loads (earlier in the prologue, where more follow it).
-  constexpr int kAfterX = 2 + (D - 2) * (kXInst + 2);
+  constexpr int kWLoads = QB == 0 ? 2 : 3;          // per K-block
+  constexpr int kAfterX = kWLoads + (D - 2) * (kXInst + kWLoads);
   static_assert(kAfterX < 64, "vmcnt holds at most 63");
   const int nk_pad = (nk + D - 1) / D * D;
   for (int i0 = 0; i0 < nk_pad; i0 += D) {
@@ -2315,11 +2431,9 @@ skinny_lds_tile(const SkinnyBatch& B, char* const (&xs)[D])
       }
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
+        const i32x4_t wf = sk_frag<QB>(wreg[d], ks);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
-                       : "+v"(acc[mt]) : "v"(wreg[d][ks]), "v"(xf[mt][ks]));
-        }
+        for (int mt = 0; mt < MT; ++mt) { sk_mfma<QB>(acc[mt], wf, xf[mt][ks]); }
       }
       issue_w(d, i + D);
     }
@@ -2348,7 +2462,7 @@ skinny_lds_tile(const SkinnyBatch& B, char* const (&xs)[D])
   }
 }
 
-template <int MT, int D>
+template <int MT, int D, int QB>
 __global__ __launch_bounds__(256) void
 skinny_lds_kernel(const SkinnyBatch B)
 {
@@ -2359,7 +2473,7 @@ skinny_lds_kernel(const SkinnyBatch B)
   __shared__ __attribute__((aligned(1024))) char xs3[kStage];
   if constexpr (D == 4) {
     char* const xs[4] = {xs0, xs1, xs2, xs3};
-    skinny_lds_tile<MT, 4>(B, xs);
+    skinny_lds_tile<MT, 4, QB>(B, xs);
   } else {
     static_assert(D == 8, "ring of 4 or 8 stages");
     __shared__ __attribute__((aligned(1024))) char xs4[kStage];
@@ -2367,7 +2481,7 @@ skinny_lds_kernel(const SkinnyBatch B)
     __shared__ __attribute__((aligned(1024))) char xs6[kStage];
     __shared__ __attribute__((aligned(1024))) char xs7[kStage];
     char* const xs[8] = {xs0, xs1, xs2, xs3, xs4, xs5, xs6, xs7};
-    skinny_lds_tile<MT, 8>(B, xs);
+    skinny_lds_tile<MT, 8, QB>(B, xs);
   }
 }
 
@@ -2457,6 +2571,16 @@ launch_skinny(F kernel, const SkinnyBatch& b, hipStream_t s, const GemmEvents& e
   return hipGetLastError();
 }
 
+template <int QB>
+hipError_t
+launch_skinny_q(const SkinnyBatch& b, hipStream_t s, const GemmEvents& ev)
+{
+  if (b.max_rows <= 16) { return launch_skinny(skinny_reg_kernel<1, QB>, b, s, ev); }
+  if (b.max_rows <= 32) { return launch_skinny(skinny_lds_kernel<2, 8, QB>, b, s, ev); }
+  if (b.max_rows <= 64) { return launch_skinny(skinny_lds_kernel<4, 8, QB>, b, s, ev); }
+  return launch_skinny(skinny_lds_kernel<8, 4, QB>, b, s, ev);
+}
+
 }  // namespace
 
 hipError_t
@@ -2464,13 +2588,16 @@ launch_skinny_bf16(const SkinnyBatch& b, hipStream_t s, const GemmEvents& ev)
 {
   if (b.total_cb <= 0 || b.max_rows <= 0) { return hipSuccess; }
   if (b.max_rows > kSkinnyMaxRows || b.kbytes % 128 != 0 ||
-      b.cols != skinny_cols(b.max_rows)) {
+      b.cols != skinny_cols(b.max_rows) ||
+      (b.qbits != 0 && b.qgroup != 32 && b.qgroup != 64)) {
     return hipErrorInvalidValue;
   }
-  if (b.max_rows <= 16) { return launch_skinny(skinny_reg_kernel<1>, b, s, ev); }
-  if (b.max_rows <= 32) { return launch_skinny(skinny_lds_kernel<2, 8>, b, s, ev); }
-  if (b.max_rows <= 64) { return launch_skinny(skinny_lds_kernel<4, 8>, b, s, ev); }
-  return launch_skinny(skinny_lds_kernel<8, 4>, b, s, ev);
+  switch (b.qbits) {
+    case 0: return launch_skinny_q<0>(b, s, ev);
+    case 4: return launch_skinny_q<4>(b, s, ev);
+    case 8: return launch_skinny_q<8>(b, s, ev);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 namespace {
@@ -2802,10 +2929,18 @@ kernels_loadable()
       reinterpret_cast<const void*>(&f32_to_bf16_kernel),
       reinterpret_cast<const void*>(&gather_rows_kernel<true>),
       reinterpret_cast<const void*>(&gather_rows_kernel<false>),
-      reinterpret_cast<const void*>(&skinny_reg_kernel<1>),
-      reinterpret_cast<const void*>(&skinny_lds_kernel<2, 8>),
-      reinterpret_cast<const void*>(&skinny_lds_kernel<4, 8>),
-      reinterpret_cast<const void*>(&skinny_lds_kernel<8, 4>),
+      reinterpret_cast<const void*>(&skinny_reg_kernel<1, 0>),
+      reinterpret_cast<const void*>(&skinny_lds_kernel<2, 8, 0>),
+      reinterpret_cast<const void*>(&skinny_lds_kernel<4, 8, 0>),
+      reinterpret_cast<const void*>(&skinny_lds_kernel<8, 4, 0>),
+      reinterpret_cast<const void*>(&skinny_reg_kernel<1, 4>),
+      reinterpret_cast<const void*>(&skinny_lds_kernel<2, 8, 4>),
+      reinterpret_cast<const void*>(&skinny_lds_kernel<4, 8, 4>),
+      reinterpret_cast<const void*>(&skinny_lds_kernel<8, 4, 4>),
+      reinterpret_cast<const void*>(&skinny_reg_kernel<1, 8>),
+      reinterpret_cast<const void*>(&skinny_lds_kernel<2, 8, 8>),
+      reinterpret_cast<const void*>(&skinny_lds_kernel<4, 8, 8>),
+      reinterpret_cast<const void*>(&skinny_lds_kernel<8, 4, 8>),
       reinterpret_cast<const void*>(&skinny_reduce_kernel),
   };
   for (const void* f : fns) {
