@@ -93,7 +93,9 @@ const char* u15h_last_error(const u15h_ctx* ctx);
  * If the int8 tier is on (u15h_enable_i8_gemm) and the shape qualifies
  * (M >= the tier's row floor, K % 128 == 0) the call is served by the int8
  * path with per-call quantisation of both operands -- the interception
- * MetalOps::linear_mma_ makes (src/u15-metal-ops.cc:283-306).
+ * MetalOps::linear_mma_ makes (src/u15-metal-ops.cc:283-306).  At most 128
+ * rows with K % 64 == 0 run a weight-streaming kernel (16 or 64 output
+ * columns per workgroup) instead of the 256 x 256 tiles.
  * Limits: M >= 0, N > 0, K > 0, K % 8 == 0, N % 8 == 0. */
 u15h_status u15h_linear(u15h_ctx* ctx, u15h_stream stream,
                         const u15h_bf16* x, const u15h_bf16* w,
@@ -162,9 +164,15 @@ u15h_status u15h_dequant_affine(u15h_ctx* ctx, u15h_stream stream,
                                 u15h_bf16* w_out);
 
 /* Replaces MetalOps::linear(enc, x, QWeight, bias, y, M, K, N) for a
- * quantized pack (src/u15-metal-ops.cc:359-433): dequant once into the
- * context's grow-only scratch, then u15h_linear's route on the expansion
- * -- including its int8 interception when the tier is on and the shape
+ * quantized pack (src/u15-metal-ops.cc:359-433).  Below the row floor (M <
+ * 96, the reference's _mma_q_min_m, src/u15-metal-ops.h:502; env
+ * U15H_Q_MIN_M) the pack is read directly, as the reference's steel qmm
+ * does (src/u15-metal-ops.cc:402-431): each weight is dequantised in
+ * registers to the expansion's bf16 value, so the result equals
+ * u15h_linear on the expansion bit for bit (K % 64 == 0; other K take the
+ * expansion).  From the floor on: dequant once into the context's
+ * grow-only scratch, then u15h_linear's route on the expansion --
+ * including its int8 interception when the tier is on and the shape
  * qualifies (the reference's linear_mma_q_ re-enters linear_mma_,
  * src/u15-metal-ops.cc:291-300, 393-399). */
 u15h_status u15h_linear_q(u15h_ctx* ctx, u15h_stream stream,
