@@ -135,7 +135,7 @@ COPY_PROBE_BYTES = 1 << 30
 # (layers, m_und, m_gen) -> rocprof traffic summary of that token split
 TRAFFIC_FILES = {
     (1, 128, 4096): REPO / "profiles" / "mot_gemm_bf16_c2_traffic.txt",
-    (1, 128, 0): REPO / "profiles" / "mot_gemm_bf16_und128_traffic.txt",
+    (2, 128, 0): REPO / "profiles" / "mot_gemm_bf16_und128_traffic.txt",
 }
 
 

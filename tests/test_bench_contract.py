@@ -63,7 +63,10 @@ def test_ridge_is_peak_over_hbm():
 
 def test_committed_traffic_figures():
     c2 = bench.measured_traffic(_Args(1, 128, 4096))
-    und = bench.measured_traffic(_Args(1, 128, 0))
+    # the und-only split is profiled as the bench runs it: two layers
+    # rotated (their weights exceed twice the Infinity Cache)
+    assert bench.parse(["--m-und", "128", "--m-gen", "0"]).layers == 2
+    und = bench.measured_traffic(_Args(2, 128, 0))
     assert c2 is not None and und is not None
     # traffic beyond L2 is at least the algorithmic bytes of a launch
     assert c2 >= _layer_bytes(128, 4096) / 4
