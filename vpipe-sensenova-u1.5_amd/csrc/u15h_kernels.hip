@@ -433,7 +433,7 @@ template <class Mma, Epi E, int WN>
 __device__ __forceinline__ void
 gemm_epilogue_staged(const GemmProblem& P, const TileWork& t, int wm, int wn,
                      int lane, const acc_array_t<Mma, WN>& acc,
-                     char* const (&ring)[2])
+                     char* const (&ring)[2], const float* scl)
 {
   constexpr int NW = kBN / WN;
   constexpr int kF = Mma::kF;
@@ -461,14 +461,17 @@ gemm_epilogue_staged(const GemmProblem& P, const TileWork& t, int wm, int wn,
     for (int c = 0; c < kCols; ++c) {
       const int i = c / kGr, g = c % kGr;
       const int n = min(t.col0 + wn * NW + i * kF + g * kGs + lh * 4, P.n - 4);
-      if constexpr (kScaled) { swn[c] = *reinterpret_cast<const float4*>(P.sw + n); }
+      if constexpr (kScaled) {
+        swn[c] = *reinterpret_cast<const float4*>(scl + kBM + wn * NW + i * kF + g * kGs +
+                                                  lh * 4);
+      }
       bia[c] = has_bias ? *reinterpret_cast<const uint2*>(P.bias + n) : uint2{0u, 0u};
     }
   }
   if constexpr (kScaled) {
 #pragma unroll
     for (int j = 0; j < FJ; ++j) {
-      sam[j] = P.sa[min(t.row0 + wm * 128 + j * kF + lr, P.rows - 1)];
+      sam[j] = scl[wm * 128 + j * kF + lr];
     }
   }
   // Every wave is past its last fragment read of the main loop.
@@ -582,7 +585,7 @@ template <class Mma, Epi E, int WN>
 __device__ __forceinline__ void
 gemm_epilogue(const GemmBatch& B, const GemmProblem& P, const TileWork& t,
               int wm, int wn, int lane, const acc_array_t<Mma, WN>& acc,
-              char* const (&ring)[2])
+              char* const (&ring)[2], const float* scl)
 {
   constexpr int NW = kBN / WN;
   constexpr int kF = Mma::kF;
@@ -620,7 +623,7 @@ gemm_epilogue(const GemmBatch& B, const GemmProblem& P, const TileWork& t,
     return;
   }
   if constexpr (E != Epi::kI32) {
-    gemm_epilogue_staged<Mma, E, WN>(P, t, wm, wn, lane_e, acc, ring);
+    gemm_epilogue_staged<Mma, E, WN>(P, t, wm, wn, lane_e, acc, ring, scl);
     return;
   }
 #pragma unroll
@@ -708,7 +711,7 @@ gemm_epilogue(const GemmBatch& B, const GemmProblem& P, const TileWork& t,
 // rows, rides in the SGPR.
 template <class Mma, Epi E, int WN, int KB, int RING>
 __device__ __forceinline__ void
-gemm_tile(const GemmBatch& B, char* const (&ring)[RING], int item)
+gemm_tile(const GemmBatch& B, char* const (&ring)[RING], float* scl, int item)
 {
   constexpr int kWaves = 2 * WN;
   constexpr int NW = kBN / WN;               // weight rows per wave
@@ -957,6 +960,24 @@ gemm_tile(const GemmBatch& B, char* const (&ring)[RING], int item)
   // ---- main loop: a multiple of RING stages; a padding stage (K past the
   // range) reads as zeros and adds exactly 0 to every accumulator --------
   const int nst_pad = (t.nst + RING - 1) / RING * RING;
+  // The dequant epilogue's scales, fetched ahead into LDS: the tile's 256
+  // row scales (wave 0) and 256 column scales (wave 1), 4 bytes per lane
+  // and instruction; entries past the problem read as zeros and scale
+  // outputs that are never stored.  Issued before the stage loads, they
+  // land before stage 0 (loads complete in issue order).
+  if constexpr (E == Epi::kDequantBf16) {
+    if (!t.is_split && wave < 2) {
+      const float* src = wave == 0 ? P.sa + t.row0 : P.sw + t.col0;
+      const int n = wave == 0 ? min(kBM, P.rows - t.row0) : min(kBN, P.n - t.col0);
+      const __amdgpu_buffer_rsrc_t rs = make_rsrc(src, n * 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rs, (__attribute__((address_space(3))) void*)(scl + wave * kBM + i * 64), 4,
+            (i * 64 + lane) * 4, 0, 0, 0);
+      }
+    }
+  }
 #pragma unroll
   for (int r = 0; r < RING; ++r) { issue_loads(ring[r], r); }
   // Stage 0 has landed once at most the later stages' loads are in flight
@@ -1008,7 +1029,7 @@ gemm_tile(const GemmBatch& B, char* const (&ring)[RING], int item)
     }
   }
 
-  gemm_epilogue<Mma, E, WN>(B, P, t, wm, wn, lane, acc, ring);
+  gemm_epilogue<Mma, E, WN>(B, P, t, wm, wn, lane, acc, ring, scl);
 }
 
 // Two 64 KiB stages of 128 bytes of K per row.
@@ -1028,6 +1049,8 @@ mot_gemm_kernel(const GemmBatch B)
   __shared__ __attribute__((aligned(1024))) char lds0[kStage];
   __shared__ __attribute__((aligned(1024))) char lds1[kStage];
   char* const ring[2] = {lds0, lds1};
+  // the dequant epilogue's row and column scales of the current tile
+  __shared__ __attribute__((aligned(16))) float scl[E == Epi::kDequantBf16 ? kBM + kBN : 4];
   const int items = grid_blocks(B);
   const int G = gridDim.x;
   const int b = blockIdx.x;
@@ -1042,7 +1065,7 @@ mot_gemm_kernel(const GemmBatch B)
     } else if (b >= R) {
       break;
     }
-    gemm_tile<Mma, E, WN, kKB, 2>(B, ring, w);
+    gemm_tile<Mma, E, WN, kKB, 2>(B, ring, scl, w);
   }
 }
 
