@@ -67,7 +67,7 @@ def test_every_epilogue_has_a_pinned_kernel(kernels):
     # each; skinny GEMM: the four row-group builds (register kernel for 16
     # rows, LDS kernel for 32, 64 and 128) for bf16 weights and 4- and
     # 8-bit packs, 16 MFMAs per 16 rows and unrolled K-block (2 k-steps),
-    # 8 blocks unrolled but 4 at 128 rows
+    # 2 blocks unrolled in the register kernel, 4 in the LDS kernels
     four = [n for n in kernels if "mot_gemm_kernel" in n]
     skinny = [n for n in kernels if "skinny_" in n]
     assert len(four) == 4 and len(skinny) == 12
@@ -75,7 +75,7 @@ def test_every_epilogue_has_a_pinned_kernel(kernels):
         assert sum(1 for s in kernels[n] if s.startswith("v_mfma")) == 256
     for n in skinny:
         mt = int(re.search(r"skinny_(?:reg|lds)_kernelILi(\d+)E", n).group(1))
-        depth = 4 if mt == 8 else 8
+        depth = 2 if mt == 1 else 4     # register kernel: kSkDepth; LDS kernels: D
         assert sum(1 for s in kernels[n] if s.startswith("v_mfma")) == 2 * mt * depth
 
 

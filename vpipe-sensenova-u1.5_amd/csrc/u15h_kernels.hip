@@ -2086,8 +2086,13 @@ transpose_rows_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ d
 // with columns 4g .. 4g + 3 of its 16 for row r of each 16-row group.
 //
 // Loads of one wave return in issue order, so a wave can only run as far
-// ahead of its data as its earliest outstanding load allows; both kernels
-// keep every operand kSkDepth K-blocks ahead.
+// ahead of its data as its earliest outstanding load allows.  The register
+// kernel keeps its operands kSkDepth K-blocks ahead, the LDS kernels D.
+// Deeper is not faster: with N = 6144, K = 4096 and 12 rotated weight
+// copies a call at 1 / 8 / 16 rows took 13.5 / 15.4 / 18.1 us at depth 2
+// against 15.8 / 17.4 / 19.8 at 8 (the extra requests in flight only
+// queue), and the LDS kernels 17.7 / 20.6 us at 32 / 64 rows with D = 4
+// against 18.2 / 21.4 with D = 8.
 //
 // The accumulators are tied to their MFMAs (inline asm "+v"): the
 // builtin's untied 16x16 result makes the compiler rotate them through
@@ -2095,7 +2100,7 @@ transpose_rows_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ d
 // reads around it keep their place; the hazards the compiler's tracking
 // would cover are covered with wait states (the zeroing before the first
 // MFMA, the last results before the epilogue reads them).
-constexpr int kSkDepth = 8;    // K-blocks in flight per wave
+constexpr int kSkDepth = 2;    // K-blocks in flight per wave
 
 // One wave's weight fragments of a K-block: lane (g, r) holds row r,
 // elements [16g, 16g + 16).  QB = 0: bf16 rows, two 16-byte loads.  QB = 4
@@ -2603,8 +2608,8 @@ hipError_t
 launch_skinny_q(const SkinnyBatch& b, hipStream_t s, const GemmEvents& ev)
 {
   if (b.max_rows <= 16) { return launch_skinny(skinny_reg_kernel<1, QB>, b, s, ev); }
-  if (b.max_rows <= 32) { return launch_skinny(skinny_lds_kernel<2, 8, QB>, b, s, ev); }
-  if (b.max_rows <= 64) { return launch_skinny(skinny_lds_kernel<4, 8, QB>, b, s, ev); }
+  if (b.max_rows <= 32) { return launch_skinny(skinny_lds_kernel<2, 4, QB>, b, s, ev); }
+  if (b.max_rows <= 64) { return launch_skinny(skinny_lds_kernel<4, 4, QB>, b, s, ev); }
   return launch_skinny(skinny_lds_kernel<8, 4, QB>, b, s, ev);
 }
 
@@ -2957,16 +2962,16 @@ kernels_loadable()
       reinterpret_cast<const void*>(&gather_rows_kernel<true>),
       reinterpret_cast<const void*>(&gather_rows_kernel<false>),
       reinterpret_cast<const void*>(&skinny_reg_kernel<1, 0>),
-      reinterpret_cast<const void*>(&skinny_lds_kernel<2, 8, 0>),
-      reinterpret_cast<const void*>(&skinny_lds_kernel<4, 8, 0>),
+      reinterpret_cast<const void*>(&skinny_lds_kernel<2, 4, 0>),
+      reinterpret_cast<const void*>(&skinny_lds_kernel<4, 4, 0>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<8, 4, 0>),
       reinterpret_cast<const void*>(&skinny_reg_kernel<1, 4>),
-      reinterpret_cast<const void*>(&skinny_lds_kernel<2, 8, 4>),
-      reinterpret_cast<const void*>(&skinny_lds_kernel<4, 8, 4>),
+      reinterpret_cast<const void*>(&skinny_lds_kernel<2, 4, 4>),
+      reinterpret_cast<const void*>(&skinny_lds_kernel<4, 4, 4>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<8, 4, 4>),
       reinterpret_cast<const void*>(&skinny_reg_kernel<1, 8>),
-      reinterpret_cast<const void*>(&skinny_lds_kernel<2, 8, 8>),
-      reinterpret_cast<const void*>(&skinny_lds_kernel<4, 8, 8>),
+      reinterpret_cast<const void*>(&skinny_lds_kernel<2, 4, 8>),
+      reinterpret_cast<const void*>(&skinny_lds_kernel<4, 4, 8>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<8, 4, 8>),
       reinterpret_cast<const void*>(&skinny_reduce_kernel),
   };
