@@ -575,7 +575,7 @@ def attention_measure(torch, ops, gen, launches):
     hev.close()
     flop = 4 * a["hq"] * a["tq"] * a["tk"] * a["d"]
     tf = flop / (ms * 1e-3) / 1e12
-    return {"kernel": "attention_kernel<128, 0>", "shape": dict(a),
+    return {"kernel": "attention_kernel<128, 0, 8>", "shape": dict(a),
             "mask": "bidirectional", "avg_launch_ms": round(ms, 5),
             "flop_per_launch": flop, "value": round(tf, 2), "unit": "TFLOP/s",
             "roofline": {"bound": "mfma", "achieved": round(tf, 2),
@@ -612,8 +612,8 @@ def attention_masks_measure(torch, ops, gen, launches):
                                                       a["tk"], q_offset=pre),
     }
     res = {}
-    for mode, kern in (("causal", "attention_kernel<128, 1>"),
-                       ("block_causal", "attention_kernel<128, 2>")):
+    for mode, kern in (("causal", "attention_kernel<128, 1, 4>"),
+                       ("block_causal", "attention_kernel<128, 2, 4>")):
         fn = calls[mode]
         for _ in range(3):
             fn()

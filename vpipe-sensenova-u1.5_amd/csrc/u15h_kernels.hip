@@ -1619,8 +1619,9 @@ f16_to_bf16_kernel(const uint2* __restrict__ src, uint2* __restrict__ dst,
 }
 
 // ---- flash attention ------------------------------------------------------
-// Grouped-query attention over a K/V cache, one workgroup per 128 queries
-// of one head (four waves of 32), keys streamed in tiles of 64.
+// Grouped-query attention over a K/V cache, one workgroup per 32 * NWV
+// queries of one head (NWV waves of 32: 8 bidirectional, 4 causal), keys
+// streamed in tiles of 64.
 //
 // The score tile is computed TRANSPOSED, S^T = K Q^T, with the key
 // fragment as the MFMA's first operand: a lane then holds 32 scores (two
@@ -1680,6 +1681,17 @@ sum_halves(float v)
 
 constexpr float kLazy = 8.0f;
 
+// Waves (32 queries each) per attention workgroup.  Bidirectional: 8, so
+// each K/V tile copied into LDS serves 256 queries (the generation pass
+// 0.295-0.302 ms against 0.309-0.311 with 4).  The causal masks keep 4:
+// a workgroup runs to the last key its last query sees, and 256-query
+// workgroups waste more masked keys (causal 12% slower with 8).
+template <int MODE>
+constexpr int attn_waves()
+{
+  return MODE == 0 ? 8 : 4;
+}
+
 // 64-byte block swizzle of V row r: four consecutive rows at one block
 // land on four different 64-byte bank ranges
 template <int D>
@@ -1692,15 +1704,19 @@ vswz(int r)
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef short i16x2_t __attribute__((ext_vector_type(2)));
 
-template <int D, int MODE>
-__global__ __launch_bounds__(256, 2) void
+template <int D, int MODE, int NWV>
+__global__ __launch_bounds__(64 * NWV, 8 / NWV) void
 attention_kernel(const AttnArgs A)
 {
   constexpr int BK = 64;
   constexpr int KCH = D / 8;                 // 16-byte chunks per row
   constexpr int NDS = D / 16;                // MFMA K-steps of the scores
   constexpr int NCB = D / 32;                // 32-row blocks of O^T
-  constexpr int CPW = D / 32;                // 1 KiB copies per wave per tile
+  constexpr int QT = 32 * NWV;               // queries per workgroup
+  constexpr int kTileKiB = BK * D * 2 / 1024;
+  // 1 KiB copies per copying wave per tile, and the waves that copy
+  constexpr int CPW = kTileKiB >= NWV ? kTileKiB / NWV : 1;
+  constexpr int kCopyWaves = kTileKiB / CPW;
   // Tile j's K sits in ks<j & 1>, its V in vs<j & 1>, its t entries in
   // ts[j % 3]: iteration t reads K of tile t+1, V and t of tile t, and
   // writes K of tile t+2, V of tile t+1, t of tile t+2.
@@ -1713,7 +1729,7 @@ attention_kernel(const AttnArgs A)
   // Work item: (query head, 128-query tile), ordered kv head first, so
   // that cutting the list into 8 runs (one per XCD, workgroups b, b+8, ...
   // run on XCD b % 8) keeps each kv head's keys in one XCD's L2.
-  const int ntq = (A.tq + 127) / 128;
+  const int ntq = (A.tq + QT - 1) / QT;
   const int items = A.hq * ntq;
   const int b = blockIdx.x;
   const int item = (items % 8 == 0) ? (b % 8) * (items / 8) + b / 8 : b;
@@ -1728,7 +1744,7 @@ attention_kernel(const AttnArgs A)
   const int lane = tid & 63;
   const int lq = lane & 31;
   const int half = lane >> 5;
-  const int qrow = qt * 128 + wave * 32 + lq;     // this lane's query
+  const int qrow = qt * QT + wave * 32 + lq;      // this lane's query
   const bool qvalid = qrow < A.tq;
   const int qpos = A.q_offset + qrow;
   const float scale = 1.4426950408889634f * rsqrtf((float)D);
@@ -1768,11 +1784,13 @@ attention_kernel(const AttnArgs A)
     const int left = max(A.tk - j0, 0);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(kbase + (long long)j0 * D, left * D * 2);
     char* dst = reinterpret_cast<char*>(dst_tile) + wave * CPW * 1024;
+    if (kCopyWaves == NWV || wave < kCopyWaves) {
 #pragma unroll
-    for (int i = 0; i < CPW; ++i) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rs, (__attribute__((address_space(3))) void*)(dst + i * 1024), 16, koffs[i],
-          0, 0, 0);
+      for (int i = 0; i < CPW; ++i) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rs, (__attribute__((address_space(3))) void*)(dst + i * 1024), 16, koffs[i],
+            0, 0, 0);
+      }
     }
     if constexpr (MODE == 2) {
       const __amdgpu_buffer_rsrc_t ts_rs = make_rsrc(A.t_index + j0, left * 4);
@@ -1783,11 +1801,13 @@ attention_kernel(const AttnArgs A)
     const int left = max(A.tk - j0, 0);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(vbase + (long long)j0 * D, left * D * 2);
     char* dst = reinterpret_cast<char*>(dst_tile) + wave * CPW * 1024;
+    if (kCopyWaves == NWV || wave < kCopyWaves) {
 #pragma unroll
-    for (int i = 0; i < CPW; ++i) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rs, (__attribute__((address_space(3))) void*)(dst + i * 1024), 16, voffs[i],
-          0, 0, 0);
+      for (int i = 0; i < CPW; ++i) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rs, (__attribute__((address_space(3))) void*)(dst + i * 1024), 16, voffs[i],
+            0, 0, 0);
+      }
     }
   };
   auto store_t = [&](int tbuf) {
@@ -1809,21 +1829,21 @@ attention_kernel(const AttnArgs A)
   f32x16_t sc[2];           // scores of the current tile
   float mb = -INFINITY;     // their max over the row (both halves)
 
-  const int q_first = A.q_offset + qt * 128;      // workgroup's first query
+  const int q_first = A.q_offset + qt * QT;       // workgroup's first query
   // One past the last key any of the workgroup's queries sees; the tiles
   // after it are fully masked and would add exactly 0.
   int kend = A.tk;
   if constexpr (MODE != 0) {
-    const int q_last = A.q_offset + min(A.tq, qt * 128 + 128) - 1;
+    const int q_last = A.q_offset + min(A.tq, qt * QT + QT) - 1;
     kend = min(A.tk, q_last + 1);
   }
   if constexpr (MODE == 2) {
     // Keys past q_last are visible only through an equal t.  Bound them by
     // the t range of the workgroup's queries: the last key whose t lies in
     // [tmin, tmax] (a superset of the visible keys; the mask is exact).
-    __shared__ int kred[3][4];
+    __shared__ int kred[3][NWV];
     int tmin = INT_MAX, tmax = INT_MIN;
-    if (tid < 128 && qt * 128 + tid < A.tq) {
+    if (tid < QT && qt * QT + tid < A.tq) {
       const int tv = A.t_index[q_first + tid];
       tmin = tv;
       tmax = tv;
@@ -1835,11 +1855,16 @@ attention_kernel(const AttnArgs A)
     }
     if (lane == 0) { kred[0][wave] = tmin; kred[1][wave] = tmax; }
     __syncthreads();
-    tmin = min(min(kred[0][0], kred[0][1]), min(kred[0][2], kred[0][3]));
-    tmax = max(max(kred[1][0], kred[1][1]), max(kred[1][2], kred[1][3]));
+    tmin = kred[0][0];
+    tmax = kred[1][0];
+#pragma unroll
+    for (int w = 1; w < NWV; ++w) {
+      tmin = min(tmin, kred[0][w]);
+      tmax = max(tmax, kred[1][w]);
+    }
     int jm = kend - 1;
 #pragma unroll 8
-    for (int j = kend + tid; j < A.tk; j += 256) {
+    for (int j = kend + tid; j < A.tk; j += 64 * NWV) {
       const int tv = A.t_index[j];
       if (tv >= tmin && tv <= tmax) { jm = j; }
     }
@@ -1847,7 +1872,10 @@ attention_kernel(const AttnArgs A)
     for (int o = 32; o > 0; o >>= 1) { jm = max(jm, __shfl_xor(jm, o)); }
     if (lane == 0) { kred[2][wave] = jm; }
     __syncthreads();
-    kend = max(max(kred[2][0], kred[2][1]), max(kred[2][2], kred[2][3])) + 1;
+    jm = kred[2][0];
+#pragma unroll
+    for (int w = 1; w < NWV; ++w) { jm = max(jm, kred[2][w]); }
+    kend = jm + 1;
   }
   const int ntiles = (kend + BK - 1) / BK;
 
@@ -2815,8 +2843,9 @@ template <int D, int MODE>
 hipError_t
 launch_attention_d(const AttnArgs& a, hipStream_t s)
 {
-  const int ntq = (a.tq + 127) / 128;
-  hipLaunchKernelGGL((attention_kernel<D, MODE>), dim3(a.hq * ntq), dim3(256),
+  constexpr int NWV = attn_waves<MODE>();
+  const int ntq = (a.tq + 32 * NWV - 1) / (32 * NWV);
+  hipLaunchKernelGGL((attention_kernel<D, MODE, NWV>), dim3(a.hq * ntq), dim3(64 * NWV),
                      0, s, a);
   return hipGetLastError();
 }
@@ -2935,15 +2964,15 @@ kernels_loadable()
 {
   const void* fns[] = {
       reinterpret_cast<const void*>(&f16_to_bf16_kernel),
-      reinterpret_cast<const void*>(&attention_kernel<128, 0>),
-      reinterpret_cast<const void*>(&attention_kernel<128, 1>),
-      reinterpret_cast<const void*>(&attention_kernel<128, 2>),
-      reinterpret_cast<const void*>(&attention_kernel<64, 0>),
-      reinterpret_cast<const void*>(&attention_kernel<64, 1>),
-      reinterpret_cast<const void*>(&attention_kernel<64, 2>),
-      reinterpret_cast<const void*>(&attention_kernel<32, 0>),
-      reinterpret_cast<const void*>(&attention_kernel<32, 1>),
-      reinterpret_cast<const void*>(&attention_kernel<32, 2>),
+      reinterpret_cast<const void*>(&attention_kernel<128, 0, attn_waves<0>()>),
+      reinterpret_cast<const void*>(&attention_kernel<128, 1, attn_waves<1>()>),
+      reinterpret_cast<const void*>(&attention_kernel<128, 2, attn_waves<2>()>),
+      reinterpret_cast<const void*>(&attention_kernel<64, 0, attn_waves<0>()>),
+      reinterpret_cast<const void*>(&attention_kernel<64, 1, attn_waves<1>()>),
+      reinterpret_cast<const void*>(&attention_kernel<64, 2, attn_waves<2>()>),
+      reinterpret_cast<const void*>(&attention_kernel<32, 0, attn_waves<0>()>),
+      reinterpret_cast<const void*>(&attention_kernel<32, 1, attn_waves<1>()>),
+      reinterpret_cast<const void*>(&attention_kernel<32, 2, attn_waves<2>()>),
       reinterpret_cast<const void*>(&transpose_rows_kernel),
       reinterpret_cast<const void*>(&split_norm_rope_kernel<true, true>),
       reinterpret_cast<const void*>(&split_norm_rope_kernel<true, false>),
