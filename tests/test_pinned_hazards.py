@@ -47,7 +47,7 @@ def kernels():
     found = {}
     name = None
     for raw in out.splitlines():
-        if re.match(r"^_Z\S*(mot_gemm_kernel\S*Li2E|skinny_(?:reg|lds)_kernel)\S*:", raw):
+        if re.match(r"^_Z\S*(mot_gemm_kernel\S*Li2E|skinny_(?:reg|lds|dma)_kernel)\S*:", raw):
             name = raw.split(":")[0]
             found[name] = []
             continue
@@ -66,16 +66,16 @@ def test_every_epilogue_has_a_pinned_kernel(kernels):
     # 4-wave GEMM: bf16, SwiGLU, int32 and dequant epilogues, 256 MFMAs
     # each; skinny GEMM: the four row-group builds (register kernel for 16
     # rows, LDS kernel for 32, 64 and 128) for bf16 weights and 4- and
-    # 8-bit packs, 16 MFMAs per 16 rows and unrolled K-block (2 k-steps),
+    # 8-bit packs, and the DMA kernel for 16 rows of bf16 weights, 16 MFMAs per 16 rows and unrolled K-block (2 k-steps),
     # 2 blocks unrolled in the register kernel, 4 in the LDS kernels
     four = [n for n in kernels if "mot_gemm_kernel" in n]
     skinny = [n for n in kernels if "skinny_" in n]
-    assert len(four) == 4 and len(skinny) == 12
+    assert len(four) == 4 and len(skinny) == 13
     for n in four:
         assert sum(1 for s in kernels[n] if s.startswith("v_mfma")) == 256
     for n in skinny:
-        mt = int(re.search(r"skinny_(?:reg|lds)_kernelILi(\d+)E", n).group(1))
-        depth = 2 if mt == 1 else 4     # register kernel: kSkDepth; LDS kernels: D
+        mt = int(re.search(r"skinny_(?:reg|lds|dma)_kernelILi(\d+)E", n).group(1))
+        depth = 2 if mt == 1 else 4     # register / DMA kernels: 2; LDS kernels: D
         assert sum(1 for s in kernels[n] if s.startswith("v_mfma")) == 2 * mt * depth
 
 

@@ -2380,6 +2380,156 @@ skinny_reg_kernel(const SkinnyBatch B)
   }
 }
 
+// Rows <= 16 with bf16 weights: skinny_reg_kernel's work split, but each
+// wave's 16 weight rows of a K-block arrive by two whole-line direct loads
+// global -> LDS (instruction i: rows 8i .. 8i+7, 8 lanes x 16 bytes per
+// 128-byte row) into the wave's own slot of a kSkDmaDepth-stage ring, and
+// the fragments are read back in the MFMA's layout (lane (g, r): row r,
+// 16-byte chunks 2g and 2g+1, the same K order as the register kernel, so
+// the two agree bit for bit).  The register kernel's lane layout asks for
+// every 128-byte line in two half-used requests.  Chunk c of row r sits at
+// position c ^ ((r >> 1) & 7) of its row, so the 16 lanes of a fragment
+// read (16 rows, one chunk) cover the 64 banks once.  The slots are
+// private to their wave: no barrier until the partial sums meet.
+// Measured (N = 6144, K = 4096, 12 rotated weight copies, same box): 12.6
+// / 13.2 / 15.4 us per call at 1 / 8 / 16 rows against 13.6-13.9 / 15.6 /
+// 18.2 for the register kernel.
+constexpr int kSkDmaDepth = 2;    // K-blocks in flight per wave (4 measured slower)
+
+template <int MT>
+__global__ __launch_bounds__(256) void
+skinny_dma_kernel(const SkinnyBatch B)
+{
+  static_assert(kSkDmaDepth == 2 || kSkDmaDepth == 4, "ring of 2 or 4 stages");
+  __shared__ f32x4_t red[4][MT][64];
+  // one __shared__ object per stage, so the compiler tells a stage's reads
+  // from the copies filling another
+  __shared__ __attribute__((aligned(1024))) char wr0[4 * 2048];
+  __shared__ __attribute__((aligned(1024))) char wr1[4 * 2048];
+  __shared__ __attribute__((aligned(1024))) char wr2[kSkDmaDepth == 4 ? 4 * 2048 : 16];
+  __shared__ __attribute__((aligned(1024))) char wr3[kSkDmaDepth == 4 ? 4 * 2048 : 16];
+  const int S = B.split;
+  const int cbg = blockIdx.x / S;
+  const int share = blockIdx.x - cbg * S;
+  const SkinnyProblem& P = B.p[skinny_problem(B, cbg)];
+  const int kbytes = B.kbytes;
+  const int nkb = kbytes / 128;
+  const int kb0 = share * nkb / S;
+  const int nk = (share + 1) * nkb / S - kb0;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4, r = lane & 15;
+  const int n0 = (cbg - P.cb_begin) * 16;
+  const int nw = (nk - wave + 3) / 4;              // this wave's K-blocks
+
+  // weight rows [n0, n0 + 16) and activation rows [0, rows); rows past
+  // either read as zero
+  const int wrows = max(0, min(16, P.n - n0));
+  const __amdgpu_buffer_rsrc_t wrs =
+      make_rsrc(static_cast<const char*>(P.w) + (size_t)min(n0, P.n) * kbytes,
+                wrows * kbytes);
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(P.a, P.rows * kbytes);
+  const int lv = r * kbytes + g * 32;               // row r, bytes 32g..
+  int dv[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int row = 8 * i + (lane >> 3);
+    dv[i] = row * kbytes + (((lane & 7) ^ ((row >> 1) & 7)) << 4);
+  }
+  const int slot = wave * 2048;
+  int rdo[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    rdo[ks] = slot + r * 128 + (((2 * g + ks) ^ ((r >> 1) & 7)) << 4);
+  }
+
+  i32x4_t xreg[kSkDmaDepth][MT][2];
+  auto issue = [&](char* stage, int d, int j) {
+    const int oob = j < nw ? 0 : kOobOffset;        // past the share: zeros
+    const int kb = kb0 + wave + 4 * min(j, max(nw - 1, 0));
+    const int ko = __builtin_amdgcn_readfirstlane(kb * 128);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          wrs, (__attribute__((address_space(3))) void*)(stage + slot + i * 1024), 16,
+          dv[i] + oob, ko, 0, 0);
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int v = lv + mt * 16 * kbytes + oob;
+      xreg[d][mt][0] = __builtin_amdgcn_raw_buffer_load_b128(xr, v, ko, 0);
+      xreg[d][mt][1] = __builtin_amdgcn_raw_buffer_load_b128(xr, v + 16, ko, 0);
+    }
+  };
+  char* const ring[4] = {wr0, wr1, wr2, wr3};
+
+  f32x4_t acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    acc[mt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    asm volatile("" : "+v"(acc[mt]));
+  }
+  asm volatile("s_nop 4");
+  // the loads in K order (compiler fences between the blocks)
+#pragma unroll
+  for (int d = 0; d < kSkDmaDepth; ++d) {
+    asm volatile("" ::: "memory");
+    issue(ring[d], d, d);
+  }
+  // a block's copies have landed once at most the later blocks' loads are
+  // in flight (loads complete in issue order; the compiler may order a
+  // block's copies and activation loads either way, so the whole block is
+  // waited for)
+  constexpr int kAfter = (kSkDmaDepth - 1) * (2 + 2 * MT);
+  static_assert(kAfter < 64, "vmcnt holds at most 63");
+  const int nw_pad = (nw + kSkDmaDepth - 1) / kSkDmaDepth * kSkDmaDepth;
+  for (int j0 = 0; j0 < nw_pad; j0 += kSkDmaDepth) {
+#pragma unroll
+    for (int d = 0; d < kSkDmaDepth; ++d) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kAfter) : "memory");
+      i32x4_t wf[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        wf[ks] = *reinterpret_cast<const i32x4_t*>(ring[d] + rdo[ks]);
+      }
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) { sk_mfma<0>(acc[mt], wf[ks], xreg[d][mt][ks]); }
+      }
+      // the MFMAs consumed this stage's reads; its slot takes block j + depth
+      asm volatile("" ::: "memory");
+      issue(ring[d], d, j0 + d + kSkDmaDepth);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
+               ::: "memory");
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    asm volatile("" : "+v"(acc[mt]));
+    red[wave][mt][lane] = acc[mt];
+  }
+  __syncthreads();
+  if (wave != 0) { return; }
+  const int n = n0 + 4 * g;
+  if (n >= P.n) { return; }
+  uint2 bb = make_uint2(0u, 0u);
+  if (S == 1 && P.bias != nullptr) { bb = *reinterpret_cast<const uint2*>(P.bias + n); }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = mt * 16 + r;
+    if (m >= P.rows) { continue; }
+    const f32x4_t v = ((red[0][mt][lane] + red[1][mt][lane]) + red[2][mt][lane]) +
+                      red[3][mt][lane];
+    if (S == 1) {
+      skinny_store(P, m, n, v, bb);
+    } else {
+      float* ws = B.ws + P.ws_off + (size_t)share * P.rows * P.n;
+      *reinterpret_cast<f32x4_t*>(ws + (size_t)m * P.n + n) = v;
+    }
+  }
+}
+
 // Rows 17..128: a workgroup computes 64 output columns over a K share.
 // Wave w streams weight rows [16w, 16w + 16) of the block into registers,
 // while the activation rows' K-block, which all four waves use, goes to
@@ -2635,7 +2785,13 @@ template <int QB>
 hipError_t
 launch_skinny_q(const SkinnyBatch& b, hipStream_t s, const GemmEvents& ev)
 {
-  if (b.max_rows <= 16) { return launch_skinny(skinny_reg_kernel<1, QB>, b, s, ev); }
+  if (b.max_rows <= 16) {
+    if constexpr (QB == 0) {
+      return launch_skinny(skinny_dma_kernel<1>, b, s, ev);
+    } else {
+      return launch_skinny(skinny_reg_kernel<1, QB>, b, s, ev);
+    }
+  }
   if (b.max_rows <= 32) { return launch_skinny(skinny_lds_kernel<2, 4, QB>, b, s, ev); }
   if (b.max_rows <= 64) { return launch_skinny(skinny_lds_kernel<4, 4, QB>, b, s, ev); }
   return launch_skinny(skinny_lds_kernel<8, 4, QB>, b, s, ev);
@@ -2991,6 +3147,7 @@ kernels_loadable()
       reinterpret_cast<const void*>(&gather_rows_kernel<true>),
       reinterpret_cast<const void*>(&gather_rows_kernel<false>),
       reinterpret_cast<const void*>(&skinny_reg_kernel<1, 0>),
+      reinterpret_cast<const void*>(&skinny_dma_kernel<1>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<2, 4, 0>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<4, 4, 0>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<8, 4, 0>),
