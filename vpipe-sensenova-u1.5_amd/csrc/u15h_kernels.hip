@@ -2531,18 +2531,21 @@ skinny_dma_kernel(const SkinnyBatch B)
 }
 
 // Rows 17..128: a workgroup computes 64 output columns over a K share.
-// Wave w streams weight rows [16w, 16w + 16) of the block into registers,
-// while the activation rows' K-block, which all four waves use, goes to
-// LDS by DMA through a ring of D stages (one __shared__ object each, so
-// the compiler can tell a stage's DMA from another stage's reads), as
-// deep as the weight lead, which a shallower ring would cut short: 8
-// stages (64 KiB) up to 64 rows, 4 (64 KiB) up to 128, so that two
-// workgroups fit a CU either way.
+// Wave w streams weight rows [16w, 16w + 16) of the block -- into its
+// slot of a weight ring by whole-line direct loads for bf16 weights up to
+// 64 rows, into registers otherwise -- while the activation rows'
+// K-block, which all four waves use, goes to LDS by DMA through a ring of
+// D = 4 stages (one __shared__ object each, so the compiler can tell a
+// stage's DMA from another stage's reads): 48 / 64 / 64 KiB of LDS at 32 /
+// 64 / 128 rows, two workgroups per CU.
 template <int MT, int D, int QB>
 __device__ __forceinline__ void
-skinny_lds_tile(const SkinnyBatch& B, char* const (&xs)[D])
+skinny_lds_tile(const SkinnyBatch& B, char* const (&xs)[D], char* const (&wsr)[D])
 {
   constexpr int kXInst = MT / 2;                    // DMA loads per wave
+  // bf16 weights up to 64 rows arrive like skinny_dma_kernel's: whole-line
+  // direct loads into the wave's slot of a D-stage weight ring
+  constexpr bool kWDma = QB == 0 && MT <= 4;
   const int S = B.split;
   const int cbg = blockIdx.x / S;
   const int share = blockIdx.x - cbg * S;
@@ -2587,10 +2590,27 @@ skinny_lds_tile(const SkinnyBatch& B, char* const (&xs)[D])
           16, xv[j] + oob, ko, 0, 0);
     }
   };
-  SkW<QB> wreg[D];
+  SkW<QB> wreg[kWDma ? 1 : D];
+  int dv[2], rdo[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int row = 8 * i + (lane >> 3);
+    dv[i] = row * kbytes + (((lane & 7) ^ ((row >> 1) & 7)) << 4);
+    rdo[i] = wave * 2048 + r * 128 + (((2 * g + i) ^ ((r >> 1) & 7)) << 4);
+  }
   auto issue_w = [&](int slot, int i) {
     const int oob = i < nk ? 0 : kOobOffset;
-    sk_load_w<QB>(wreg[slot], wsrc, kb0 + min(i, nk - 1), oob, B.qgroup);
+    if constexpr (kWDma) {
+      const int ko = __builtin_amdgcn_readfirstlane((kb0 + min(i, nk - 1)) * 128);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            wsrc.w, (__attribute__((address_space(3))) void*)(wsr[slot] + wave * 2048 + j * 1024),
+            16, dv[j] + oob, ko, 0, 0);
+      }
+    } else {
+      sk_load_w<QB>(wreg[slot], wsrc, kb0 + min(i, nk - 1), oob, B.qgroup);
+    }
   };
 
   f32x4_t acc[MT];
@@ -2602,20 +2622,35 @@ skinny_lds_tile(const SkinnyBatch& B, char* const (&xs)[D])
   asm volatile("s_nop 4");
 
   // The wait before each barrier counts loads in issue order, so the order
-  // is pinned with compiler fences: the prologue's x stages, then its
-  // weight blocks in K order; in each block the x refill, then the weight
-  // refill.
+  // is pinned with compiler fences.  In each block: the x refill, then the
+  // weight refill.  Prologue with weights in LDS: the blocks in K order,
+  // weights before x (the last block's x stage comes with the loop), so
+  // that block j's weight copies always go out before its x stage.  With
+  // weights in registers, whose reads the compiler makes wait by itself:
+  // the x stages, then the weight blocks (measured 1-2% faster for the
+  // w8 pack at 32-64 rows than the interleaved order).
+  if constexpr (kWDma) {
 #pragma unroll
-  for (int i = 0; i + 1 < D; ++i) { issue_x(xs[i], i); }
+    for (int i = 0; i < D; ++i) {
+      asm volatile("" ::: "memory");
+      issue_w(i, i);
+      asm volatile("" ::: "memory");
+      if (i + 1 < D) { issue_x(xs[i], i); }
+    }
+  } else {
 #pragma unroll
-  for (int i = 0; i < D; ++i) {
-    asm volatile("" ::: "memory");
-    issue_w(i, i);
+    for (int i = 0; i + 1 < D; ++i) { issue_x(xs[i], i); }
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+      asm volatile("" ::: "memory");
+      issue_w(i, i);
+    }
   }
-  // Before block i's barrier this wave's DMA of x stage i has landed: at
-  // most the loads issued after it may be in flight -- the weight loads
-  // of its own iteration and D - 2 later iterations' x and weight
-  // loads (earlier in the prologue, where more follow it).
+  // Before block i's barrier this wave's DMA of x stage i (and, in LDS,
+  // block i's weights) has landed: at most the loads issued after it may
+  // be in flight -- the weight loads of block i + 1 and D - 2 later
+  // blocks' x and weight loads (in the register prologue more follow x
+  // stage i, and the wait holds more back than it needs).
   constexpr int kWLoads = QB == 0 ? 2 : 3;          // per K-block
   constexpr int kAfterX = kWLoads + (D - 2) * (kXInst + kWLoads);
   static_assert(kAfterX < 64, "vmcnt holds at most 63");
@@ -2641,10 +2676,19 @@ skinny_lds_tile(const SkinnyBatch& B, char* const (&xs)[D])
       }
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const i32x4_t wf = sk_frag<QB>(wreg[d], ks);
+        i32x4_t wf;
+        if constexpr (kWDma) {
+          // block i's weight copies were issued before its x stage, which
+          // the barrier above has seen land
+          wf = *reinterpret_cast<const i32x4_t*>(wsr[d] + rdo[ks]);
+        } else {
+          wf = sk_frag<QB>(wreg[d], ks);
+        }
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) { sk_mfma<QB>(acc[mt], wf, xf[mt][ks]); }
       }
+      // (the MFMAs consumed this block's weight reads before the refill)
+      asm volatile("" ::: "memory");
       issue_w(d, i + D);
     }
   }
@@ -2677,22 +2721,19 @@ __global__ __launch_bounds__(256) void
 skinny_lds_kernel(const SkinnyBatch B)
 {
   constexpr int kStage = MT * 16 * 128;
+  constexpr int kWStage = QB == 0 && MT <= 4 ? 4 * 2048 : 16;   // weight ring stage
   __shared__ __attribute__((aligned(1024))) char xs0[kStage];
   __shared__ __attribute__((aligned(1024))) char xs1[kStage];
   __shared__ __attribute__((aligned(1024))) char xs2[kStage];
   __shared__ __attribute__((aligned(1024))) char xs3[kStage];
-  if constexpr (D == 4) {
-    char* const xs[4] = {xs0, xs1, xs2, xs3};
-    skinny_lds_tile<MT, 4, QB>(B, xs);
-  } else {
-    static_assert(D == 8, "ring of 4 or 8 stages");
-    __shared__ __attribute__((aligned(1024))) char xs4[kStage];
-    __shared__ __attribute__((aligned(1024))) char xs5[kStage];
-    __shared__ __attribute__((aligned(1024))) char xs6[kStage];
-    __shared__ __attribute__((aligned(1024))) char xs7[kStage];
-    char* const xs[8] = {xs0, xs1, xs2, xs3, xs4, xs5, xs6, xs7};
-    skinny_lds_tile<MT, 8, QB>(B, xs);
-  }
+  __shared__ __attribute__((aligned(1024))) char ws0[kWStage];
+  __shared__ __attribute__((aligned(1024))) char ws1[kWStage];
+  __shared__ __attribute__((aligned(1024))) char ws2[kWStage];
+  __shared__ __attribute__((aligned(1024))) char ws3[kWStage];
+  static_assert(D == 4, "a ring of 4 stages (8 measured slower)");
+  char* const xs[4] = {xs0, xs1, xs2, xs3};
+  char* const wsr[4] = {ws0, ws1, ws2, ws3};
+  skinny_lds_tile<MT, 4, QB>(B, xs, wsr);
 }
 
 // Sums the S partial sums of every output in share order, adds the bias
