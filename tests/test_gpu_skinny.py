@@ -48,6 +48,8 @@ CASES = [
     (16, 4096, 4096),    # S=8
     (17, 128, 72),       # S=1 (two K-blocks), the <=32-row build
     (64, 12288, 512),    # S=16, the <=64-row build
+    (65, 4096, 1032),    # the <=96-row build, ragged rows, N % 64 = 8
+    (96, 4096, 6144),    # the <=96-row build, full, S=4
     (100, 4096, 1000),   # the <=128-row build, ragged rows, N % 64 = 40
     (128, 4096, 6144),   # config-5 und rows at q|k|v width, S=4
     (128, 12288, 4096),  # config-5 und rows at the down projection, S=8

@@ -70,7 +70,7 @@ def test_every_epilogue_has_a_pinned_kernel(kernels):
     # 2 blocks unrolled in the register kernel, 4 in the LDS kernels
     four = [n for n in kernels if "mot_gemm_kernel" in n]
     skinny = [n for n in kernels if "skinny_" in n]
-    assert len(four) == 4 and len(skinny) == 13
+    assert len(four) == 4 and len(skinny) == 16
     for n in four:
         assert sum(1 for s in kernels[n] if s.startswith("v_mfma")) == 256
     for n in skinny:

@@ -2545,7 +2545,7 @@ skinny_lds_tile(const SkinnyBatch& B, char* const (&xs)[D], char* const (&wsr)[D
   constexpr int kXInst = MT / 2;                    // DMA loads per wave
   // bf16 weights up to 64 rows arrive like skinny_dma_kernel's: whole-line
   // direct loads into the wave's slot of a D-stage weight ring
-  constexpr bool kWDma = QB == 0 && MT <= 4;
+  constexpr bool kWDma = QB == 0 && MT <= 6;
   const int S = B.split;
   const int cbg = blockIdx.x / S;
   const int share = blockIdx.x - cbg * S;
@@ -2721,7 +2721,7 @@ __global__ __launch_bounds__(256) void
 skinny_lds_kernel(const SkinnyBatch B)
 {
   constexpr int kStage = MT * 16 * 128;
-  constexpr int kWStage = QB == 0 && MT <= 4 ? 4 * 2048 : 16;   // weight ring stage
+  constexpr int kWStage = QB == 0 && MT <= 6 ? 4 * 2048 : 16;   // weight ring stage
   __shared__ __attribute__((aligned(1024))) char xs0[kStage];
   __shared__ __attribute__((aligned(1024))) char xs1[kStage];
   __shared__ __attribute__((aligned(1024))) char xs2[kStage];
@@ -2835,6 +2835,7 @@ launch_skinny_q(const SkinnyBatch& b, hipStream_t s, const GemmEvents& ev)
   }
   if (b.max_rows <= 32) { return launch_skinny(skinny_lds_kernel<2, 4, QB>, b, s, ev); }
   if (b.max_rows <= 64) { return launch_skinny(skinny_lds_kernel<4, 4, QB>, b, s, ev); }
+  if (b.max_rows <= 96) { return launch_skinny(skinny_lds_kernel<6, 4, QB>, b, s, ev); }
   return launch_skinny(skinny_lds_kernel<8, 4, QB>, b, s, ev);
 }
 
@@ -3191,14 +3192,17 @@ kernels_loadable()
       reinterpret_cast<const void*>(&skinny_dma_kernel<1>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<2, 4, 0>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<4, 4, 0>),
+      reinterpret_cast<const void*>(&skinny_lds_kernel<6, 4, 0>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<8, 4, 0>),
       reinterpret_cast<const void*>(&skinny_reg_kernel<1, 4>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<2, 4, 4>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<4, 4, 4>),
+      reinterpret_cast<const void*>(&skinny_lds_kernel<6, 4, 4>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<8, 4, 4>),
       reinterpret_cast<const void*>(&skinny_reg_kernel<1, 8>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<2, 4, 8>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<4, 4, 8>),
+      reinterpret_cast<const void*>(&skinny_lds_kernel<6, 4, 8>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<8, 4, 8>),
       reinterpret_cast<const void*>(&skinny_reduce_kernel),
   };
