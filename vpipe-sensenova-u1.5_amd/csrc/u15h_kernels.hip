@@ -2545,7 +2545,7 @@ skinny_lds_tile(const SkinnyBatch& B, char* const (&xs)[D], char* const (&wsr)[D
   constexpr int kXInst = MT / 2;                    // DMA loads per wave
   // bf16 weights up to 64 rows arrive like skinny_dma_kernel's: whole-line
   // direct loads into the wave's slot of a D-stage weight ring
-  constexpr bool kWDma = QB == 0 && MT <= 6;
+  constexpr bool kWDma = QB == 0;
   const int S = B.split;
   const int cbg = blockIdx.x / S;
   const int share = blockIdx.x - cbg * S;
@@ -2720,20 +2720,26 @@ template <int MT, int D, int QB>
 __global__ __launch_bounds__(256) void
 skinny_lds_kernel(const SkinnyBatch B)
 {
+  static_assert(D == 3 || D == 4, "a ring of 3 or 4 stages (8 measured slower)");
   constexpr int kStage = MT * 16 * 128;
-  constexpr int kWStage = QB == 0 && MT <= 6 ? 4 * 2048 : 16;   // weight ring stage
+  constexpr int kWStage = QB == 0 ? 4 * 2048 : 16;   // weight ring stage
   __shared__ __attribute__((aligned(1024))) char xs0[kStage];
   __shared__ __attribute__((aligned(1024))) char xs1[kStage];
   __shared__ __attribute__((aligned(1024))) char xs2[kStage];
-  __shared__ __attribute__((aligned(1024))) char xs3[kStage];
+  __shared__ __attribute__((aligned(1024))) char xs3[D == 4 ? kStage : 16];
   __shared__ __attribute__((aligned(1024))) char ws0[kWStage];
   __shared__ __attribute__((aligned(1024))) char ws1[kWStage];
   __shared__ __attribute__((aligned(1024))) char ws2[kWStage];
-  __shared__ __attribute__((aligned(1024))) char ws3[kWStage];
-  static_assert(D == 4, "a ring of 4 stages (8 measured slower)");
-  char* const xs[4] = {xs0, xs1, xs2, xs3};
-  char* const wsr[4] = {ws0, ws1, ws2, ws3};
-  skinny_lds_tile<MT, 4, QB>(B, xs, wsr);
+  __shared__ __attribute__((aligned(1024))) char ws3[D == 4 ? kWStage : 16];
+  if constexpr (D == 4) {
+    char* const xs[4] = {xs0, xs1, xs2, xs3};
+    char* const wsr[4] = {ws0, ws1, ws2, ws3};
+    skinny_lds_tile<MT, 4, QB>(B, xs, wsr);
+  } else {
+    char* const xs[3] = {xs0, xs1, xs2};
+    char* const wsr[3] = {ws0, ws1, ws2};
+    skinny_lds_tile<MT, 3, QB>(B, xs, wsr);
+  }
 }
 
 // Sums the S partial sums of every output in share order, adds the bias
@@ -2836,7 +2842,11 @@ launch_skinny_q(const SkinnyBatch& b, hipStream_t s, const GemmEvents& ev)
   if (b.max_rows <= 32) { return launch_skinny(skinny_lds_kernel<2, 4, QB>, b, s, ev); }
   if (b.max_rows <= 64) { return launch_skinny(skinny_lds_kernel<4, 4, QB>, b, s, ev); }
   if (b.max_rows <= 96) { return launch_skinny(skinny_lds_kernel<6, 4, QB>, b, s, ev); }
-  return launch_skinny(skinny_lds_kernel<8, 4, QB>, b, s, ev);
+  if constexpr (QB == 0) {
+    return launch_skinny(skinny_lds_kernel<8, 3, QB>, b, s, ev);
+  } else {
+    return launch_skinny(skinny_lds_kernel<8, 4, QB>, b, s, ev);
+  }
 }
 
 }  // namespace
@@ -3193,7 +3203,7 @@ kernels_loadable()
       reinterpret_cast<const void*>(&skinny_lds_kernel<2, 4, 0>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<4, 4, 0>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<6, 4, 0>),
-      reinterpret_cast<const void*>(&skinny_lds_kernel<8, 4, 0>),
+      reinterpret_cast<const void*>(&skinny_lds_kernel<8, 3, 0>),
       reinterpret_cast<const void*>(&skinny_reg_kernel<1, 4>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<2, 4, 4>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<4, 4, 4>),
