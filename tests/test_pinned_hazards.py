@@ -66,19 +66,22 @@ def test_every_epilogue_has_a_pinned_kernel(kernels):
     # 4-wave GEMM: bf16, SwiGLU, int32 and dequant epilogues, 256 MFMAs
     # each; skinny GEMM: the five row-group builds (register kernel for 16
     # rows, LDS kernel for 32, 64, 96 and 128) for bf16 weights and 4- and
-    # 8-bit packs, with the DMA kernel for 16 rows of bf16 weights: 2 MFMAs
-    # (k-steps) per 16 rows and unrolled K-block, 2 blocks unrolled in the
-    # register and DMA kernels, D (the ring depth) in the LDS kernels
+    # 8-bit packs, with the DMA kernel for 16 rows of bf16 weights and the
+    # 32-column-wave build for 128 rows of bf16 weights: 2 MFMAs
+    # (k-steps) per 16 rows, 16 columns and unrolled K-block, 2 blocks
+    # unrolled in the register and DMA kernels, D (the ring depth) in the
+    # LDS kernels
     four = [n for n in kernels if "mot_gemm_kernel" in n]
     skinny = [n for n in kernels if "skinny_" in n]
-    assert len(four) == 4 and len(skinny) == 16
+    assert len(four) == 4 and len(skinny) == 17
     for n in four:
         assert sum(1 for s in kernels[n] if s.startswith("v_mfma")) == 256
     for n in skinny:
-        m = re.search(r"skinny_(reg|lds|dma)_kernelILi(\d+)E(?:Li(\d+)E)?", n)
+        m = re.search(r"skinny_(reg|lds|dma)_kernelILi(\d+)E(?:Li(\d+)ELi\d+E(?:Li(\d+)E)?)?", n)
         mt = int(m.group(2))
         depth = int(m.group(3)) if m.group(1) == "lds" else 2
-        assert sum(1 for s in kernels[n] if s.startswith("v_mfma")) == 2 * mt * depth
+        cw = int(m.group(4)) if m.group(4) else 1    # 16-column fragments per wave
+        assert sum(1 for s in kernels[n] if s.startswith("v_mfma")) == 2 * mt * depth * cw
 
 
 def _operands(s):

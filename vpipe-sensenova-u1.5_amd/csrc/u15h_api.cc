@@ -247,7 +247,40 @@ skinny_launch(u15h_ctx* ctx, const GemmBatch& b, hipStream_t s, bool noalloc,
     k.p[0].qb = static_cast<const uint16_t*>(q->biases);
   }
   for (int i = 0; i < b.nprob; ++i) { k.max_rows = std::max(k.max_rows, b.p[i].rows); }
-  k.cols = u15h::skinny_cols(k.max_rows);
+  const int K = b.kbytes / 2;
+  const int nkb = b.kbytes / 128;
+  // two resident workgroups per CU (at most 80 KiB of LDS each in the LDS
+  // kernels); a share keeps 32 K-blocks (8 per wave) in the register
+  // kernel, 16 in the LDS kernels
+  const int per_cu = 2;
+  auto blocks = [&](int cols) {
+    int cb = 0;
+    for (int i = 0; i < b.nprob; ++i) { cb += (b.p[i].n + cols - 1) / cols; }
+    return cb;
+  };
+  auto shares = [&](int cols, int cb) {
+    const int min_kb = cols == 16 ? 32 : 16;
+    int S = 1;
+    while (S < 16 && 2 * S * cb <= per_cu * ctx->num_cu &&
+           nkb / (2 * S) >= min_kb && 2 * S * k.max_rows * 8 <= K) {
+      S *= 2;
+    }
+    return S;
+  };
+  k.cols = u15h::skinny_cols(k.max_rows, k.qbits);
+  int S = shares(k.cols, blocks(k.cols));
+  // Above 96 rows, bf16 weights: waves of 32 columns (each activation
+  // fragment read from LDS serves two weight fragments), with no more K
+  // shares than 16-column waves take, where that keeps at least 3/4 of the
+  // CUs busy
+  if (u15h::skinny_wide_ok(k.max_rows, k.qbits)) {
+    const int cb2 = blocks(2 * k.cols);
+    const int S2 = std::min(shares(2 * k.cols, cb2), S);
+    if (4 * S2 * cb2 >= 3 * ctx->num_cu) {
+      k.cols *= 2;
+      S = S2;
+    }
+  }
   for (int i = 0; i < b.nprob; ++i) {
     const GemmProblem& p = b.p[i];
     u15h::SkinnyProblem& q = k.p[i];
@@ -260,18 +293,6 @@ skinny_launch(u15h_ctx* ctx, const GemmBatch& b, hipStream_t s, bool noalloc,
     q.ldy = p.ldy;
     q.cb_begin = k.total_cb;
     k.total_cb += (p.n + k.cols - 1) / k.cols;
-  }
-  const int K = b.kbytes / 2;
-  const int nkb = b.kbytes / 128;
-  // two resident workgroups per CU (64 KiB of LDS each in the LDS
-  // kernels); a share keeps 32 K-blocks (8 per wave) in the register
-  // kernel, 16 in the LDS kernels
-  const int per_cu = 2;
-  const int min_kb = k.cols == 16 ? 32 : 16;
-  int S = 1;
-  while (S < 16 && 2 * S * k.total_cb <= per_cu * ctx->num_cu &&
-         nkb / (2 * S) >= min_kb && 2 * S * k.max_rows * 8 <= K) {
-    S *= 2;
   }
   const size_t cap = noalloc ? u15h::kNoAllocScratchBytes : split_ws_capacity(ctx);
   for (;;) {

@@ -96,13 +96,15 @@ hipError_t launch_gemm_bf16(const GemmBatch& b, Epi epi, const GemmShape& g,
                             hipStream_t s, const GemmEvents& ev);
 
 // The skinny bf16 GEMM for problems of at most kSkinnyMaxRows rows: one
-// workgroup per column block (skinny_cols(max_rows) output columns: 16 up
-// to 16 rows, 64 above) and K share.  Problem p's column blocks are
+// workgroup per column block (skinny_cols(max_rows, qbits) output columns:
+// 16 up to 16 rows, 64 above; or twice that where skinny_wide_ok, 32 per
+// wave) and K share.  Problem p's column blocks are
 // [cb_begin, cb_begin + ceil(n / cols)); with S > 1 the shares' fp32
 // partial sums go to ws + ws_off as [S][rows][n] and a second kernel adds
 // them in share order, the bias, and rounds to bf16.
 constexpr int kSkinnyMaxRows = 128;
-constexpr int skinny_cols(int max_rows) { return max_rows <= 16 ? 16 : 64; }
+constexpr int skinny_cols(int max_rows, int) { return max_rows <= 16 ? 16 : 64; }
+constexpr bool skinny_wide_ok(int max_rows, int qbits) { return qbits == 0 && max_rows > 96; }
 struct SkinnyProblem {
   const void*     a;      // activation rows [rows][K] (bf16)
   const void*     w;      // weight rows [n][K] (bf16), or the pack's codes

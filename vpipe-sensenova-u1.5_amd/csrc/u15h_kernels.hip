@@ -2530,21 +2530,22 @@ skinny_dma_kernel(const SkinnyBatch B)
   }
 }
 
-// Rows 17..128: a workgroup computes 64 output columns over a K share.
-// Wave w streams weight rows [16w, 16w + 16) of the block -- into its
-// slot of a weight ring by whole-line direct loads for bf16 weights up to
-// 64 rows, into registers otherwise -- while the activation rows'
-// K-block, which all four waves use, goes to LDS by DMA through a ring of
-// D = 4 stages (one __shared__ object each, so the compiler can tell a
-// stage's DMA from another stage's reads): 48 / 64 / 64 KiB of LDS at 32 /
-// 64 / 128 rows, two workgroups per CU.
-template <int MT, int D, int QB>
+// Rows 17..128: a workgroup computes 64 CW output columns over a K share.
+// Wave w streams weight rows [16 CW w, 16 CW (w + 1)) of the block -- into
+// its slot of a weight ring by whole-line direct loads for bf16 weights,
+// into registers for packs -- while the activation rows' K-block, which
+// all four waves use, goes to LDS by DMA through a ring of D stages (one
+// __shared__ object each, so the compiler can tell a stage's DMA from
+// another stage's reads).  MT row groups of 16; with CW = 2 every
+// activation fragment read from LDS serves two weight fragments.
+template <int MT, int D, int QB, int CW>
 __device__ __forceinline__ void
 skinny_lds_tile(const SkinnyBatch& B, char* const (&xs)[D], char* const (&wsr)[D])
 {
   constexpr int kXInst = MT / 2;                    // DMA loads per wave
-  // bf16 weights up to 64 rows arrive like skinny_dma_kernel's: whole-line
-  // direct loads into the wave's slot of a D-stage weight ring
+  // bf16 weights arrive like skinny_dma_kernel's: whole-line direct loads
+  // into the wave's slot of a D-stage weight ring; packs load theirs into
+  // registers
   constexpr bool kWDma = QB == 0;
   const int S = B.split;
   const int cbg = blockIdx.x / S;
@@ -2557,10 +2558,17 @@ skinny_lds_tile(const SkinnyBatch& B, char* const (&xs)[D], char* const (&wsr)[D
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 4, r = lane & 15;
-  const int n0 = (cbg - P.cb_begin) * 64 + wave * 16;
+  const int n0 = (cbg - P.cb_begin) * 64 * CW + wave * 16 * CW;
 
-  // weight rows [n0, n0 + 16) clipped to n: rows past it read as zero
-  const SkWSrc wsrc = sk_wsrc<QB>(B, P, n0, lane);
+  // weight rows [n0 + 16c, n0 + 16c + 16) clipped to n: rows past it read
+  // as zero
+  SkWSrc wsrc[CW];
+#pragma unroll
+  for (int c = 0; c < CW; ++c) { wsrc[c] = sk_wsrc<QB>(B, P, n0 + 16 * c, lane); }
+  // the direct loads' view: rows [n0, n0 + 16 CW) clipped to n
+  const __amdgpu_buffer_rsrc_t wdr = make_rsrc(
+      static_cast<const char*>(P.w) + (size_t)min(n0, P.n) * kbytes,
+      max(0, min(16 * CW, P.n - n0)) * kbytes);
   // activation rows [0, rows): rows past them read as zero
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(P.a, P.rows * kbytes);
   // DMA: instruction j of wave w fills 16-byte stage slots
@@ -2590,34 +2598,46 @@ skinny_lds_tile(const SkinnyBatch& B, char* const (&xs)[D], char* const (&wsr)[D
           16, xv[j] + oob, ko, 0, 0);
     }
   };
-  SkW<QB> wreg[kWDma ? 1 : D];
-  int dv[2], rdo[2];
+  SkW<QB> wreg[kWDma ? 1 : D][CW];
+  // direct load j of a K-block: the wave's rows 8j .. 8j + 7, lane l
+  // landing at slot l % 8 of row 8j + l / 8 and carrying chunk
+  // (l % 8) ^ ((row / 2) % 8) (conflict-free fragment reads)
+  int dv[2 * CW], rdo[2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int row = 8 * i + (lane >> 3);
-    dv[i] = row * kbytes + (((lane & 7) ^ ((row >> 1) & 7)) << 4);
-    rdo[i] = wave * 2048 + r * 128 + (((2 * g + i) ^ ((r >> 1) & 7)) << 4);
+  for (int j = 0; j < 2 * CW; ++j) {
+    const int row = 8 * j + (lane >> 3);
+    dv[j] = row * kbytes + (((lane & 7) ^ ((row >> 1) & 7)) << 4);
+  }
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    rdo[ks] = wave * 2048 * CW + r * 128 + (((2 * g + ks) ^ ((r >> 1) & 7)) << 4);
   }
   auto issue_w = [&](int slot, int i) {
     const int oob = i < nk ? 0 : kOobOffset;
     if constexpr (kWDma) {
       const int ko = __builtin_amdgcn_readfirstlane((kb0 + min(i, nk - 1)) * 128);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < 2 * CW; ++j) {
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            wsrc.w, (__attribute__((address_space(3))) void*)(wsr[slot] + wave * 2048 + j * 1024),
+            wdr, (__attribute__((address_space(3))) void*)(wsr[slot] + wave * 2048 * CW + j * 1024),
             16, dv[j] + oob, ko, 0, 0);
       }
     } else {
-      sk_load_w<QB>(wreg[slot], wsrc, kb0 + min(i, nk - 1), oob, B.qgroup);
+#pragma unroll
+      for (int c = 0; c < CW; ++c) {
+        sk_load_w<QB>(wreg[slot][c], wsrc[c], kb0 + min(i, nk - 1), oob, B.qgroup);
+      }
     }
   };
 
-  f32x4_t acc[MT];
+  f32x4_t acc[CW][MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    acc[mt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    asm volatile("" : "+v"(acc[mt]));
+  for (int c = 0; c < CW; ++c) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      acc[c][mt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      asm volatile("" : "+v"(acc[c][mt]));
+    }
   }
   asm volatile("s_nop 4");
 
@@ -2651,7 +2671,7 @@ skinny_lds_tile(const SkinnyBatch& B, char* const (&xs)[D], char* const (&wsr)[D
   // be in flight -- the weight loads of block i + 1 and D - 2 later
   // blocks' x and weight loads (in the register prologue more follow x
   // stage i, and the wait holds more back than it needs).
-  constexpr int kWLoads = QB == 0 ? 2 : 3;          // per K-block
+  constexpr int kWLoads = (QB == 0 ? 2 : 3) * CW;   // per K-block
   constexpr int kAfterX = kWLoads + (D - 2) * (kXInst + kWLoads);
   static_assert(kAfterX < 64, "vmcnt holds at most 63");
   const int nk_pad = (nk + D - 1) / D * D;
@@ -2676,16 +2696,19 @@ skinny_lds_tile(const SkinnyBatch& B, char* const (&xs)[D], char* const (&wsr)[D
       }
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        i32x4_t wf;
-        if constexpr (kWDma) {
-          // block i's weight copies were issued before its x stage, which
-          // the barrier above has seen land
-          wf = *reinterpret_cast<const i32x4_t*>(wsr[d] + rdo[ks]);
-        } else {
-          wf = sk_frag<QB>(wreg[d], ks);
-        }
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) { sk_mfma<QB>(acc[mt], wf, xf[mt][ks]); }
+        for (int c = 0; c < CW; ++c) {
+          i32x4_t wf;
+          if constexpr (kWDma) {
+            // block i's weight copies were issued before its x stage, which
+            // the barrier above has seen land
+            wf = *reinterpret_cast<const i32x4_t*>(wsr[d] + c * 2048 + rdo[ks]);
+          } else {
+            wf = sk_frag<QB>(wreg[d][c], ks);
+          }
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) { sk_mfma<QB>(acc[c][mt], wf, xf[mt][ks]); }
+        }
       }
       // (the MFMAs consumed this block's weight reads before the refill)
       asm volatile("" ::: "memory");
@@ -2697,32 +2720,38 @@ skinny_lds_tile(const SkinnyBatch& B, char* const (&xs)[D], char* const (&wsr)[D
   asm volatile("s_waitcnt vmcnt(0)\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
                ::: "memory");
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) { asm volatile("" : "+v"(acc[mt])); }
-
-  const int n = n0 + 4 * g;
-  if (n >= P.n) { return; }
-  uint2 bb = make_uint2(0u, 0u);
-  if (S == 1 && P.bias != nullptr) { bb = *reinterpret_cast<const uint2*>(P.bias + n); }
+  for (int c = 0; c < CW; ++c) {
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = mt * 16 + r;
-    if (m >= P.rows) { continue; }
-    if (S == 1) {
-      skinny_store(P, m, n, acc[mt], bb);
-    } else {
-      float* ws = B.ws + P.ws_off + (size_t)share * P.rows * P.n;
-      *reinterpret_cast<f32x4_t*>(ws + (size_t)m * P.n + n) = acc[mt];
+    for (int mt = 0; mt < MT; ++mt) { asm volatile("" : "+v"(acc[c][mt])); }
+  }
+
+#pragma unroll
+  for (int c = 0; c < CW; ++c) {
+    const int n = n0 + 16 * c + 4 * g;
+    if (n >= P.n) { return; }
+    uint2 bb = make_uint2(0u, 0u);
+    if (S == 1 && P.bias != nullptr) { bb = *reinterpret_cast<const uint2*>(P.bias + n); }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = mt * 16 + r;
+      if (m >= P.rows) { continue; }
+      if (S == 1) {
+        skinny_store(P, m, n, acc[c][mt], bb);
+      } else {
+        float* ws = B.ws + P.ws_off + (size_t)share * P.rows * P.n;
+        *reinterpret_cast<f32x4_t*>(ws + (size_t)m * P.n + n) = acc[c][mt];
+      }
     }
   }
 }
 
-template <int MT, int D, int QB>
+template <int MT, int D, int QB, int CW = 1>
 __global__ __launch_bounds__(256) void
 skinny_lds_kernel(const SkinnyBatch B)
 {
   static_assert(D == 3 || D == 4, "a ring of 3 or 4 stages (8 measured slower)");
   constexpr int kStage = MT * 16 * 128;
-  constexpr int kWStage = QB == 0 ? 4 * 2048 : 16;   // weight ring stage
+  constexpr int kWStage = QB == 0 ? 4 * 2048 * CW : 16;   // weight ring stage
   __shared__ __attribute__((aligned(1024))) char xs0[kStage];
   __shared__ __attribute__((aligned(1024))) char xs1[kStage];
   __shared__ __attribute__((aligned(1024))) char xs2[kStage];
@@ -2734,11 +2763,11 @@ skinny_lds_kernel(const SkinnyBatch B)
   if constexpr (D == 4) {
     char* const xs[4] = {xs0, xs1, xs2, xs3};
     char* const wsr[4] = {ws0, ws1, ws2, ws3};
-    skinny_lds_tile<MT, 4, QB>(B, xs, wsr);
+    skinny_lds_tile<MT, 4, QB, CW>(B, xs, wsr);
   } else {
     char* const xs[3] = {xs0, xs1, xs2};
     char* const wsr[3] = {ws0, ws1, ws2};
-    skinny_lds_tile<MT, 3, QB>(B, xs, wsr);
+    skinny_lds_tile<MT, 3, QB, CW>(B, xs, wsr);
   }
 }
 
@@ -2843,6 +2872,7 @@ launch_skinny_q(const SkinnyBatch& b, hipStream_t s, const GemmEvents& ev)
   if (b.max_rows <= 64) { return launch_skinny(skinny_lds_kernel<4, 4, QB>, b, s, ev); }
   if (b.max_rows <= 96) { return launch_skinny(skinny_lds_kernel<6, 4, QB>, b, s, ev); }
   if constexpr (QB == 0) {
+    if (b.cols == 128) { return launch_skinny(skinny_lds_kernel<8, 4, QB, 2>, b, s, ev); }
     return launch_skinny(skinny_lds_kernel<8, 3, QB>, b, s, ev);
   } else {
     return launch_skinny(skinny_lds_kernel<8, 4, QB>, b, s, ev);
@@ -2856,7 +2886,8 @@ launch_skinny_bf16(const SkinnyBatch& b, hipStream_t s, const GemmEvents& ev)
 {
   if (b.total_cb <= 0 || b.max_rows <= 0) { return hipSuccess; }
   if (b.max_rows > kSkinnyMaxRows || b.kbytes % 128 != 0 ||
-      b.cols != skinny_cols(b.max_rows) ||
+      (b.cols != skinny_cols(b.max_rows, b.qbits) &&
+       !(skinny_wide_ok(b.max_rows, b.qbits) && b.cols == 2 * skinny_cols(b.max_rows, b.qbits))) ||
       (b.qbits != 0 && b.qgroup != 32 && b.qgroup != 64)) {
     return hipErrorInvalidValue;
   }
@@ -3204,6 +3235,7 @@ kernels_loadable()
       reinterpret_cast<const void*>(&skinny_lds_kernel<4, 4, 0>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<6, 4, 0>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<8, 3, 0>),
+      reinterpret_cast<const void*>(&skinny_lds_kernel<8, 4, 0, 2>),
       reinterpret_cast<const void*>(&skinny_reg_kernel<1, 4>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<2, 4, 4>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<4, 4, 4>),
