@@ -269,7 +269,7 @@ skinny_launch(u15h_ctx* ctx, const GemmBatch& b, hipStream_t s, bool noalloc,
   };
   k.cols = u15h::skinny_cols(k.max_rows, k.qbits);
   int S = shares(k.cols, blocks(k.cols));
-  // Above 96 rows, bf16 weights: waves of 32 columns (each activation
+  // Above 64 rows, bf16 weights: waves of 32 columns (each activation
   // fragment read from LDS serves two weight fragments), with no more K
   // shares than 16-column waves take, where that keeps at least 3/4 of the
   // CUs busy

@@ -104,7 +104,7 @@ hipError_t launch_gemm_bf16(const GemmBatch& b, Epi epi, const GemmShape& g,
 // them in share order, the bias, and rounds to bf16.
 constexpr int kSkinnyMaxRows = 128;
 constexpr int skinny_cols(int max_rows, int) { return max_rows <= 16 ? 16 : 64; }
-constexpr bool skinny_wide_ok(int max_rows, int qbits) { return qbits == 0 && max_rows > 96; }
+constexpr bool skinny_wide_ok(int max_rows, int qbits) { return qbits == 0 && max_rows > 64; }
 struct SkinnyProblem {
   const void*     a;      // activation rows [rows][K] (bf16)
   const void*     w;      // weight rows [n][K] (bf16), or the pack's codes

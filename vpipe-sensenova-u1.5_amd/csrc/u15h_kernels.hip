@@ -2870,7 +2870,10 @@ launch_skinny_q(const SkinnyBatch& b, hipStream_t s, const GemmEvents& ev)
   }
   if (b.max_rows <= 32) { return launch_skinny(skinny_lds_kernel<2, 4, QB>, b, s, ev); }
   if (b.max_rows <= 64) { return launch_skinny(skinny_lds_kernel<4, 4, QB>, b, s, ev); }
-  if (b.max_rows <= 96) { return launch_skinny(skinny_lds_kernel<6, 4, QB>, b, s, ev); }
+  if (b.max_rows <= 96) {
+    if (QB == 0 && b.cols == 128) { return launch_skinny(skinny_lds_kernel<6, 4, 0, 2>, b, s, ev); }
+    return launch_skinny(skinny_lds_kernel<6, 4, QB>, b, s, ev);
+  }
   if constexpr (QB == 0) {
     if (b.cols == 128) { return launch_skinny(skinny_lds_kernel<8, 4, QB, 2>, b, s, ev); }
     return launch_skinny(skinny_lds_kernel<8, 3, QB>, b, s, ev);
@@ -3236,6 +3239,7 @@ kernels_loadable()
       reinterpret_cast<const void*>(&skinny_lds_kernel<6, 4, 0>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<8, 3, 0>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<8, 4, 0, 2>),
+      reinterpret_cast<const void*>(&skinny_lds_kernel<6, 4, 0, 2>),
       reinterpret_cast<const void*>(&skinny_reg_kernel<1, 4>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<2, 4, 4>),
       reinterpret_cast<const void*>(&skinny_lds_kernel<4, 4, 4>),
