@@ -69,6 +69,36 @@ def test_dequant_affine_extreme_values(ops):
                           oracle.dequant_affine(codes, sc, bi, 8, 64, K))
 
 
+@pytest.mark.parametrize("bits", [8, 4])
+def test_dequant_product_rounds_before_the_bias(ops, bits):
+    """scale * code overflows to inf before the bias is added (the pack
+    fixture's multiply, then add): scale 3e38, code 2, bias -3e38 gives
+    +inf, where a fused multiply-add would give 3e38.  Checked on the
+    expansion against the oracle, and on the direct route (M < 96) against
+    the dense GEMM of that expansion, whose one non-zero activation meets
+    the weights' inf (and the zero activations make NaNs)."""
+    N, K, G = 16, 128, 64
+    per = 32 // bits
+    word = sum(2 << (bits * e) for e in range(per))
+    codes = np.full((N, K * bits // 32), word, np.uint32)
+    sc = oracle.f32_to_bf16(np.full((N, K // G), 3e38, np.float32))
+    bi = oracle.f32_to_bf16(np.full((N, K // G), -3e38, np.float32))
+    ref = oracle.dequant_affine(codes, sc, bi, bits, G, K)
+    assert np.all(ref == 0x7F80)                     # the oracle: +inf
+    qw = qpack(codes, sc, bi, bits, G)
+    w = torch.empty(N, K, dtype=torch.bfloat16, device="cuda")
+    ops.dequant_affine(qw, N, K, w)
+    x = torch.zeros(1, K, dtype=torch.bfloat16, device="cuda")
+    x[0, 0] = 1.0
+    y = torch.empty(1, N, dtype=torch.bfloat16, device="cuda")
+    y2 = torch.empty_like(y)
+    ops.linear_q(x, qw, None, y, 1, K, N)
+    ops.linear(x, w, None, y2, 1, K, N)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_bits(w), ref)
+    assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
+
+
 @pytest.mark.parametrize("M", [1, 8, 32, 64, 96, 128, 160, 192, 256, 512, 1024])
 def test_linear_q_reference_w8g64(ops, M):
     """test_gemm_q (tests/u15-m5-test.cc:313-366): K=4096, N=6144, G=64,

@@ -1357,8 +1357,10 @@ swiglu_kernel(const uint4* __restrict__ g, const uint4* __restrict__ u,
 
 // ---- affine-quantized weights: dequant once to bf16 ----------------------
 // One thread per u32 code word (32/BITS codes of one row): w = scale * code
-// + bias of the code's group, a multiply then an add in f32 (no fused
-// multiply-add, so the rounding is the pack fixture's), rounded to bf16.
+// + bias of the code's group, a multiply then an add in f32 (contraction
+// into a fused multiply-add is switched off: it would round differently
+// from the pack fixture's arithmetic where the product is subnormal),
+// rounded to bf16 to nearest even by v_cvt_pk_bf16_f32.
 template <int BITS>
 __global__ __launch_bounds__(256) void
 dequant_affine_kernel(const uint32_t* __restrict__ codes,
@@ -1381,9 +1383,10 @@ dequant_affine_kernel(const uint32_t* __restrict__ codes,
   uint32_t out[kPer / 2];
 #pragma unroll
   for (int e = 0; e < kPer; e += 2) {
-    const float v0 = __fadd_rn(__fmul_rn(s, (float)((word >> (e * BITS)) & kMask)), b);
-    const float v1 = __fadd_rn(__fmul_rn(s, (float)((word >> ((e + 1) * BITS)) & kMask)), b);
-    out[e / 2] = bf16_bits(v0) | (bf16_bits(v1) << 16);
+    float p0 = s * (float)((word >> (e * BITS)) & kMask);
+    float p1 = s * (float)((word >> ((e + 1) * BITS)) & kMask);
+    asm("" : "+v"(p0), "+v"(p1));     // the products stay rounded: no fma
+    out[e / 2] = pack_bf16x2(p0 + b, p1 + b);
   }
   uint16_t* dst = w + (size_t)n * K + k0;
   if constexpr (BITS == 8) {
@@ -2233,9 +2236,11 @@ sk_frag(const SkW<QB>& d, int ks)
         c0 = ((uint32_t)d.c[ks] >> (e * 4)) & kMask;
         c1 = ((uint32_t)d.c[ks] >> ((e + 1) * 4)) & kMask;
       }
-      const float v0 = __fadd_rn(__fmul_rn(sc, (float)c0), bi);
-      const float v1 = __fadd_rn(__fmul_rn(sc, (float)c1), bi);
-      f[e >> 1] = (int)(bf16_bits(v0) | (bf16_bits(v1) << 16));
+      // a multiply, then an add (not fused), as dequant_affine_kernel
+      float p0 = sc * (float)c0;
+      float p1 = sc * (float)c1;
+      asm("" : "+v"(p0), "+v"(p1));
+      f[e >> 1] = (int)pack_bf16x2(p0 + bi, p1 + bi);
     }
     return f;
   }
