@@ -190,18 +190,30 @@ def step_work(m_und, m_gen, layers):
     quant_bytes = (3 * in_elems + 4 * 4 * M) * layers        # bf16 in, int8 + scale out
     return {"flop": flop, "bf16_bytes": bf16_bytes, "i8_bytes": i8_bytes,
             "quant_bytes": quant_bytes, "gemm_launches": 4 * layers,
-            "quant_launches": 4 * layers}
+            "quant_launches": 4 * layers, "max_rows": max(m_und, m_gen)}
 
 
-def kernel_label(int8):
+def kernel_label(int8, max_rows=None):
     """The GEMM kernel instance the library's environment knobs select
-    (read at u15h_create, as the library reads them)."""
+    (read at u15h_create, as the library reads them) for a step whose
+    largest group has `max_rows` rows: bf16 batches of at most 128 rows per
+    problem take the skinny kernels (the build by row count; above 64 rows
+    the planner picks 16- or 32-column waves per launch)."""
     def env(name, dflt):
         v = os.environ.get(name, "")
         try:
             return int(v) if v else dflt
         except ValueError:
             return dflt
+    if not int8 and max_rows is not None and max_rows <= 128 and env("U15H_SKINNY", 1):
+        if max_rows <= 16:
+            return "skinny_dma_kernel<1>"
+        for top, mt, d in ((32, 2, 4), (64, 4, 4)):
+            if max_rows <= top:
+                return f"skinny_lds_kernel<{mt}, {d}, 0, 1>"
+        if max_rows <= 96:
+            return "skinny_lds_kernel<6, 4, 0, 1|2>"
+        return "skinny_lds_kernel<8, 3, 0, 1> | <8, 4, 0, 2>"
     epi = "kDequantBf16" if int8 else "kBf16"
     if env("U15H_WAVES", 8) == 4:
         return f"mot_gemm_kernel<{'MmaI8x16' if int8 else 'MmaBf16x16'}, {epi}, 2>"
@@ -395,7 +407,7 @@ def tier_result(work, ms, k, steps, int8, traffic):
     gbps = nbytes / (kern_ms * 1e-3) / 1e9
     peak, unit = (PEAK_I8, "TOPS") if int8 else (PEAK_BF16, "TFLOP/s")
     roof = dict(_roof(flop_launch, nbytes, rate, gbps, peak, unit),
-                traffic=traffic, kernel=kernel_label(int8),
+                traffic=traffic, kernel=kernel_label(int8, work.get("max_rows")),
                 avg_launch_ms=round(kern_ms, 5), flop_per_launch=flop_launch,
                 alg_bytes_per_launch=int(nbytes), achieved_GBps=round(gbps, 1),
                 split_reduce_ms_per_step=round(k["post_ms"] / steps, 5))
@@ -406,7 +418,8 @@ def tier_result(work, ms, k, steps, int8, traffic):
         q_launch_ms = k["pre_ms"] / (work["quant_launches"] * steps)
         q_bytes = work["quant_bytes"] / work["quant_launches"]
         out["quant_kernel"] = {
-            "kernel": "quant_rows_i8_kernel", "bound": "hbm",
+            "kernel": "quant_rows_i8_kernel<2> (K 4096) | quant_rows_i8_wide_kernel (K 12288)",
+            "bound": "hbm",
             "avg_launch_ms": round(q_launch_ms, 5),
             "alg_bytes_per_launch": int(q_bytes),
             "achieved_GBps": round(q_bytes / (q_launch_ms * 1e-3) / 1e9, 1),

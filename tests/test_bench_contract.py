@@ -147,6 +147,23 @@ def test_kernel_label_follows_the_knobs(monkeypatch):
     assert bench.kernel_label(True) == "mot_gemm_kernel<MmaI8x16, kDequantBf16, 4>"
 
 
+def test_kernel_label_names_the_skinny_route(monkeypatch):
+    """bf16 steps whose groups all have <= 128 rows run the skinny kernels
+    (the build by rows); int8, larger groups and U15H_SKINNY=0 the tiled
+    kernel."""
+    for k in ("U15H_WAVES", "U15H_MFMA16", "U15H_SKINNY"):
+        monkeypatch.delenv(k, raising=False)
+    assert bench.kernel_label(False, 1) == "skinny_dma_kernel<1>"
+    assert bench.kernel_label(False, 64) == "skinny_lds_kernel<4, 4, 0, 1>"
+    assert bench.kernel_label(False, 128).startswith("skinny_lds_kernel<8")
+    assert bench.kernel_label(False, 129) == "mot_gemm_kernel<MmaBf16x16, kBf16, 4>"
+    assert bench.kernel_label(True, 128) == "mot_gemm_kernel<MmaI8x16, kDequantBf16, 4>"
+    assert bench.step_work(128, 0, 1)["max_rows"] == 128
+    assert bench.step_work(128, 4096, 1)["max_rows"] == 4096
+    monkeypatch.setenv("U15H_SKINNY", "0")
+    assert bench.kernel_label(False, 128) == "mot_gemm_kernel<MmaBf16x16, kBf16, 4>"
+
+
 def test_small_m_rotates_past_the_cache():
     """Below the ridge a pass cycles more than twice the 256 MB Infinity
     Cache of weights; above it one layer is the step."""
