@@ -142,6 +142,38 @@ def test_masked_with_query_offset(ops, mode):
     assert rel_l2(host_f32(out), ref) < BAR
 
 
+@pytest.mark.parametrize("pre", [64, 70])
+def test_block_causal_image_blocks(ops, pre):
+    """Image blocks of 256 tokens after a text prefix, as in the generation
+    pass: each 128-query workgroup lies in one block, so the tiles of its
+    block past the causal frontier are wholly visible and skip the mask
+    when all 64 of their keys carry the block's t (prefix 64: tiles align
+    with the blocks); with prefix 70 the tiles straddle the prefix and the
+    block boundaries and keep the mask.  Two blocks, so the second block's
+    keys stay hidden from the first block's queries."""
+    hq, hkv, d = 4, 2, 128
+    tq = 512
+    tk = pre + tq
+    cap = tk + 3
+    rng = np.random.default_rng(pre)
+    qb = oracle.f32_to_bf16(rng.standard_normal((hq, tq, d)).astype(np.float32))
+    kb = bf16_cache(rng.standard_normal((hkv, tk, d)).astype(np.float32), cap)
+    vb = bf16_cache(rng.standard_normal((hkv, tk, d)).astype(np.float32), cap)
+    t_idx = np.concatenate([np.arange(pre), pre + np.arange(tq) // 256]).astype(np.int32)
+    q = dev_bf16(qb)
+    out = torch.empty_like(q)
+    ops.sdpa_block_causal(q, dev_bf16(kb), dev_bf16(vb), out,
+                          torch.from_numpy(t_idx).cuda(), hkv, tk, pre)
+    torch.cuda.synchronize()
+    ref = oracle.attention(widen(qb), widen(kb), widen(vb), hkv, tk, "block_causal",
+                           t_idx, q_offset=pre)
+    causal = oracle.attention(widen(qb), widen(kb), widen(vb), hkv, tk, "causal",
+                              t_idx, q_offset=pre)
+    got = host_f32(out)
+    assert rel_l2(got, ref) < BAR
+    assert rel_l2(got, causal) > 1e-2          # the blocks are load-bearing
+
+
 def test_model_shape_generation_pass(ops):
     """Config 2's generation pass: 32 query heads over 8 kv heads, 4096 gen
     queries against the 128-token frozen prefix plus themselves

@@ -1728,6 +1728,9 @@ attention_kernel(const AttnArgs A)
   __shared__ __attribute__((aligned(16))) uint16_t vs0[BK * D];
   __shared__ __attribute__((aligned(16))) uint16_t vs1[BK * D];
   __shared__ int32_t ts[3][BK];
+  // block-causal: whether every key of the tile in ts[i] carries the one t
+  // all the workgroup's queries share (then the tile needs no mask)
+  __shared__ int32_t tsame[3];
 
   // Work item: (query head, 128-query tile), ordered kv head first, so
   // that cutting the list into 8 runs (one per XCD, workgroups b, b+8, ...
@@ -1813,9 +1816,15 @@ attention_kernel(const AttnArgs A)
       }
     }
   };
+  int t_wg = INT_MIN;        // block-causal: the queries' one t, or INT_MIN
   auto store_t = [&](int tbuf) {
     if constexpr (MODE == 2) {
-      if (tid < BK) { ts[tbuf][tid] = tr; }
+      if (tid < BK) {
+        ts[tbuf][tid] = tr;
+        // wave 0 holds the tile's 64 t entries, one per lane
+        const bool same = __all(tr == t_wg && t_wg != INT_MIN);
+        if (tid == 0) { tsame[tbuf] = same; }
+      }
     }
   };
 
@@ -1865,6 +1874,7 @@ attention_kernel(const AttnArgs A)
       tmin = min(tmin, kred[0][w]);
       tmax = max(tmax, kred[1][w]);
     }
+    if (tmin == tmax) { t_wg = tmin; }
     int jm = kend - 1;
 #pragma unroll 8
     for (int j = kend + tid; j < A.tk; j += 64 * NWV) {
@@ -1885,7 +1895,9 @@ attention_kernel(const AttnArgs A)
   // -inf for the scores of tile j0 that the mode hides; a no-op for a tile
   // whose keys are all below tk and (causal masks) the first query
   auto mask = [&](f32x16_t (&s)[2], int j0, int tbuf) {
-    const bool full = j0 + BK <= A.tk && (MODE == 0 || j0 + BK - 1 <= q_first);
+    bool full = j0 + BK <= A.tk && (MODE == 0 || j0 + BK - 1 <= q_first);
+    // block-causal: every key of the tile shares the queries' one t
+    if constexpr (MODE == 2) { full = full || (j0 + BK <= A.tk && tsame[tbuf] != 0); }
     if (full) { return; }
     // branch-free: every lane reads its t entry (kl < 64 is in bounds) and
     // the conditions combine bitwise, so the mask is a select
