@@ -474,64 +474,101 @@ gemm_epilogue_staged(const GemmProblem& P, const TileWork& t, int wm, int wn,
       sam[j] = scl[wm * 128 + j * kF + lr];
     }
   }
-  // Every wave is past its last fragment read of the main loop.
-  __syncthreads();
-  char* const half = wm ? ring[1] : ring[0];
-  auto put = [&](int row, int col, uint32_t lo, uint32_t hi) {
-    // row within the half (0..127), col = first of 4 output columns
-    const int c = col >> 3;
-    char* p = half + row * RB + ((c ^ (row % CH)) << 4) + ((col & 7) << 1);
-    *reinterpret_cast<u32x2_t*>(p) = u32x2_t{lo, hi};
-  };
+  // The tile's results in bf16 (bias or SwiGLU applied) are computed
+  // before the barrier: a wave that leaves the main loop early converts
+  // while its partner still issues MFMAs, and only the LDS writes wait
+  // (bf16 step 0.35% faster, interleaved, one box).  There the bias test
+  // is taken once, outside the loops: inside them its branches split the
+  // code into blocks the held results spill across.
+  constexpr int KC = E == Epi::kSwiglu ? (FI / 2) * kGr : FI * kGr;
+  u32x2_t pk[kScaled ? 1 : FJ][KC];
+  // bias: 0 none, 1 added, 2 tested per group (the dequant epilogue's
+  // original form, whose registers fit only that way)
+  auto convert = [&](auto bias_mode, auto&& emit) {
+    constexpr int kBias = decltype(bias_mode)::value;
 #pragma unroll
-  for (int j = 0; j < FJ; ++j) {
-    const int row = j * kF + lr;
-    if constexpr (E == Epi::kSwiglu) {
+    for (int j = 0; j < FJ; ++j) {
+      if constexpr (E == Epi::kSwiglu) {
 #pragma unroll
-      for (int i = 0; i < FI / 2; ++i) {
+        for (int i = 0; i < FI / 2; ++i) {
 #pragma unroll
-        for (int g = 0; g < kGr; ++g) {
-          const int col = wn * (NW / 2) + i * kF + g * kGs + lh * 4;
-          const auto& ga = acc[i][j];
-          const auto& ua = acc[i + FI / 2][j];
-          put(row, col,
-              pack_bf16x2(swiglu_f(ga[g * 4 + 0], ua[g * 4 + 0]),
-                          swiglu_f(ga[g * 4 + 1], ua[g * 4 + 1])),
-              pack_bf16x2(swiglu_f(ga[g * 4 + 2], ua[g * 4 + 2]),
-                          swiglu_f(ga[g * 4 + 3], ua[g * 4 + 3])));
+          for (int g = 0; g < kGr; ++g) {
+            const auto& ga = acc[i][j];
+            const auto& ua = acc[i + FI / 2][j];
+            emit(j, i * kGr + g, u32x2_t{
+                pack_bf16x2(swiglu_f(ga[g * 4 + 0], ua[g * 4 + 0]),
+                            swiglu_f(ga[g * 4 + 1], ua[g * 4 + 1])),
+                pack_bf16x2(swiglu_f(ga[g * 4 + 2], ua[g * 4 + 2]),
+                            swiglu_f(ga[g * 4 + 3], ua[g * 4 + 3]))});
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < FI; ++i) {
+#pragma unroll
+          for (int g = 0; g < kGr; ++g) {
+            const int c = i * kGr + g;
+            const auto& a = acc[i][j];
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              if constexpr (kScaled) {
+                v[e] = (float)bits_as<int>(a[g * 4 + e]);
+              } else {
+                v[e] = a[g * 4 + e];
+              }
+            }
+            if constexpr (kScaled) {
+              v[0] = (v[0] * sam[j]) * swn[c].x;
+              v[1] = (v[1] * sam[j]) * swn[c].y;
+              v[2] = (v[2] * sam[j]) * swn[c].z;
+              v[3] = (v[3] * sam[j]) * swn[c].w;
+            }
+            if (kBias == 1 || (kBias == 2 && has_bias)) {
+              v[0] += bf16_to_f32(bia[c].x & 0xffffu);
+              v[1] += bf16_to_f32(bia[c].x >> 16);
+              v[2] += bf16_to_f32(bia[c].y & 0xffffu);
+              v[3] += bf16_to_f32(bia[c].y >> 16);
+            }
+            emit(j, c, u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])});
+          }
         }
       }
+    }
+  };
+  // The dequant epilogue converts after the barrier, writing each group
+  // as it goes: held until then, its packed results beside its scales
+  // overflow the registers.
+  char* const half = wm ? ring[1] : ring[0];
+  // LDS address of the 4 output columns from `col` of row `row` (within
+  // the half)
+  auto put_at = [&](int row, int col) {
+    const int c = col >> 3;
+    return half + row * RB + ((c ^ (row % CH)) << 4) + ((col & 7) << 1);
+  };
+  auto col_of = [&](int cg) {
+    const int i = cg / kGr, g = cg % kGr;
+    return (E == Epi::kSwiglu ? wn * (NW / 2) : wn * NW) + i * kF + g * kGs + lh * 4;
+  };
+  if constexpr (kScaled) {
+    __syncthreads();
+    convert(std::integral_constant<int, 2>{}, [&](int j, int cg, u32x2_t v) {
+      *reinterpret_cast<u32x2_t*>(put_at(j * kF + lr, col_of(cg))) = v;
+    });
+  } else {
+    auto hold = [&](int j, int cg, u32x2_t v) { pk[j][cg] = v; };
+    if (has_bias) {
+      convert(std::integral_constant<int, 1>{}, hold);
     } else {
+      convert(std::integral_constant<int, 0>{}, hold);
+    }
+    // Every wave is past its last fragment read of the main loop.
+    __syncthreads();
 #pragma unroll
-      for (int i = 0; i < FI; ++i) {
+    for (int j = 0; j < FJ; ++j) {
 #pragma unroll
-        for (int g = 0; g < kGr; ++g) {
-          const int c = i * kGr + g;
-          const int col = wn * NW + i * kF + g * kGs + lh * 4;
-          const auto& a = acc[i][j];
-          float v[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if constexpr (kScaled) {
-              v[e] = (float)bits_as<int>(a[g * 4 + e]);
-            } else {
-              v[e] = a[g * 4 + e];
-            }
-          }
-          if constexpr (kScaled) {
-            v[0] = (v[0] * sam[j]) * swn[c].x;
-            v[1] = (v[1] * sam[j]) * swn[c].y;
-            v[2] = (v[2] * sam[j]) * swn[c].z;
-            v[3] = (v[3] * sam[j]) * swn[c].w;
-          }
-          if (has_bias) {
-            v[0] += bf16_to_f32(bia[c].x & 0xffffu);
-            v[1] += bf16_to_f32(bia[c].x >> 16);
-            v[2] += bf16_to_f32(bia[c].y & 0xffffu);
-            v[3] += bf16_to_f32(bia[c].y >> 16);
-          }
-          put(row, col, pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-        }
+      for (int cg = 0; cg < KC; ++cg) {
+        *reinterpret_cast<u32x2_t*>(put_at(j * kF + lr, col_of(cg))) = pk[j][cg];
       }
     }
   }
