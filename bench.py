@@ -139,13 +139,19 @@ TRAFFIC_FILES = {
     (1, 128, 4096): REPO / "profiles" / "mot_gemm_bf16_c2_traffic.txt",
     (2, 128, 0): REPO / "profiles" / "mot_gemm_bf16_und128_traffic.txt",
 }
+# the same for the int8 grouped GEMM (fused dequant)
+TRAFFIC_FILES_I8 = {
+    (1, 128, 4096): REPO / "profiles" / "mot_gemm_i8_c2_traffic.txt",
+}
 
 
-def measured_traffic(args):
-    """HBM bytes per launch of the bf16 grouped GEMM, as the committed
-    rocprof FETCH_SIZE / WRITE_SIZE summary of this token split records them
-    (scaled by a plain copy of known size), or None if not measured."""
-    f = TRAFFIC_FILES.get((args.layers, args.m_und, args.m_gen))
+def measured_traffic(args, int8=False):
+    """HBM bytes per launch of the bf16 (or int8) grouped GEMM, as the
+    committed rocprof FETCH_SIZE / WRITE_SIZE summary of this token split
+    records them (scaled by a plain copy of known size), or None if not
+    measured."""
+    files = TRAFFIC_FILES_I8 if int8 else TRAFFIC_FILES
+    f = files.get((args.layers, args.m_und, args.m_gen))
     if f is None:
         return None
     try:
@@ -909,7 +915,8 @@ def main(argv=None):
                           layers=args.layers)
         ms8 = timed_step(torch, runs8, args.steps, args.warmup)
         k8 = timed_kernels(torch, ops, runs8, args.steps)
-        result["int8"] = tier_result(work, ms8, k8, args.steps, True, None)
+        result["int8"] = tier_result(work, ms8, k8, args.steps, True,
+                                     measured_traffic(args, int8=True))
         arms["int8"] = runs8
     result["samples"] = interleaved(torch, arms, args.steps, args.rounds)
     if args.ab:

@@ -73,6 +73,14 @@ def test_committed_traffic_figures():
     assert und >= _layer_bytes(128, 0) / 4
     assert bench.measured_traffic(_Args(42, 128, 4096)) is None
     assert bench.measured_traffic(_Args(1, 4352, 12288)) is None
+    # the int8 kernel's figure is its own, at least its algorithmic bytes
+    # (int8 weights and codes, f32 scales, bf16 output) and below bf16's
+    c2_i8 = bench.measured_traffic(_Args(1, 128, 4096), int8=True)
+    assert c2_i8 is not None and c2_i8 != c2
+    work = bench.step_work(128, 4096, 1)
+    assert c2_i8 >= work["i8_bytes"] / work["gemm_launches"]
+    assert c2_i8 < c2
+    assert bench.measured_traffic(_Args(2, 128, 0), int8=True) is None
 
 
 def test_more_than_one_gpu_is_refused():
