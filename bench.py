@@ -85,9 +85,10 @@ def parse(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    # Each tier's per-launch pass runs before its timed block, so even 5
-    # warmup steps time the steady state (1260-1264 TFLOP/s against
-    # 1264-1273 with 50; with the timed block first, 5 gave 1222-1229).
+    # The per-launch passes and the interleaved samples run before the
+    # timed blocks, so even 5 warmup steps time the steady state (with the
+    # timed block first, 5 gave 1222-1229 TFLOP/s against 1264-1273 with
+    # 50).
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c2",
                     help="c2: one layer, 128 und + 4096 gen tokens (the "
@@ -886,11 +887,18 @@ def main(argv=None):
 
     runs = step_runs(u15h, ops, model, io, mu, mg, u15h.TIER_BF16,
                      args.fused_swiglu, args.layers)
-    # The per-launch pass runs first: `steps` real steps that leave the GPU
-    # in the workload's steady state (clocks under the MFMA power draw, the
-    # layer's pages mapped), so a short warm-up does not put the ramp into
-    # the contract's block.
+    arms = {"bf16": runs}
+    if want_i8:
+        arms["int8"] = step_runs(u15h, ops, model, io, mu, mg, u15h.TIER_I8,
+                                 layers=args.layers)
+    # The per-launch passes and the interleaved samples run first: real
+    # steps that leave the GPU in the workload's steady state (clocks under
+    # the MFMA power draw, the layer's pages mapped), so a short warm-up does
+    # not put the ramp into the contract's blocks.
     k16 = timed_kernels(torch, ops, runs, args.steps)
+    if want_i8:
+        k8 = timed_kernels(torch, ops, arms["int8"], args.steps)
+    samples = interleaved(torch, arms, args.steps, args.rounds)
     ms = timed_step(torch, runs, args.steps, args.warmup)     # the contract's block
     bf16 = tier_result(work, ms, k16, args.steps, False, measured_traffic(args))
     _, _, _, wdesc = WORKLOADS[args.workload]
@@ -914,16 +922,11 @@ def main(argv=None):
         "pct_of_peak": bf16["pct_of_peak"],
         "roofline": bf16["roofline"],
     }
-    arms = {"bf16": runs}
     if want_i8:
-        runs8 = step_runs(u15h, ops, model, io, mu, mg, u15h.TIER_I8,
-                          layers=args.layers)
-        k8 = timed_kernels(torch, ops, runs8, args.steps)
-        ms8 = timed_step(torch, runs8, args.steps, args.warmup)
+        ms8 = timed_step(torch, arms["int8"], args.steps, args.warmup)
         result["int8"] = tier_result(work, ms8, k8, args.steps, True,
                                      measured_traffic(args, int8=True))
-        arms["int8"] = runs8
-    result["samples"] = interleaved(torch, arms, args.steps, args.rounds)
+    result["samples"] = samples
     if args.ab:
         result["ab"] = ab_compare(torch, u15h, ops, args.ab, model, io, args,
                                   want_i8)
