@@ -186,3 +186,17 @@ def test_small_m_rotates_past_the_cache():
     assert a.layers == 2
     assert bench.parse([]).layers == 1
     assert bench.parse(["--workload", "c5"]).layers == 42
+
+
+def test_timed_blocks_follow_the_warming_passes():
+    """The contract's timed blocks (timed_step with args.warmup) run after
+    the per-launch passes and the interleaved samples, so the driver's
+    5-step warm-up times the steady state (with the timed block first, 5
+    warmup steps measured 3.5% slow)."""
+    import inspect
+    src = inspect.getsource(bench.main)
+    first_timed = src.index("timed_step(torch, runs, args.steps, args.warmup)")
+    assert src.index("timed_kernels(torch, ops, runs, args.steps)") < first_timed
+    assert src.index("interleaved(torch, arms, args.steps, args.rounds)") < first_timed
+    assert src.index('timed_kernels(torch, ops, arms["int8"], args.steps)') < first_timed
+    assert first_timed < src.index('timed_step(torch, arms["int8"], args.steps, args.warmup)')
