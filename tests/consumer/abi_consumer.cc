@@ -1,11 +1,11 @@
 // abi_consumer.cc -- TEST PROGRAM: a C++ caller of include/u15h.h, linked
-// against libu15h.so the way a reference build would link it (see the
-// C++ sketch in INTEGRATION.md), with the CPU oracle (liboracle.so) as the
-// checker.
+// against libu15h.so the way a reference build would link it (the
+// reference's layer step calling the C ABI in place of MetalOps), with the
+// CPU oracle (liboracle.so) as the checker.
 //
 // It runs, on config 1's split (64 und + 192 gen rows, hidden 4096):
-//   1. the sketch's grouped call: q, k and v of both experts in ONE
-//      u15h_mot_linear launch;
+//   1. the grouped call a layer step makes: q, k and v of both experts in
+//      ONE u15h_mot_linear launch;
 //   2. MetalOps::linear's replacement, u15h_linear, on the o projection of
 //      the gen expert;
 //   3. the layer stack: all 14 matrices bound by the reference's tensor
@@ -148,7 +148,7 @@ main()
       up((size_t)M * I * 2), down((size_t)M * H * 2);
   auto W = [&](int e, int p) { return wd[e][p]->as<const u15h_bf16>(); };
 
-  // ---- 1. the sketch: q, k, v of both experts in one grouped launch ------
+  // ---- 1. q, k, v of both experts in one grouped launch -----------------
   u15h_mot_proj qkv[3] = {
       {W(0, 0), W(1, 0), nullptr, nullptr, q.as<u15h_bf16>(), NH * HD},
       {W(0, 1), W(1, 1), nullptr, nullptr, k.as<u15h_bf16>(), KV * HD},

@@ -1,6 +1,6 @@
 """A compiled C++ caller of the C ABI (tests/consumer/abi_consumer.cc,
 built against include/u15h.h and libu15h.so by __graft_entry__.build()):
-the grouped q|k|v call of the integration sketch, u15h_linear, and the
+the grouped q|k|v call a layer step makes, u15h_linear, and the
 layer stack bound by the reference's tensor names, each checked by the
 program itself against the CPU oracle."""
 import pathlib
