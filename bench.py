@@ -90,6 +90,11 @@ def parse(argv=None):
     # timed block first, 5 gave 1222-1229 TFLOP/s against 1264-1273 with
     # 50).
     ap.add_argument("--warmup", type=int, default=50)
+    # ... and at least this long: a short warm-up (the driver's 5 steps)
+    # times a colder state (5 steps before the timed block measured
+    # 1222-1229 TFLOP/s against 1264-1273 with 50).  The line reports the
+    # untimed steps actually run before each timed block.
+    ap.add_argument("--warmup-ms", type=float, default=300.0)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c2",
                     help="c2: one layer, 128 und + 4096 gen tokens (the "
                          "headline); c4: one layer, edit + CFG, 4352 und + "
@@ -297,6 +302,26 @@ def step_runs(u15h, ops, model, io, mu, mg, tier, fused=False, layers=None):
     return runs
 
 
+def warm(torch, runs, warmup, min_ms):
+    """`warmup` untimed steps, then more until at least `min_ms` of host
+    time has passed since the first (checked after each synchronised
+    batch), so the timed block starts in the workload's steady state
+    (clocks under the MFMA power draw) whatever --warmup says.  Returns
+    the number of untimed steps run."""
+    t0 = time.perf_counter()
+    n = 0
+    batch = max(1, warmup)
+    while True:
+        for _ in range(batch):
+            for r in runs:
+                r()
+        n += batch
+        torch.cuda.synchronize()
+        if (time.perf_counter() - t0) * 1e3 >= min_ms:
+            return n
+        batch = max(1, n)
+
+
 def timed_step(torch, runs, steps, warmup):
     """`steps` steps of `runs` between two events on the launch stream
     (after `warmup` untimed steps), synchronised on both sides, nothing else
@@ -368,10 +393,56 @@ class HipEvents:
             raise RuntimeError("hipEventElapsedTime failed")
         return ms.value
 
+    def elapsed_or_zero(self, a, b):
+        """elapsed(a, b), or 0 for a pair the library never recorded (its
+        kernel did not run in that call)."""
+        ms = self.ct.c_float()
+        if self.hip.hipEventElapsedTime(self.ct.byref(ms), a, b) != 0:
+            # clear the thread's last-error state, which the failed query
+            # set and the next hipGetLastError() would otherwise report
+            self.hip.hipGetLastError()
+            return 0.0
+        return ms.value
+
     def close(self):
         for ev in self.pool:
             self.hip.hipEventDestroy(ev)
         self.pool = []
+
+
+def timed_step_kernels(torch, ops, runs, steps, hev):
+    """`steps` steps with every call's quantiser, GEMM kernel and reduction
+    kernel timed by events bound to those kernels' own dispatches (their
+    start and end timestamps, as a kernel trace reports them; the
+    library's u15h_profile_next_kernels).  Returns this pass's ms per step
+    and the summed kernel times.  The binding costs the stream some
+    time between kernels (this pass's step runs ~2% longer than an
+    unprofiled one), so the contract's block is timed separately, right
+    after this pass, without it."""
+    stream = torch.cuda.current_stream()
+    pairs = [[(hev.create(), hev.create()) for _ in range(3)]
+             for _ in range(steps * len(runs))]
+    torch.cuda.synchronize()
+    t0, t1 = hev.create(), hev.create()
+    hev.record(t0, stream)
+    i = 0
+    for _ in range(steps):
+        for r in runs:
+            q, g, red = pairs[i]
+            ops.profile_next_kernels(quant=q, gemm=g, reduce=red)
+            r()
+            i += 1
+    hev.record(t1, stream)
+    torch.cuda.synchronize()
+    ms = hev.elapsed(t0, t1) / steps
+    gemm = pre = post = 0.0
+    for q, g, red in pairs:
+        gemm += hev.elapsed(*g)
+        pre += hev.elapsed_or_zero(*q)      # no quantiser in a bf16 call
+        post += hev.elapsed_or_zero(*red)   # no split tail in some calls
+    hev.close()
+    return ms, {"gemm_ms": gemm, "pre_ms": pre, "post_ms": post,
+                "calls": len(pairs)}
 
 
 def timed_kernels(torch, ops, runs, steps):
@@ -419,6 +490,12 @@ def tier_result(work, ms, k, steps, int8, traffic):
                 avg_launch_ms=round(kern_ms, 5), flop_per_launch=flop_launch,
                 alg_bytes_per_launch=int(nbytes), achieved_GBps=round(gbps, 1),
                 split_reduce_ms_per_step=round(k["post_ms"] / steps, 5))
+    # The bracketed pass runs after the timed block, in the same steady
+    # state: its kernels (GEMMs, quantisers before them, split-K reductions
+    # after them) must fit inside a step of the timed block.
+    kernels_ms = (k["gemm_ms"] + k["pre_ms"] + k["post_ms"]) / steps
+    roof["kernels_ms_per_step"] = round(kernels_ms, 5)
+    roof["fits_step"] = bool(kernels_ms <= ms)
     out = {"value": round(flop / (ms * 1e-3) / 1e12, 2), "unit": unit,
            "pct_of_peak": round(100 * flop / (ms * 1e-3) / 1e12 / peak, 2),
            "ms_per_step": round(ms, 4), "roofline": roof}
@@ -426,7 +503,7 @@ def tier_result(work, ms, k, steps, int8, traffic):
         q_launch_ms = k["pre_ms"] / (work["quant_launches"] * steps)
         q_bytes = work["quant_bytes"] / work["quant_launches"]
         out["quant_kernel"] = {
-            "kernel": "quant_rows_i8_kernel<2> (K 4096) | quant_rows_i8_wide_kernel (K 12288)",
+            "kernel": "quant_rows_i8_waves_kernel<4, 2, 1> (K 4096) | quant_rows_i8_wide_kernel (K 12288)",
             "bound": "hbm",
             "avg_launch_ms": round(q_launch_ms, 5),
             "alg_bytes_per_launch": int(q_bytes),
@@ -437,13 +514,15 @@ def tier_result(work, ms, k, steps, int8, traffic):
 
 def stack_passes(torch, u15h, ops, model, gen, args, want_i8):
     """Config 5: one pass over the whole resident stack (u15h_stack_forward)
-    at 128 + 4096 and at 128 + 1024 tokens, both tiers, interleaved rounds
-    (medians)."""
+    at 128 + 4096 and at 128 + 1024 tokens, and the und-only prefill at 128
+    + 0 (below the ridge: the 42 layers' 16.2 GB of und weights are the
+    traffic, so it is also reported against 8 TB/s), both tiers,
+    interleaved rounds (medians)."""
     res = {"layers": model.n_layers, "weight_sets": 2 * model.n_layers,
            "resident_bf16_GB": round(2 * LAYER_WEIGHT_BYTES * model.n_layers / 1e9, 2),
            "resident_int8_GB": round(LAYER_WEIGHT_BYTES * model.n_layers / 1e9, 2)
            if want_i8 else 0.0}
-    for mu, mg in ((128, 4096), (128, 1024)):
+    for mu, mg in ((128, 4096), (128, 1024), (128, 0)):
         t, io = make_io(torch, u15h, gen, mu + mg)
         arms = {"bf16": [lambda: ops.stack_forward(model.stack, io, mu, mg,
                                                    u15h.TIER_BF16)]}
@@ -464,6 +543,12 @@ def stack_passes(torch, u15h, ops, model, gen, args, want_i8):
                          "pct_of_peak": round(100 * rate / peak, 2),
                          "achieved_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
                          "min_ms": g["min_ms"], "max_ms": g["max_ms"]}
+            if max(mu, mg) < PEAK_BF16 / PEAK_HBM * 1e3:
+                # below the ridge (M FLOP per bf16 weight byte, 2M int8 ops
+                # per int8 weight byte; both ridges at M ~ 315): the
+                # weights bound it
+                one[tier]["bound"] = "hbm"
+                one[tier]["hbm_frac"] = round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM, 4)
         res[f"m{mu}_{mg}"] = one
         del t, io
     return res
@@ -891,22 +976,31 @@ def main(argv=None):
     if want_i8:
         arms["int8"] = step_runs(u15h, ops, model, io, mu, mg, u15h.TIER_I8,
                                  layers=args.layers)
-    # The per-launch passes and the interleaved samples run first: real
-    # steps that leave the GPU in the workload's steady state (clocks under
-    # the MFMA power draw, the layer's pages mapped), so a short warm-up does
-    # not put the ramp into the contract's blocks.
-    k16 = timed_kernels(torch, ops, runs, args.steps)
+    # The contract's block: the warm-up (at least --warmup steps and
+    # --warmup-ms of time), then exactly --steps steps.  The interleaved
+    # samples and the per-launch brackets follow, in the same steady state,
+    # so the per-launch kernel times add up to at most a step.
+    # Per tier: the warm-up (at least --warmup steps and --warmup-ms of
+    # time), the per-kernel pass, then the contract's block of exactly
+    # --steps steps, unprofiled, in the same steady state.  The kernels of
+    # the profiled pass must add up to at most a step of the block.
+    n_warm = warm(torch, runs, args.warmup, args.warmup_ms)
+    pms16, k16 = timed_step_kernels(torch, ops, runs, args.steps, HipEvents())
+    ms = timed_step(torch, runs, args.steps, 0)
     if want_i8:
-        k8 = timed_kernels(torch, ops, arms["int8"], args.steps)
+        n_warm8 = warm(torch, arms["int8"], args.warmup, args.warmup_ms)
+        pms8, k8 = timed_step_kernels(torch, ops, arms["int8"], args.steps,
+                                      HipEvents())
+        ms8 = timed_step(torch, arms["int8"], args.steps, 0)
     samples = interleaved(torch, arms, args.steps, args.rounds)
-    ms = timed_step(torch, runs, args.steps, args.warmup)     # the contract's block
     bf16 = tier_result(work, ms, k16, args.steps, False, measured_traffic(args))
     _, _, _, wdesc = WORKLOADS[args.workload]
 
     result = {
         "metric": "MoT proj GEMM bf16 TFLOP/s + int8 TOPS at 4096 tok; % of MFMA peak",
         "value": bf16["value"], "unit": "TFLOP/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup,
+        "steps": args.steps, "warmup": n_warm,
+        "warmup_requested": args.warmup, "warmup_min_ms": args.warmup_ms,
         "ms_per_step": bf16["ms_per_step"], "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights, "
@@ -920,12 +1014,13 @@ def main(argv=None):
                    "fused_swiglu": bool(args.fused_swiglu),
                    "entry": "u15h_stack_layer"},
         "pct_of_peak": bf16["pct_of_peak"],
-        "roofline": bf16["roofline"],
+        "roofline": dict(bf16["roofline"], profiled_pass_ms_per_step=round(pms16, 5)),
     }
     if want_i8:
-        ms8 = timed_step(torch, arms["int8"], args.steps, args.warmup)
         result["int8"] = tier_result(work, ms8, k8, args.steps, True,
                                      measured_traffic(args, int8=True))
+        result["int8"]["warmup"] = n_warm8
+        result["int8"]["roofline"]["profiled_pass_ms_per_step"] = round(pms8, 5)
     result["samples"] = samples
     if args.ab:
         result["ab"] = ab_compare(torch, u15h, ops, args.ab, model, io, args,

@@ -93,7 +93,12 @@ const char* u15h_last_error(const u15h_ctx* ctx);
  * If the int8 tier is on (u15h_enable_i8_gemm) and the shape qualifies
  * (M >= the tier's row floor, K % 128 == 0) the call is served by the int8
  * path with per-call quantisation of both operands -- the interception
- * MetalOps::linear_mma_ makes (src/u15-metal-ops.cc:283-306).  At most 128
+ * MetalOps::linear_mma_ makes (src/u15-metal-ops.cc:283-306).  The K rule
+ * differs from the reference's on purpose: its tier quantises per 512-wide
+ * group of K and so takes only K % 512 == 0 (src/u15-metal-ops.h:76-83);
+ * this tier's scales are per token and per output channel (no K groups),
+ * so any K its 128-byte LDS stages divide qualifies.  Every projection of
+ * the model (K = 4096, 12288) passes both rules.  At most 128
  * rows with K % 64 == 0 run a weight-streaming kernel (16 or 64 output
  * columns per workgroup) instead of the 256 x 256 tiles.
  * Limits: M >= 0, N > 0, K > 0, K % 8 == 0, N % 8 == 0. */
@@ -481,7 +486,9 @@ u15h_status u15h_stack_set(u15h_stack* st, int layer, int expert, int proj,
  * ExpertLayer::complete, src/u15-weights.cc:333-339): every layer's seven
  * matrices of the und expert (need_und) and/or the gen expert (need_gen),
  * bf16 (tier 0) or int8 (tier 1).  On EINVAL, `missing` (if not NULL)
- * receives the reference name of the first unbound matrix. */
+ * receives the reference name of the first unbound matrix, or, for the
+ * int8 tier, why the stack's widths do not fit it (every projection's K
+ * must be a multiple of 128 and at most 131072). */
 u15h_status u15h_stack_check(const u15h_stack* st, int need_und,
                              int need_gen, int tier, char* missing,
                              size_t missing_cap);
@@ -532,7 +539,11 @@ u15h_status u15h_stack_layer(u15h_ctx* ctx, u15h_stream stream,
 
 /* Every layer's projection steps in order, layer after layer, on the
  * same io buffers: forward_many's layer loop (src/u15-backbone.cc:
- * 386-426) with the non-projection ops of layer_step_ left out. */
+ * 386-426) with the non-projection ops of layer_step_ left out.  There is
+ * no stop hook between layers: the reference's cooperative per-layer stop
+ * (src/u15-backbone.cc:394-397) belongs to a caller that loops
+ * u15h_stack_layer itself and checks its flag between the calls.  Only
+ * the last layer's outputs survive in io. */
 u15h_status u15h_stack_forward(u15h_ctx* ctx, u15h_stream stream,
                                const u15h_stack* st, const u15h_layer_io* io,
                                int M_und, int M_gen, int tier, int flags);
@@ -543,17 +554,29 @@ u15h_status u15h_stack_forward(u15h_ctx* ctx, u15h_stream stream,
 
 /* Profiling hook; no counterpart in the reference (whose perf test times
  * whole command buffers, tests/u15-perf-test.cc:63-110).  `event` is a
- * hipEvent_t: the next GEMM launched through this context records it on
- * that call's stream right after the GEMM kernel and before any split-K
- * reduction kernel, then forgets it -- so a caller brackets the GEMM
- * kernel alone between its own event and this one.  NULL cancels. */
+ * hipEvent_t: the next GEMM launched through this context completes it
+ * with the GEMM kernel's own end timestamp (the event is bound to the
+ * kernel's dispatch, hipExtLaunchKernel; no extra packet on the stream),
+ * before any split-K reduction kernel, then forgets it.  NULL cancels. */
 u15h_status u15h_profile_next_gemm(u15h_ctx* ctx, void* event);
-/* The same with a second event recorded right BEFORE the next GEMM kernel
- * (after any quantisation the same call launches first), so the pair
- * brackets exactly that kernel.  Either may be NULL.  No reference
- * counterpart. */
+/* The same with a second event taking the next GEMM kernel's START
+ * timestamp (after any quantisation the same call launches first), so the
+ * pair times exactly that kernel's execution, as a kernel trace does.
+ * Either may be NULL.  No reference counterpart. */
 u15h_status u15h_profile_bracket_next_gemm(u15h_ctx* ctx, void* before,
                                            void* after);
+/* The general form (hipEvent_t pairs, each bound to one kernel's start and
+ * end timestamps): the next quantiser launched through this context
+ * (u15h_quant_rows_i8, as the stack's int8 steps call it), the next GEMM
+ * kernel, and that GEMM call's reduction kernel (split-K tail or skinny
+ * K shares).  A pair whose kernel does not run in that call is never
+ * recorded.  Every pending pair is dropped once the next GEMM call has
+ * launched.  Any may be NULL.  No reference counterpart: it lets a caller
+ * sum exactly the kernel time of its own timed steps. */
+u15h_status u15h_profile_next_kernels(u15h_ctx* ctx, void* quant_start,
+                                      void* quant_end, void* gemm_start,
+                                      void* gemm_end, void* reduce_start,
+                                      void* reduce_end);
 
 /* ------------------------------------------------------------------ */
 /* per-token routing                                                   */

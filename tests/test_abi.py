@@ -169,3 +169,64 @@ def test_stack_refusals_without_a_device():
     assert lib.u15h_stack_layer(None, None, h, 0, ctypes.byref(io), 0, 1, 15, 0, 0) == u15h.EINVAL
     assert lib.u15h_stack_forward(None, None, h, ctypes.byref(io), 0, 1, 0, 0) == u15h.EINVAL
     lib.u15h_stack_destroy(h)
+
+
+def test_stack_check_refuses_int8_widths_past_the_gemm_limit():
+    """An int8-tier pass over a stack whose widths exceed u15h_mot_gemm_i8's
+    K limits is refused by the stack's own check, which the pass runs before
+    its first launch (so no step's quantiser runs before a later step
+    would refuse)."""
+    big = u15h.Stack(1, hidden=4096, heads=32, kv_heads=8, head_dim=128,
+                     inter=131072 + 128)
+    assert "at most 131072" in big.check(tier=u15h.TIER_I8)
+    # the bf16 tier has no such limit: it reports the first unbound matrix
+    assert big.check().endswith("q_proj.weight")
+    big.close()
+    odd = u15h.Stack(1, hidden=4096 + 64, heads=32, kv_heads=8, head_dim=128,
+                     inter=12288)
+    assert "multiple of 128" in odd.check(tier=u15h.TIER_I8)
+    odd.close()
+
+
+def test_stack_io_is_checked_against_the_stack_before_the_call():
+    """Ops.stack_layer / stack_forward check every io buffer the requested
+    steps and tier use (the C ABI cannot see sizes): short, mistyped or
+    missing buffers raise before anything is launched.  Host tensors of
+    the right shapes pass the shape checks and stop at the device check."""
+    import torch
+    st = u15h.Stack(1, hidden=64, heads=2, kv_heads=1, head_dim=32, inter=128)
+    M = 5
+
+    def bufs(**over):
+        b = dict(x=torch.zeros(M, 64, dtype=torch.bfloat16),
+                 q=torch.zeros(M, 64, dtype=torch.bfloat16),
+                 k=torch.zeros(M, 32, dtype=torch.bfloat16),
+                 v=torch.zeros(M, 32, dtype=torch.bfloat16),
+                 xq=torch.zeros(M, 128, dtype=torch.int8),
+                 sx=torch.zeros(M, dtype=torch.float32))
+        b.update(over)
+        return {k: v for k, v in b.items() if v is not None}
+
+    def check(steps=u15h.STEP_QKV, tier=u15h.TIER_BF16, **over):
+        u15h._check_io(st, u15h.layer_io(**bufs(**over)), M, steps, tier, 0)
+
+    with pytest.raises(ValueError, match="shape"):       # q one column short
+        check(q=torch.zeros(M, 63, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="shape"):       # one row short
+        check(k=torch.zeros(M - 1, 32, dtype=torch.bfloat16))
+    with pytest.raises(TypeError):                       # f32 output
+        check(v=torch.zeros(M, 32, dtype=torch.float32))
+    with pytest.raises(ValueError, match="required"):    # missing output
+        check(v=None)
+    with pytest.raises(ValueError, match="required"):    # o step: no attn
+        check(steps=u15h.STEP_O)
+    with pytest.raises(ValueError, match="xq"):          # int8: xq too narrow
+        check(tier=u15h.TIER_I8, xq=torch.zeros(M, 64, dtype=torch.int8))
+    with pytest.raises(ValueError, match="GPU"):         # shapes right, host memory
+        check()
+    with pytest.raises(ValueError, match="unknown"):
+        u15h.layer_io(xx=torch.zeros(1))
+    # an io not made by layer_io carries no tensors to check
+    with pytest.raises(ValueError, match="layer_io"):
+        u15h._check_io(st, u15h._LayerIO(), M, u15h.STEP_QKV, u15h.TIER_BF16, 0)
+    st.close()

@@ -188,15 +188,54 @@ def test_small_m_rotates_past_the_cache():
     assert bench.parse(["--workload", "c5"]).layers == 42
 
 
-def test_timed_blocks_follow_the_warming_passes():
-    """The contract's timed blocks (timed_step with args.warmup) run after
-    the per-launch passes and the interleaved samples, so the driver's
-    5-step warm-up times the steady state (with the timed block first, 5
-    warmup steps measured 3.5% slow)."""
+def test_timed_blocks_follow_their_kernel_pass():
+    """Per tier: the warm-up (at least --warmup steps and --warmup-ms of
+    time; the line reports the steps actually run), the per-kernel pass
+    (events bound to the kernels' dispatches), then the contract's block,
+    unprofiled, in the same steady state; the interleaved samples follow."""
     import inspect
     src = inspect.getsource(bench.main)
-    first_timed = src.index("timed_step(torch, runs, args.steps, args.warmup)")
-    assert src.index("timed_kernels(torch, ops, runs, args.steps)") < first_timed
-    assert src.index("interleaved(torch, arms, args.steps, args.rounds)") < first_timed
-    assert src.index('timed_kernels(torch, ops, arms["int8"], args.steps)') < first_timed
-    assert first_timed < src.index('timed_step(torch, arms["int8"], args.steps, args.warmup)')
+    w16 = src.index("warm(torch, runs, args.warmup, args.warmup_ms)")
+    k16 = src.index("timed_step_kernels(torch, ops, runs, args.steps")
+    t16 = src.index("timed_step(torch, runs, args.steps, 0)")
+    w8 = src.index('warm(torch, arms["int8"], args.warmup, args.warmup_ms)')
+    k8 = src.index('timed_step_kernels(torch, ops, arms["int8"], args.steps')
+    t8 = src.index('timed_step(torch, arms["int8"], args.steps, 0)')
+    inter = src.index("interleaved(torch, arms, args.steps, args.rounds)")
+    assert w16 < k16 < t16 < w8 < k8 < t8 < inter
+    assert '"warmup": n_warm' in src
+    assert bench.parse([]).warmup_ms >= 100
+    body = inspect.getsource(bench.timed_step_kernels)
+    assert "profile_next_kernels" in body
+
+
+def test_warm_runs_at_least_the_requested_steps_and_time():
+    class _T:       # a torch stand-in: synchronize only
+        class cuda:
+            @staticmethod
+            def synchronize():
+                pass
+    calls = []
+    n = bench.warm(_T, [lambda: calls.append(1)], 5, 0.0)
+    assert n == 5 and len(calls) == 5
+    import time as _time
+    slow = [lambda: _time.sleep(0.002)]
+    n = bench.warm(_T, slow, 1, 30.0)
+    assert n >= 8          # 30 ms of 2 ms steps, in doubling batches
+
+
+@pytest.mark.parametrize("int8", [False, True])
+def test_tier_result_checks_that_the_kernels_fit_the_step(int8):
+    """launches x avg_launch_ms + reductions (+ quantisers) against the
+    timed step: fits_step says whether the bracketed kernels add up to at
+    most a step."""
+    w = bench.step_work(128, 4096, 1)
+    steps = 4
+    k = {"gemm_ms": 0.30 * 4 * steps, "pre_ms": (0.015 * 4 * steps) if int8 else 0.0,
+         "post_ms": 0.02 * steps, "calls": 4 * steps}
+    per_step = (k["gemm_ms"] + k["pre_ms"] + k["post_ms"]) / steps
+    ok = bench.tier_result(w, per_step * 1.01, k, steps, int8, None)["roofline"]
+    assert ok["fits_step"] and ok["kernels_ms_per_step"] == pytest.approx(per_step)
+    assert ok["avg_launch_ms"] * 4 + ok["split_reduce_ms_per_step"] <= per_step * 1.01
+    bad = bench.tier_result(w, per_step * 0.97, k, steps, int8, None)["roofline"]
+    assert not bad["fits_step"]

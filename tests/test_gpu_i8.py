@@ -112,11 +112,12 @@ def test_quant_rows_codes_stay_in_range(ops):
     assert np.array_equal(qh[1], qo[1])
 
 
-# 8 and 136: fewer chunks than threads; 4096: every register slot of the
-# two-chunk build; 4104: the six-chunk build; 8200: past 8192 but not a
-# multiple of 16 (six chunks); 8208, 12288 and 16384: the 512-thread build
-# (partial, typical, full); 16400: six chunks and a second read
-@pytest.mark.parametrize("K", [8, 136, 4096, 4104, 8200, 8208, 12288, 16384, 16400])
+# The four-wave builds: 8, 136 and 2048 (one chunk per lane: partial and
+# full), 2056 and 4096 (two), 4104 and 8192 (four); 8200: past 8192 but
+# not a multiple of 16 (the six-chunk row kernel); 8208, 12288 and 16384:
+# the 512-thread build (partial, typical, full); 16400: six chunks and a
+# second read
+@pytest.mark.parametrize("K", [8, 136, 2048, 2056, 4096, 4104, 8192, 8200, 8208, 12288, 16384, 16400])
 def test_quant_rows_other_widths(ops, K):
     rng = np.random.default_rng(K)
     xb = rand_bf16_bits(rng, (33, K))

@@ -1,6 +1,6 @@
 """The int8 quantiser's no-division fast path, emulated on the CPU.
 
-The device kernel (quant_rows_i8_kernel / quant8) does not divide each
+The device kernels (quant_rows_i8_*_kernel / quant8) does not divide each
 element by the row scale s = absmax / 127.  It forms the biased code
 u = fma(x, 1/s, 128), rounds it, and redoes a chunk with the division only
 when some element lies near a half-integer.  That shortcut is exact only

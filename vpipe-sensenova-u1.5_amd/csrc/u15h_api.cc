@@ -30,10 +30,11 @@ struct u15h_ctx {
   // GEMM kernel build: 8 or 4 waves per workgroup (env U15H_WAVES) and the
   // 8-wave build's MFMA shape (env U15H_MFMA16).
   u15h::GemmShape gemm = {8, 0, 1};
-  // One-shot profiling events: recorded right before and right after the
-  // next GEMM kernel.
-  hipEvent_t profile_before = nullptr;
-  hipEvent_t profile_event = nullptr;
+  // One-shot profiling events, bound to the next launches of a quantiser,
+  // a GEMM kernel and its reduction (start and end of each); all dropped
+  // when the next GEMM call has launched.
+  hipEvent_t prof_quant[2] = {nullptr, nullptr};
+  u15h::GemmEvents prof_gemm;
   // Partial-sum workspace of split tiles: at most num_cu K shares of one
   // 256x256 tile each (allocated on first use, kept until destroy).
   void* split_ws = nullptr;
@@ -95,14 +96,24 @@ bind_device(u15h_ctx* ctx)
   return U15H_OK;
 }
 
-// The profiling events of the next GEMM launch (one-shot).
+// The profiling events of the next GEMM launch (one-shot: taking them
+// drops every pending profiling event, the quantiser's included).
 u15h::GemmEvents
 take_profile_event(u15h_ctx* ctx)
 {
-  const u15h::GemmEvents e = {ctx->profile_before, ctx->profile_event};
-  ctx->profile_before = nullptr;
-  ctx->profile_event = nullptr;
+  const u15h::GemmEvents e = ctx->prof_gemm;
+  ctx->prof_gemm = u15h::GemmEvents{};
+  ctx->prof_quant[0] = ctx->prof_quant[1] = nullptr;
   return e;
+}
+
+// The profiling events of the next quantiser launch (one-shot).
+void
+take_quant_events(u15h_ctx* ctx, hipEvent_t* start, hipEvent_t* end)
+{
+  *start = ctx->prof_quant[0];
+  *end = ctx->prof_quant[1];
+  ctx->prof_quant[0] = ctx->prof_quant[1] = nullptr;
 }
 
 u15h_status
@@ -249,16 +260,16 @@ skinny_launch(u15h_ctx* ctx, const GemmBatch& b, hipStream_t s, bool noalloc,
   for (int i = 0; i < b.nprob; ++i) { k.max_rows = std::max(k.max_rows, b.p[i].rows); }
   const int K = b.kbytes / 2;
   const int nkb = b.kbytes / 128;
-  // two resident workgroups per CU (at most 80 KiB of LDS each in the LDS
-  // kernels); a share keeps 32 K-blocks (8 per wave) in the register
-  // kernel, 16 in the LDS kernels
-  const int per_cu = 2;
+  // Resident workgroups per CU: two for the 16-column-wave builds (at most
+  // 80 KiB of LDS each), one for the 32-column-wave builds (112-128 KiB).
+  // A share keeps 32 K-blocks (8 per wave) in the register kernel, 16 in
+  // the LDS kernels.
   auto blocks = [&](int cols) {
     int cb = 0;
     for (int i = 0; i < b.nprob; ++i) { cb += (b.p[i].n + cols - 1) / cols; }
     return cb;
   };
-  auto shares = [&](int cols, int cb) {
+  auto shares = [&](int cols, int cb, int per_cu) {
     const int min_kb = cols == 16 ? 32 : 16;
     int S = 1;
     while (S < 16 && 2 * S * cb <= per_cu * ctx->num_cu &&
@@ -268,14 +279,14 @@ skinny_launch(u15h_ctx* ctx, const GemmBatch& b, hipStream_t s, bool noalloc,
     return S;
   };
   k.cols = u15h::skinny_cols(k.max_rows, k.qbits);
-  int S = shares(k.cols, blocks(k.cols));
+  int S = shares(k.cols, blocks(k.cols), 2);
   // Above 64 rows, bf16 weights: waves of 32 columns (each activation
   // fragment read from LDS serves two weight fragments), with no more K
   // shares than 16-column waves take, where that keeps at least 3/4 of the
-  // CUs busy
+  // CUs busy (one such workgroup per CU)
   if (u15h::skinny_wide_ok(k.max_rows, k.qbits)) {
     const int cb2 = blocks(2 * k.cols);
-    const int S2 = std::min(shares(2 * k.cols, cb2), S);
+    const int S2 = std::min(shares(2 * k.cols, cb2, 1), S);
     if (4 * S2 * cb2 >= 3 * ctx->num_cu) {
       k.cols *= 2;
       S = S2;
@@ -294,7 +305,10 @@ skinny_launch(u15h_ctx* ctx, const GemmBatch& b, hipStream_t s, bool noalloc,
     q.cb_begin = k.total_cb;
     k.total_cb += (p.n + k.cols - 1) / k.cols;
   }
-  const size_t cap = noalloc ? u15h::kNoAllocScratchBytes : split_ws_capacity(ctx);
+  // One cap for both destinations, so u15h_mot_linear and
+  // u15h_mot_linear_noalloc pick the same share count (and the same bits)
+  // on every GPU.
+  const size_t cap = std::min(u15h::kNoAllocScratchBytes, split_ws_capacity(ctx));
   for (;;) {
     k.split = S;
     if (S == 1 || u15h::skinny_ws_floats(k) * 4 <= cap) { break; }
@@ -746,9 +760,22 @@ u15h_profile_next_gemm(u15h_ctx* ctx, void* event)
 u15h_status
 u15h_profile_bracket_next_gemm(u15h_ctx* ctx, void* before, void* after)
 {
+  return u15h_profile_next_kernels(ctx, nullptr, nullptr, before, after,
+                                   nullptr, nullptr);
+}
+
+u15h_status
+u15h_profile_next_kernels(u15h_ctx* ctx, void* quant_start, void* quant_end,
+                          void* gemm_start, void* gemm_end, void* reduce_start,
+                          void* reduce_end)
+{
   if (ctx == nullptr) { return U15H_EINVAL; }
-  ctx->profile_before = static_cast<hipEvent_t>(before);
-  ctx->profile_event = static_cast<hipEvent_t>(after);
+  ctx->prof_quant[0] = static_cast<hipEvent_t>(quant_start);
+  ctx->prof_quant[1] = static_cast<hipEvent_t>(quant_end);
+  ctx->prof_gemm.before = static_cast<hipEvent_t>(gemm_start);
+  ctx->prof_gemm.after = static_cast<hipEvent_t>(gemm_end);
+  ctx->prof_gemm.red_before = static_cast<hipEvent_t>(reduce_start);
+  ctx->prof_gemm.red_after = static_cast<hipEvent_t>(reduce_end);
   return U15H_OK;
 }
 
@@ -774,8 +801,10 @@ u15h_quant_rows_i8(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
   }
   u15h_status st = bind_device(ctx);
   if (st != U15H_OK) { return st; }
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  take_quant_events(ctx, &e0, &e1);
   return launched(
-      ctx, u15h::launch_quant_rows_i8(x, rows, K, q, s, as_stream(stream)),
+      ctx, u15h::launch_quant_rows_i8(x, rows, K, q, s, as_stream(stream), e0, e1),
       "quant_rows_i8");
 }
 

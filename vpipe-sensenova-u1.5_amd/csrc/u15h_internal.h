@@ -88,9 +88,14 @@ struct GemmShape {
 // Profiling events of one GEMM launch: `before`, when not null, is
 // recorded on the launch stream right before the GEMM kernel, `after`
 // right after it and before any split-K reduction kernel.
+// Profiling events bound to kernel dispatches (hipExtLaunchKernel: each
+// takes its kernel's start or end timestamp; no packet of its own).  Null
+// members are not recorded.
 struct GemmEvents {
-  hipEvent_t before;
-  hipEvent_t after;
+  hipEvent_t before = nullptr;        // GEMM kernel start
+  hipEvent_t after = nullptr;         // GEMM kernel end
+  hipEvent_t red_before = nullptr;    // split-K / skinny reduction start
+  hipEvent_t red_after = nullptr;     // its end
 };
 hipError_t launch_gemm_bf16(const GemmBatch& b, Epi epi, const GemmShape& g,
                             hipStream_t s, const GemmEvents& ev);
@@ -147,7 +152,9 @@ hipError_t launch_skinny_bf16(const SkinnyBatch& b, hipStream_t s,
 hipError_t launch_gemm_i8(const GemmBatch& b, Epi epi, const GemmShape& g,
                           hipStream_t s, const GemmEvents& ev);
 hipError_t launch_quant_rows_i8(const uint16_t* x, int rows, int K,
-                                int8_t* q, float* sc, hipStream_t s);
+                                int8_t* q, float* sc, hipStream_t s,
+                                hipEvent_t start = nullptr,
+                                hipEvent_t end = nullptr);
 hipError_t launch_swiglu(const uint16_t* g, const uint16_t* u, uint16_t* o,
                          int64_t n, hipStream_t s);
 hipError_t launch_dequant_affine(const uint32_t* codes, const uint16_t* sc,

@@ -210,6 +210,22 @@ run_step(u15h_ctx* ctx, u15h_stream s, const u15h_stack* st, int layer,
   return u15h_mot_linear(ctx, s, in, M_und, M_gen, K, p, np);
 }
 
+// The int8 tier's limits on the stack's widths, each some projection's K:
+// u15h_mot_gemm_i8's K % 128 == 0 and K <= 131072 (int32 accumulators stay
+// exact).  Checked before a pass's first launch, so no step's quantiser or
+// GEMM runs before a later step would refuse.
+const char*
+i8_widths_error(const u15h_stack* st)
+{
+  if (st->hidden % 128 || st->qdim % 128 || st->inter % 128) {
+    return "int8 tier: every projection's K must be a multiple of 128";
+  }
+  if (st->hidden > 131072 || st->qdim > 131072 || st->inter > 131072) {
+    return "int8 tier: every projection's K must be at most 131072";
+  }
+  return nullptr;
+}
+
 // Arguments of a stack call; nullptr if they are acceptable, else why not.
 const char*
 check_call(const u15h_stack* st, const u15h_layer_io* io, int M_und,
@@ -225,9 +241,8 @@ check_call(const u15h_stack* st, const u15h_layer_io* io, int M_und,
   if (tier == U15H_TIER_I8 && (flags & U15H_FUSED_SWIGLU)) {
     return "the fused SwiGLU epilogue is a bf16-tier option";
   }
-  if (tier == U15H_TIER_I8 &&
-      (st->hidden % 128 || st->qdim % 128 || st->inter % 128)) {
-    return "int8 tier: every projection's K must be a multiple of 128";
+  if (tier == U15H_TIER_I8) {
+    if (const char* why = i8_widths_error(st)) { return why; }
   }
   if (M_und + M_gen > 0 && !io_ok(io, steps, tier, flags)) {
     return "an io buffer the steps need is null or not 16-byte aligned";
@@ -373,6 +388,14 @@ u15h_stack_check(const u15h_stack* st, int need_und, int need_gen, int tier,
 {
   if (st == nullptr || (tier != U15H_TIER_BF16 && tier != U15H_TIER_I8)) {
     return U15H_EINVAL;
+  }
+  if (tier == U15H_TIER_I8) {
+    if (const char* why = i8_widths_error(st)) {
+      if (missing != nullptr && missing_cap > 0) {
+        std::snprintf(missing, missing_cap, "%s", why);
+      }
+      return U15H_EINVAL;
+    }
   }
   for (int l = 0; l < st->n_layers; ++l) {
     for (int e = 0; e < 2; ++e) {

@@ -99,6 +99,7 @@ def load_library() -> ctypes.CDLL:
         "u15h_i8_min_m": (i, [vp]),
         "u15h_profile_next_gemm": (i, [vp, vp]),
         "u15h_profile_bracket_next_gemm": (i, [vp, vp, vp]),
+        "u15h_profile_next_kernels": (i, [vp, vp, vp, vp, vp, vp, vp]),
         "u15h_quant_rows_i8": (i, [vp, vp, vp, i, i, vp, vp]),
         "u15h_mot_gemm_i8_i32": (i, [vp, vp, vp, i, i, i,
                                      ctypes.POINTER(_MotProjI8), i]),
@@ -272,12 +273,77 @@ class Stack:
 
 
 def layer_io(**bufs):
-    """A u15h_layer_io from torch tensors (missing entries are NULL)."""
+    """A u15h_layer_io from torch tensors (missing entries are NULL).  The
+    tensors ride along (`io.tensors`) so that Ops.stack_layer and
+    Ops.stack_forward can check them against the stack before the call."""
+    unknown = set(bufs) - {n for n, _ in _LayerIO._fields_}
+    if unknown:
+        raise ValueError(f"layer_io: unknown buffers {sorted(unknown)}")
     io = _LayerIO()
     for name, _ in _LayerIO._fields_:
         t = bufs.get(name)
         setattr(io, name, None if t is None else t.data_ptr())
+    io.tensors = dict(bufs)
     return io
+
+
+# Which io buffers a step reads and writes, with their widths (a function
+# of the stack): (name, width) pairs; the int8 tier adds xq and sx.
+def _step_buffers(stack, step, fused):
+    H, Q, KV, I = stack.hidden, stack.qdim, stack.kvdim, stack.inter
+    if step == STEP_QKV:
+        return [("x", H), ("q", Q), ("k", KV), ("v", KV)]
+    if step == STEP_O:
+        return [("attn", Q), ("o", H)]
+    if step == STEP_GATE_UP:
+        return [("x2", H), ("h", I)] if fused else \
+            [("x2", H), ("gate", I), ("up", I)]
+    return [("h", I), ("down", H)]
+
+
+def _check_io(stack, io, M, steps, tier, flags):
+    """Every io buffer the steps use: bf16 [M][width], contiguous, on the
+    GPU; int8 tier: xq int8 [M][>= the widest K], sx f32 [M].  The C ABI
+    cannot see sizes, so a short buffer would be written past its end."""
+    tensors = getattr(io, "tensors", None)
+    if tensors is None:
+        raise ValueError("io must come from u15h.layer_io()")
+    if M == 0:
+        return
+    # The io's pointers are fixed when it is made, so a passed check holds
+    # for every later call with the same shapes (the bench's timed loop
+    # calls the stack per step).
+    key = (stack.hidden, stack.qdim, stack.kvdim, stack.inter, M, steps,
+           tier, flags)
+    done = io.__dict__.setdefault("checked", set())
+    if key in done:
+        return
+    fused = bool(flags & FUSED_SWIGLU)
+    want = []
+    for b in range(4):
+        step = 1 << b
+        if steps & step:
+            want += [(f"io.{n}", tensors.get(n), torch.bfloat16, (M, w))
+                     for n, w in _step_buffers(stack, step, fused)]
+    if tier == TIER_I8:
+        xq = tensors.get("xq")
+        kmax = max(stack.hidden, stack.qdim, stack.inter)
+        if xq is None or xq.dtype != torch.int8 or xq.dim() != 2 or \
+                xq.shape[0] != M or xq.shape[1] < kmax:
+            raise ValueError(f"io.xq must be an int8 tensor [{M}][>= {kmax}]")
+        want += [("io.xq", xq, torch.int8, tuple(xq.shape)),
+                 ("io.sx", tensors.get("sx"), torch.float32, (M,))]
+    # sizes of every buffer first (the usual mistake), then placement
+    for name, t, dtype, shape in want:
+        if t is None:
+            raise ValueError(f"{name} is required")
+        if t.dtype != dtype:
+            raise TypeError(f"{name}: dtype {t.dtype}, expected {dtype}")
+        if tuple(t.shape) != tuple(shape):
+            raise ValueError(f"{name}: shape {tuple(t.shape)}, expected {tuple(shape)}")
+    for name, t, dtype, shape in want:
+        _need(t, dtype, shape, name)
+    done.add(key)
 
 
 def build_rope_tables(pos_t, pos_h, pos_w, head_dim, d_t, d_h,
@@ -645,6 +711,19 @@ class Ops:
                                                              h(after)),
                     "u15h_profile_bracket_next_gemm")
 
+    def profile_next_kernels(self, quant=(None, None), gemm=(None, None),
+                             reduce=(None, None)):
+        """Bind raw hipEvent_t pairs to the start and end timestamps of the
+        next quantiser, GEMM kernel and reduction kernel launched through
+        this context (u15h_profile_next_kernels)."""
+        def h(e):
+            if e is None or isinstance(e, ctypes.c_void_p):
+                return e
+            return ctypes.c_void_p(e)
+        self._check(self._lib.u15h_profile_next_kernels(
+            self._ctx, h(quant[0]), h(quant[1]), h(gemm[0]), h(gemm[1]),
+            h(reduce[0]), h(reduce[1])), "u15h_profile_next_kernels")
+
     # ---- the step after the q/k projections -------------------------------
     def _head(self, x, heads, head_dim):
         tokens = x.shape[0]
@@ -767,6 +846,7 @@ class Ops:
                     tier=TIER_BF16, flags=0, stream=None):
         """One layer's projection steps (u15h_stack_layer); `io` from
         layer_io()."""
+        _check_io(stack, io, M_und + M_gen, steps, tier, flags)
         st = self._lib.u15h_stack_layer(self._ctx, _stream(stream), stack._h,
                                         layer, ctypes.byref(io), M_und, M_gen,
                                         steps, tier, flags)
@@ -775,6 +855,7 @@ class Ops:
     def stack_forward(self, stack, io, M_und, M_gen, tier=TIER_BF16, flags=0,
                       stream=None):
         """Every layer's projection steps in order (u15h_stack_forward)."""
+        _check_io(stack, io, M_und + M_gen, STEP_ALL, tier, flags)
         st = self._lib.u15h_stack_forward(self._ctx, _stream(stream), stack._h,
                                           ctypes.byref(io), M_und, M_gen, tier,
                                           flags)
