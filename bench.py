@@ -115,8 +115,8 @@ def parse(argv=None):
     ap.add_argument("--no-stack", action="store_true",
                     help="skip the config-5 42-layer stack passes")
     ap.add_argument("--attn-only", action="store_true",
-                    help="only the attention measurement (--steps launches), "
-                         "printed as its own JSON object")
+                    help="only the attention and norm/RoPE measurements "
+                         "(--steps launches), printed as their own JSON object")
     ap.add_argument("--m-sweep", action="store_true",
                     help="only the M sweep of the dense / dequant-once / int8 "
                          "routes at K=4096, N=6144")
@@ -743,6 +743,62 @@ def attention_masks_measure(torch, ops, gen, launches):
     return res
 
 
+def prologue_measure(torch, ops, gen, launches, cs, sn):
+    """Config 2's attention prologue (128 und + 4096 gen tokens, 32 q heads,
+    8 kv heads, head_dim 128) as one u15h_mot_attention_prologue launch,
+    against the six calls it replaces (q and k norm + RoPE per expert
+    group, then k and v into the caches).  HBM-bound: q read and written, k
+    and v read and written into the caches, the two f32 tables read."""
+    Mu, Mg, HQ, KV, D, d_t, d_h = 128, 4096, 32, 8, 128, 64, 32
+    T = Mu + Mg
+    q = torch.randn(T, HQ * D, generator=gen, device="cuda").to(torch.bfloat16)
+    k = torch.randn(T, KV * D, generator=gen, device="cuda").to(torch.bfloat16)
+    v = torch.randn(T, KV * D, generator=gen, device="cuda").to(torch.bfloat16)
+    kc = torch.empty(KV, T, D, dtype=torch.bfloat16, device="cuda")
+    vc = torch.empty(KV, T, D, dtype=torch.bfloat16, device="cuda")
+    norms = {e: {f: (1 + 0.1 * torch.randn(D // 2, generator=gen, device="cuda"))
+                 .to(torch.bfloat16) for f in ("q_t", "q_hw", "k_t", "k_hw")}
+             for e in ("und", "gen")}
+    groups = (("und", slice(0, Mu)), ("gen", slice(Mu, T)))
+
+    def fused():
+        ops.mot_attention_prologue(q, k, v, norms["und"], norms["gen"], cs, sn,
+                                   Mu, Mg, HQ, KV, D, d_t, d_h, kc, vc)
+
+    def calls():
+        for e, r in groups:
+            w = norms[e]
+            ops.split_qk_norm_rope(q[r], w["q_t"], w["q_hw"], cs[r], sn[r], HQ, D, d_t, d_h)
+            ops.split_qk_norm_rope(k[r], w["k_t"], w["k_hw"], cs[r], sn[r], KV, D, d_t, d_h)
+        ops.transpose_into_cache(k, kc, T, KV, D, 0)
+        ops.transpose_into_cache(v, vc, T, KV, D, 0)
+
+    hev = HipEvents()
+    stream = torch.cuda.current_stream()
+    ms = {}
+    for name, fn in (("fused", fused), ("calls", calls)):
+        for _ in range(3):
+            fn()
+        e0, e1 = hev.create(), hev.create()
+        torch.cuda.synchronize()
+        hev.record(e0, stream)
+        for _ in range(launches):
+            fn()
+        hev.record(e1, stream)
+        torch.cuda.synchronize()
+        ms[name] = hev.elapsed(e0, e1) / launches
+    hev.close()
+    nbytes = 2 * T * HQ * D * 2 + 2 * 2 * T * KV * D * 2 + 2 * T * D * 4
+    gbs = nbytes / (ms["fused"] * 1e-3) / 1e9
+    return {"kernel": "attention_prologue_kernel",
+            "shape": {"m_und": Mu, "m_gen": Mg, "hq": HQ, "hkv": KV, "head_dim": D},
+            "avg_launch_ms": round(ms["fused"], 5),
+            "separate_calls_ms": round(ms["calls"], 5),
+            "alg_bytes_per_launch": nbytes, "achieved_GBps": round(gbs, 1),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM,
+                         "unit": "GB/s", "frac": round(gbs / PEAK_HBM, 4)}}
+
+
 def norm_rope_measure(torch, ops, gen, launches):
     """Average launch time of the fused split q/k norm + split RoPE pass
     over config 2's q (32 heads) and k (8 heads) rows: 4224 tokens,
@@ -773,6 +829,7 @@ def norm_rope_measure(torch, ops, gen, launches):
         out[name] = {"heads": H, "avg_launch_ms": round(ms, 5),
                      "alg_bytes_per_launch": nbytes, "achieved_GBps": round(gbs, 1)}
     hev.close()
+    out["prologue"] = prologue_measure(torch, ops, gen, launches, cs, sn)
     return {"kernel": "split_norm_rope_vec_kernel<true, true>",
             "shape": {"tokens": T, "head_dim": D, "d_t": d_t, "d_h": d_h},
             **out,
@@ -954,6 +1011,7 @@ def main(argv=None):
     if args.attn_only:
         res = attention_measure(torch, ops, gen, args.steps)
         res["masks"] = attention_masks_measure(torch, ops, gen, args.steps)
+        res["split_norm_rope"] = norm_rope_measure(torch, ops, gen, args.steps)
         print(json.dumps(res), flush=True)
         ops.close()
         return

@@ -258,6 +258,39 @@ u15h_status u15h_split_qk_norm_rope(u15h_ctx* ctx, u15h_stream stream,
                                     int tokens, int head_dim, int d_t,
                                     int d_h, float eps);
 
+/* One expert's q and k norm weights (ExpertLayer's q_norm, q_norm_hw,
+ * k_norm, k_norm_hw; src/u15-weights.h:97-117), each [head_dim / 2]. */
+typedef struct {
+  const u15h_bf16* q_t;
+  const u15h_bf16* q_hw;
+  const u15h_bf16* k_t;
+  const u15h_bf16* k_hw;
+} u15h_qk_norm;
+
+/* The attention prologue of a two-group pass in ONE launch.  It replaces
+ * the calls between the q/k/v projections and attention in
+ * U15Backbone::layer_step_ (src/u15-backbone.cc:203-216: split_qk_norm on
+ * q and k, split_rope on q and k, transpose_into_cache of k and v), with
+ * rows [0, M_und) taking `und`'s norm weights and the next M_gen rows
+ * `gen`'s, as the grouped projections do.  For token t and head h:
+ *   q[t][h]                    <- rope(norm(q[t][h]))   in place
+ *   k_cache[h][offset + t][:]  <- rope(norm(k[t][h]))
+ *   v_cache[h][offset + t][:]  <- v[t][h]
+ * q is [T][hq*head_dim], k and v [T][hkv*head_dim] (T = M_und + M_gen),
+ * caches [hkv][cap][head_dim].  k and v are only read.  Bits equal
+ * u15h_split_qk_norm_rope on q and k per expert group, then
+ * u15h_transpose_into_cache of k and v.  No reference counterpart as one
+ * call.  Limits: head_dim a power of two in [16, 512], d_t / 16 and
+ * d_h / 16 powers of two with d_h dividing d_t (the model's 64 | 32 | 32),
+ * every pointer 16-byte aligned, offset + T <= cap; other shapes take the
+ * separate calls. */
+u15h_status u15h_mot_attention_prologue(
+    u15h_ctx* ctx, u15h_stream stream, u15h_bf16* q, const u15h_bf16* k,
+    const u15h_bf16* v, const u15h_qk_norm* und, const u15h_qk_norm* gen,
+    const float* cos_tab, const float* sin_tab, int M_und, int M_gen, int hq,
+    int hkv, int head_dim, int d_t, int d_h, float eps, u15h_bf16* k_cache,
+    u15h_bf16* v_cache, int cap, int offset);
+
 /* Replaces MetalOps::build_rope_tables(pos_t, pos_h, pos_w, head_dim, d_t,
  * d_h, theta_t, theta_hw) (src/u15-metal-ops.h:186-195, .cc:547-600).  HOST
  * function, no context: fills host arrays cos_tab/sin_tab [tokens]

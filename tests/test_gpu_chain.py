@@ -7,6 +7,8 @@ x -> grouped q|k|v -> split q/k norm + three-way RoPE per expert group
 (u15h_split_qk_norm_rope) -> k, v into a head-major cache whose stride is
 its capacity (u15h_transpose_into_cache) -> bidirectional GQA attention
 over the cache, token-major (u15h_attention_token_major) -> grouped o.
+The norm, RoPE and cache steps run either as those calls or as the one
+launch that replaces them (u15h_mot_attention_prologue).
 
 The reference runs the same layer half in f32 from the same bf16 inputs:
 u15::ref::split_rope_project for q and k, ref::linear for v, ref::attention
@@ -41,7 +43,8 @@ def _f32(t):
     return oracle.bf16_to_f32(host_bits(t))
 
 
-def test_attention_half_chain_vs_reference(ops):
+@pytest.mark.parametrize("prologue", ["calls", "fused"])
+def test_attention_half_chain_vs_reference(ops, prologue):
     if oracle.ref_lib() is None:
         pytest.skip("the compiled reference (oracle/_ref) is not built")
     Mu, Mg = 64, 192
@@ -67,16 +70,22 @@ def test_attention_half_chain_vs_reference(ops):
                                     for n, y in (("q", q), ("k", k), ("v", v))])
     cs, sn = (torch.from_numpy(a).cuda() for a in
               u15h.build_rope_tables(pos_t, pos_h, pos_w, HD, D_T, D_H))
-    for e, r in groups:
-        ops.split_qk_norm_rope(q[r], W[e]["qn_t"], W[e]["qn_hw"], cs[r], sn[r],
-                               NH, HD, D_T, D_H)
-        ops.split_qk_norm_rope(k[r], W[e]["kn_t"], W[e]["kn_hw"], cs[r], sn[r],
-                               KV, HD, D_T, D_H)
     cap = T + 40                    # the cache stride is its capacity, not T
     kc = torch.full((KV, cap, HD), float("nan"), dtype=torch.bfloat16, device="cuda")
     vc = torch.full((KV, cap, HD), float("nan"), dtype=torch.bfloat16, device="cuda")
-    ops.transpose_into_cache(k, kc, T, KV, HD, 0)
-    ops.transpose_into_cache(v, vc, T, KV, HD, 0)
+    if prologue == "calls":
+        for e, r in groups:
+            ops.split_qk_norm_rope(q[r], W[e]["qn_t"], W[e]["qn_hw"], cs[r], sn[r],
+                                   NH, HD, D_T, D_H)
+            ops.split_qk_norm_rope(k[r], W[e]["kn_t"], W[e]["kn_hw"], cs[r], sn[r],
+                                   KV, HD, D_T, D_H)
+        ops.transpose_into_cache(k, kc, T, KV, HD, 0)
+        ops.transpose_into_cache(v, vc, T, KV, HD, 0)
+    else:
+        norms = {e: dict(q_t=W[e]["qn_t"], q_hw=W[e]["qn_hw"],
+                         k_t=W[e]["kn_t"], k_hw=W[e]["kn_hw"]) for e in ("und", "gen")}
+        ops.mot_attention_prologue(q, k, v, norms["und"], norms["gen"], cs, sn,
+                                   Mu, Mg, NH, KV, HD, D_T, D_H, kc, vc)
     attn = torch.empty(T, NH * HD, dtype=torch.bfloat16, device="cuda")
     ops.attention_token_major(q, kc, vc, attn, NH, KV, T, mode=0)
     o = torch.empty(T, HID, dtype=torch.bfloat16, device="cuda")

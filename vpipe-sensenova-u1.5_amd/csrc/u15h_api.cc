@@ -1352,6 +1352,91 @@ u15h_split_qk_norm_rope(u15h_ctx* ctx, u15h_stream stream, u15h_bf16* x,
 }
 
 u15h_status
+u15h_mot_attention_prologue(u15h_ctx* ctx, u15h_stream stream, u15h_bf16* q,
+                            const u15h_bf16* k, const u15h_bf16* v,
+                            const u15h_qk_norm* und, const u15h_qk_norm* gen,
+                            const float* cos_tab, const float* sin_tab,
+                            int M_und, int M_gen, int hq, int hkv,
+                            int head_dim, int d_t, int d_h, float eps,
+                            u15h_bf16* k_cache, u15h_bf16* v_cache, int cap,
+                            int offset)
+{
+  if (ctx == nullptr) { return U15H_EINVAL; }
+  const char* what = "mot_attention_prologue";
+  if (M_und < 0 || M_gen < 0 || (long long)M_und + M_gen > (1 << 30)) {
+    return fail(ctx, U15H_EINVAL, "%s: M_und=%d M_gen=%d", what, M_und, M_gen);
+  }
+  const int T = M_und + M_gen;
+  u15h_status st = check_head(ctx, hq, T, head_dim, d_t, d_h);
+  if (st != U15H_OK) { return st; }
+  if ((st = check_head(ctx, hkv, T, head_dim, d_t, d_h)) != U15H_OK) { return st; }
+  auto pow2 = [](int x) { return x > 0 && (x & (x - 1)) == 0; };
+  if (!pow2(head_dim) || head_dim < 16 || d_t % 16 != 0 || d_h % 16 != 0 ||
+      !pow2(d_t / 16) || !pow2(d_h / 16) || d_t % d_h != 0) {
+    return fail(ctx, U15H_EINVAL, "%s: head_dim=%d d_t=%d d_h=%d (head_dim a "
+                "power of two >= 16, d_t/16 and d_h/16 powers of two, d_h | "
+                "d_t; other shapes take the separate calls)", what, head_dim,
+                d_t, d_h);
+  }
+  if (offset < 0 || cap <= 0 || (long long)offset + T > cap) {
+    return fail(ctx, U15H_EINVAL, "%s: offset %d + T %d exceeds capacity %d",
+                what, offset, T, cap);
+  }
+  if (!(eps >= 0.0f)) {
+    return fail(ctx, U15H_EINVAL, "%s: eps must be >= 0", what);
+  }
+  if (T == 0) { ctx->err.clear(); return U15H_OK; }
+  const u15h_qk_norm* sets[2] = {und, gen};
+  const bool used[2] = {M_und > 0, M_gen > 0};
+  u15h::PrologueArgs a{};
+  for (int e = 0; e < 2; ++e) {
+    if (!used[e]) { continue; }
+    const u15h_qk_norm* n = sets[e];
+    if (n == nullptr || n->q_t == nullptr || n->q_hw == nullptr ||
+        n->k_t == nullptr || n->k_hw == nullptr || !aligned16(n->q_t) ||
+        !aligned16(n->q_hw) || !aligned16(n->k_t) || !aligned16(n->k_hw)) {
+      return fail(ctx, U15H_EINVAL, "%s: %s norm weights null or misaligned",
+                  what, e == 0 ? "und" : "gen");
+    }
+    a.w[e][0] = n->q_t;
+    a.w[e][1] = n->q_hw;
+    a.w[e][2] = n->k_t;
+    a.w[e][3] = n->k_hw;
+  }
+  // an unused group's slots point at the used one's (never read)
+  for (int j = 0; j < 4; ++j) {
+    if (!used[0]) { a.w[0][j] = a.w[1][j]; }
+    if (!used[1]) { a.w[1][j] = a.w[0][j]; }
+  }
+  const void* ptrs[7] = {q, k, v, k_cache, v_cache, cos_tab, sin_tab};
+  for (const void* ptr : ptrs) {
+    if (ptr == nullptr || !aligned16(ptr)) {
+      return fail(ctx, U15H_EINVAL, "%s: null or misaligned operand", what);
+    }
+  }
+  if ((st = bind_device(ctx)) != U15H_OK) { return st; }
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.k_cache = k_cache;
+  a.v_cache = v_cache;
+  a.cosf = cos_tab;
+  a.sinf = sin_tab;
+  a.tokens = T;
+  a.m_und = M_und;
+  a.hq = hq;
+  a.hkv = hkv;
+  a.d = head_dim;
+  a.d_t = d_t;
+  a.d_h = d_h;
+  a.cap = cap;
+  a.offset = offset;
+  a.eps = eps;
+  return launched(ctx, u15h::launch_attention_prologue(a, as_stream(stream)),
+                  what);
+}
+
+u15h_status
 u15h_build_rope_tables(const int32_t* pos_t, const int32_t* pos_h,
                        const int32_t* pos_w, int tokens, int head_dim, int d_t,
                        int d_h, double theta_t, double theta_hw,

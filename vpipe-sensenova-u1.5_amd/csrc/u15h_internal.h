@@ -179,6 +179,25 @@ struct AttnArgs {
   int hq, hkv, tq, tk, cap, q_offset, d, mode;
 };
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
+// The attention prologue of a two-group pass in one launch: q normed and
+// rotated in place, k normed and rotated into its cache, v copied into its
+// cache.  Shapes as split_norm_rope_vec_kernel's (d a power of two in
+// [16, 512], d_t / 16 and d_h / 16 powers of two, d_h dividing d_t), every
+// pointer 16-byte aligned.  Expert e's norm weights are w[e][0..3] = q_t,
+// q_hw, k_t, k_hw; rows [0, m_und) take e = 0.
+struct PrologueArgs {
+  uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  const uint16_t* w[2][4];
+  const float* cosf;
+  const float* sinf;
+  int tokens, m_und, hq, hkv, d, d_t, d_h, cap, offset;
+  float eps;
+};
+hipError_t launch_attention_prologue(const PrologueArgs& a, hipStream_t s);
 hipError_t launch_transpose_rows(const uint16_t* src, uint16_t* dst, int T,
                                  int H, int D, long long src_t, long long src_h,
                                  long long dst_t, long long dst_h,

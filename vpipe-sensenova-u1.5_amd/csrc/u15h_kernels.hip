@@ -1607,28 +1607,15 @@ split_norm_rope_kernel(uint16_t* __restrict__ x,
 // elements away (r = half its range), sits on the lane r/8 away (xor, as
 // every range starts at a multiple of its own width).  Shapes: D a power of
 // two in [16, 512], d_t/16 and d_h/16 powers of two, d_h dividing d_t.
+// Every lane of a row runs this (the shuffles read the row's other lanes).
+// `w_t`/`w_hw` are the norm weights, `cp`/`sp` the token's table rows.
 template <bool NORM, bool ROPE>
-__global__ __launch_bounds__(256) void
-split_norm_rope_vec_kernel(uint16_t* __restrict__ x,
-                           const uint16_t* __restrict__ w_t,
-                           const uint16_t* __restrict__ w_hw,
-                           const float* __restrict__ cosf,
-                           const float* __restrict__ sinf, int rows, int H,
-                           int D, int d_t, int d_h, float eps)
+__device__ __forceinline__ void
+norm_rope_chunk(float (&v)[8], int c, int D, int d_t, int d_h, float eps,
+                const uint16_t* w_t, const uint16_t* w_hw, const float* cp,
+                const float* sp)
 {
   const int cpr = D >> 3;                          // chunks (lanes) per row
-  const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
-  const long long row = gid / cpr;
-  const int c = (int)(gid % cpr);
-  const bool active = row < rows;
-  uint16_t* p = x + (active ? row : 0) * D + c * 8;
-  i32x4_t raw = active ? *reinterpret_cast<const i32x4_t*>(p) : i32x4_t{0, 0, 0, 0};
-  float v[8];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    v[2 * i] = __uint_as_float((uint32_t)raw[i] << 16);
-    v[2 * i + 1] = __uint_as_float((uint32_t)raw[i] & 0xffff0000u);
-  }
   const int hc = cpr >> 1;                         // chunks per half
   if constexpr (NORM) {
     float ss = 0.0f;
@@ -1652,26 +1639,119 @@ split_norm_rope_vec_kernel(uint16_t* __restrict__ x,
     float vp[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) { vp[i] = __shfl_xor(v[i], r >> 3); }
-    const long long t = (active ? row : 0) / H;
-    const float* cp = cosf + t * D + e0;
-    const float* sp = sinf + t * D + e0;
     float cs[8], sn[8];
-    *reinterpret_cast<i32x4_t*>(cs) = *reinterpret_cast<const i32x4_t*>(cp);
-    *reinterpret_cast<i32x4_t*>(cs + 4) = *reinterpret_cast<const i32x4_t*>(cp + 4);
-    *reinterpret_cast<i32x4_t*>(sn) = *reinterpret_cast<const i32x4_t*>(sp);
-    *reinterpret_cast<i32x4_t*>(sn + 4) = *reinterpret_cast<const i32x4_t*>(sp + 4);
+    *reinterpret_cast<i32x4_t*>(cs) = *reinterpret_cast<const i32x4_t*>(cp + e0);
+    *reinterpret_cast<i32x4_t*>(cs + 4) = *reinterpret_cast<const i32x4_t*>(cp + e0 + 4);
+    *reinterpret_cast<i32x4_t*>(sn) = *reinterpret_cast<const i32x4_t*>(sp + e0);
+    *reinterpret_cast<i32x4_t*>(sn + 4) = *reinterpret_cast<const i32x4_t*>(sp + e0 + 4);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       v[i] = lower ? v[i] * cs[i] - vp[i] * sn[i] : v[i] * cs[i] + vp[i] * sn[i];
     }
   }
-  if (!active) { return; }
+}
+
+__device__ __forceinline__ void
+unpack_bf16x8(const i32x4_t raw, float (&v)[8])
+{
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float((uint32_t)raw[i] << 16);
+    v[2 * i + 1] = __uint_as_float((uint32_t)raw[i] & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ i32x4_t
+pack_bf16x8(const float (&v)[8])
+{
   i32x4_t o;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     o[i] = (int)(bf16_bits(v[2 * i]) | (bf16_bits(v[2 * i + 1]) << 16));
   }
-  *reinterpret_cast<i32x4_t*>(p) = o;
+  return o;
+}
+
+template <bool NORM, bool ROPE>
+__global__ __launch_bounds__(256) void
+split_norm_rope_vec_kernel(uint16_t* __restrict__ x,
+                           const uint16_t* __restrict__ w_t,
+                           const uint16_t* __restrict__ w_hw,
+                           const float* __restrict__ cosf,
+                           const float* __restrict__ sinf, int rows, int H,
+                           int D, int d_t, int d_h, float eps)
+{
+  const int cpr = D >> 3;
+  const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
+  const long long row = gid / cpr;
+  const int c = (int)(gid % cpr);
+  const bool active = row < rows;
+  uint16_t* p = x + (active ? row : 0) * D + c * 8;
+  const i32x4_t raw = active ? *reinterpret_cast<const i32x4_t*>(p) : i32x4_t{0, 0, 0, 0};
+  float v[8];
+  unpack_bf16x8(raw, v);
+  const long long t = (active ? row : 0) / H;
+  norm_rope_chunk<NORM, ROPE>(v, c, D, d_t, d_h, eps, w_t, w_hw, cosf + t * D,
+                              sinf + t * D);
+  if (!active) { return; }
+  *reinterpret_cast<i32x4_t*>(p) = pack_bf16x8(v);
+}
+
+// The attention prologue of a two-group pass (PrologueArgs), one thread
+// per 16-byte chunk as above.  The grid is three runs of whole workgroups:
+// q rows (token-major [t][h], normed and rotated in place), k rows (normed
+// and rotated, stored to k_cache[h][offset + t]) and v rows (copied to
+// v_cache[h][offset + t]), so every branch below is uniform per workgroup.
+// Rows of tokens below m_und take the und norm weights.
+__global__ __launch_bounds__(256) void
+attention_prologue_kernel(const PrologueArgs a)
+{
+  const int D = a.d;
+  const int cpr = D >> 3;
+  const int rpb = 256 / cpr;                       // rows per workgroup
+  const long long nq = (long long)a.tokens * a.hq;
+  const long long nk = (long long)a.tokens * a.hkv;
+  const long long bq = (nq + rpb - 1) / rpb;
+  const long long bk = (nk + rpb - 1) / rpb;
+  long long blk = blockIdx.x;
+  int part;                                        // 0 q, 1 k, 2 v
+  long long nrows;
+  if (blk < bq) {
+    part = 0; nrows = nq;
+  } else if (blk < bq + bk) {
+    part = 1; nrows = nk; blk -= bq;
+  } else {
+    part = 2; nrows = nk; blk -= bq + bk;
+  }
+  const long long row = blk * rpb + threadIdx.x / cpr;
+  const int c = threadIdx.x % cpr;
+  const bool active = row < nrows;
+  const long long rr = active ? row : 0;
+  const int H = part == 0 ? a.hq : a.hkv;
+  const long long t = rr / H;
+  const int h = (int)(rr % H);
+  const uint16_t* src = part == 0 ? a.q : (part == 1 ? a.k : a.v);
+  const i32x4_t raw = active
+      ? *reinterpret_cast<const i32x4_t*>(src + rr * D + c * 8)
+      : i32x4_t{0, 0, 0, 0};
+  if (part == 2) {
+    if (active) {
+      *reinterpret_cast<i32x4_t*>(
+          a.v_cache + ((long long)h * a.cap + a.offset + t) * D + c * 8) = raw;
+    }
+    return;
+  }
+  float v[8];
+  unpack_bf16x8(raw, v);
+  const int e = t < a.m_und ? 0 : 1;
+  norm_rope_chunk<true, true>(v, c, D, a.d_t, a.d_h, a.eps, a.w[e][2 * part],
+                              a.w[e][2 * part + 1], a.cosf + t * D,
+                              a.sinf + t * D);
+  if (!active) { return; }
+  uint16_t* dst = part == 0
+      ? a.q + rr * D
+      : a.k_cache + ((long long)h * a.cap + a.offset + t) * D;
+  *reinterpret_cast<i32x4_t*>(dst + c * 8) = pack_bf16x8(v);
 }
 
 // ---- f16 -> bf16, the loader's conversion -----------------------------------
@@ -3197,6 +3277,19 @@ launch_split_norm_rope(uint16_t* x, const uint16_t* w_t, const uint16_t* w_hw,
 }
 
 hipError_t
+launch_attention_prologue(const PrologueArgs& a, hipStream_t s)
+{
+  if (a.tokens <= 0) { return hipSuccess; }
+  const int rpb = 256 / (a.d / 8);
+  const long long nq = (long long)a.tokens * a.hq;
+  const long long nk = (long long)a.tokens * a.hkv;
+  const long long blocks = (nq + rpb - 1) / rpb + 2 * ((nk + rpb - 1) / rpb);
+  hipLaunchKernelGGL(attention_prologue_kernel, dim3((unsigned)blocks), dim3(256),
+                     0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t
 launch_f16_to_bf16(const uint16_t* src, int64_t n, uint16_t* dst, hipStream_t s)
 {
   const int64_t nvec = n / 4;
@@ -3350,6 +3443,7 @@ kernels_loadable()
       reinterpret_cast<const void*>(&split_norm_rope_vec_kernel<true, true>),
       reinterpret_cast<const void*>(&split_norm_rope_vec_kernel<true, false>),
       reinterpret_cast<const void*>(&split_norm_rope_vec_kernel<false, true>),
+      reinterpret_cast<const void*>(&attention_prologue_kernel),
       reinterpret_cast<const void*>(&quant_rows_i8_waves_kernel<4, 1, 1>),
       reinterpret_cast<const void*>(&quant_rows_i8_waves_kernel<4, 2, 1>),
       reinterpret_cast<const void*>(&quant_rows_i8_waves_kernel<4, 4, 1>),

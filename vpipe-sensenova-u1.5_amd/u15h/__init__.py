@@ -58,6 +58,11 @@ class _LayerIO(ctypes.Structure):
                  "down", "xq", "sx")]
 
 
+class _QkNorm(ctypes.Structure):
+    _fields_ = [("q_t", ctypes.c_void_p), ("q_hw", ctypes.c_void_p),
+                ("k_t", ctypes.c_void_p), ("k_hw", ctypes.c_void_p)]
+
+
 class _QWeight(ctypes.Structure):
     _fields_ = [("codes", ctypes.c_void_p), ("scales", ctypes.c_void_p),
                 ("biases", ctypes.c_void_p), ("bits", ctypes.c_int),
@@ -124,6 +129,11 @@ def load_library() -> ctypes.CDLL:
         "u15h_split_rope": (i, [vp, vp, vp, vp, vp, i, i, i, i, i]),
         "u15h_split_qk_norm_rope": (i, [vp, vp, vp, vp, vp, vp, vp, i, i, i,
                                         i, i, ctypes.c_float]),
+        "u15h_mot_attention_prologue": (i, [vp, vp, vp, vp, vp,
+                                            ctypes.POINTER(_QkNorm),
+                                            ctypes.POINTER(_QkNorm), vp, vp,
+                                            i, i, i, i, i, i, i,
+                                            ctypes.c_float, vp, vp, i, i]),
         "u15h_build_rope_tables": (i, [vp, vp, vp, i, i, i, i,
                                        ctypes.c_double, ctypes.c_double, vp,
                                        vp]),
@@ -762,6 +772,42 @@ class Ops:
             self._ctx, _stream(stream), _ptr(x), _ptr(w_t), _ptr(w_hw),
             _ptr(cos), _ptr(sin), heads, T, head_dim, d_t, d_h, eps)
         self._check(st, "u15h_split_qk_norm_rope")
+
+    def mot_attention_prologue(self, q, k, v, und, gen, cos, sin, M_und,
+                               M_gen, hq, hkv, head_dim, d_t, d_h, k_cache,
+                               v_cache, offset=0, eps=1e-6, stream=None):
+        """u15h_mot_attention_prologue: q [T][hq*d] normed and rotated in
+        place, k normed and rotated into k_cache [hkv][cap][d] at token
+        offset `offset`, v copied into v_cache; rows [0, M_und) take `und`'s
+        norm weights (a dict q_t, q_hw, k_t, k_hw of [d/2] bf16 tensors),
+        the rest `gen`'s."""
+        T = M_und + M_gen
+        _need(q, torch.bfloat16, (T, hq * head_dim), "q")
+        _need(k, torch.bfloat16, (T, hkv * head_dim), "k")
+        _need(v, torch.bfloat16, (T, hkv * head_dim), "v")
+        _need(cos, torch.float32, (T, head_dim), "cos")
+        _need(sin, torch.float32, (T, head_dim), "sin")
+        if k_cache.dim() != 3:
+            raise ValueError("k_cache must be [hkv][cap][head_dim]")
+        cap = k_cache.shape[1]
+        _need(k_cache, torch.bfloat16, (hkv, cap, head_dim), "k_cache")
+        _need(v_cache, torch.bfloat16, (hkv, cap, head_dim), "v_cache")
+        norms = []
+        for tag, n, rows in (("und", und, M_und), ("gen", gen, M_gen)):
+            if rows == 0:
+                norms.append(None)
+                continue
+            for f in ("q_t", "q_hw", "k_t", "k_hw"):
+                _need(n.get(f) if n else None, torch.bfloat16,
+                      (head_dim // 2,), f"{tag}.{f}")
+            norms.append(_QkNorm(*[_ptr(n[f]) for f in ("q_t", "q_hw", "k_t", "k_hw")]))
+        st = self._lib.u15h_mot_attention_prologue(
+            self._ctx, _stream(stream), _ptr(q), _ptr(k), _ptr(v),
+            None if norms[0] is None else ctypes.byref(norms[0]),
+            None if norms[1] is None else ctypes.byref(norms[1]),
+            _ptr(cos), _ptr(sin), M_und, M_gen, hq, hkv, head_dim, d_t, d_h,
+            eps, _ptr(k_cache), _ptr(v_cache), cap, offset)
+        self._check(st, "u15h_mot_attention_prologue")
 
     # ---- attention -------------------------------------------------------
     def sdpa(self, q, k, v, out, hkv, tk, causal=False, q_offset=0,
