@@ -24,6 +24,11 @@ struct u15h_ctx {
   bool split_on = true;      // env U15H_SPLIT=0 turns the split-K tail off
   // env U15H_SKINNY=0 keeps batches of <= 128-row problems on the tiled GEMM
   bool skinny_on = true;
+  // heads of one token per thread in u15h_mot_attention_prologue (1, 2 or
+  // 4; env U15H_PROLOGUE_RPT).  At config 2 (4224 tokens, 32 + 8 + 8
+  // heads of 128) 2 measured 21.6-21.9 us against 22.9-24.5 (1) and
+  // 23.0-24.9 (4), three interleaved rounds on one box.
+  int prologue_rpt = 2;
   // u15h_linear_q below this many rows reads the pack directly (the
   // reference's _mma_q_min_m, u15-metal-ops.h:502; env U15H_Q_MIN_M)
   int q_min_m = 96;
@@ -515,6 +520,7 @@ u15h_create(int device, u15h_ctx** out)
   ctx->num_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
   ctx->split_on = env_int("U15H_SPLIT", 1) != 0;
   ctx->skinny_on = env_int("U15H_SKINNY", 1) != 0;
+  ctx->prologue_rpt = env_int("U15H_PROLOGUE_RPT", 2);
   ctx->q_min_m = std::max(0, std::min(u15h::kSkinnyMaxRows + 1, env_int("U15H_Q_MIN_M", 96)));
   ctx->gemm.waves = env_int("U15H_WAVES", 8) == 4 ? 4 : 8;
   ctx->gemm.cus = env_int("U15H_PERSIST", 1) != 0 ? ctx->num_cu : 0;
@@ -1432,7 +1438,9 @@ u15h_mot_attention_prologue(u15h_ctx* ctx, u15h_stream stream, u15h_bf16* q,
   a.cap = cap;
   a.offset = offset;
   a.eps = eps;
-  return launched(ctx, u15h::launch_attention_prologue(a, as_stream(stream)),
+  return launched(ctx,
+                  u15h::launch_attention_prologue(a, as_stream(stream),
+                                                  ctx->prologue_rpt),
                   what);
 }
 

@@ -85,9 +85,6 @@ struct GemmShape {
   int mfma16;
 };
 
-// Profiling events of one GEMM launch: `before`, when not null, is
-// recorded on the launch stream right before the GEMM kernel, `after`
-// right after it and before any split-K reduction kernel.
 // Profiling events bound to kernel dispatches (hipExtLaunchKernel: each
 // takes its kernel's start or end timestamp; no packet of its own).  Null
 // members are not recorded.
@@ -197,7 +194,9 @@ struct PrologueArgs {
   int tokens, m_und, hq, hkv, d, d_t, d_h, cap, offset;
   float eps;
 };
-hipError_t launch_attention_prologue(const PrologueArgs& a, hipStream_t s);
+// Up to max_rpt (1, 2 or 4) heads of a token per thread.
+hipError_t launch_attention_prologue(const PrologueArgs& a, hipStream_t s,
+                                     int max_rpt);
 hipError_t launch_transpose_rows(const uint16_t* src, uint16_t* dst, int T,
                                  int H, int D, long long src_t, long long src_h,
                                  long long dst_t, long long dst_h,

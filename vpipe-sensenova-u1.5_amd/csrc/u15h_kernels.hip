@@ -1608,12 +1608,12 @@ split_norm_rope_kernel(uint16_t* __restrict__ x,
 // every range starts at a multiple of its own width).  Shapes: D a power of
 // two in [16, 512], d_t/16 and d_h/16 powers of two, d_h dividing d_t.
 // Every lane of a row runs this (the shuffles read the row's other lanes).
-// `w_t`/`w_hw` are the norm weights, `cp`/`sp` the token's table rows.
+// `w_t`/`w_hw` are the norm weights, `cs`/`sn` the chunk's 8 table entries.
 template <bool NORM, bool ROPE>
 __device__ __forceinline__ void
 norm_rope_chunk(float (&v)[8], int c, int D, int d_t, int d_h, float eps,
-                const uint16_t* w_t, const uint16_t* w_hw, const float* cp,
-                const float* sp)
+                const uint16_t* w_t, const uint16_t* w_hw, const float (&cs)[8],
+                const float (&sn)[8])
 {
   const int cpr = D >> 3;                          // chunks (lanes) per row
   const int hc = cpr >> 1;                         // chunks per half
@@ -1639,16 +1639,23 @@ norm_rope_chunk(float (&v)[8], int c, int D, int d_t, int d_h, float eps,
     float vp[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) { vp[i] = __shfl_xor(v[i], r >> 3); }
-    float cs[8], sn[8];
-    *reinterpret_cast<i32x4_t*>(cs) = *reinterpret_cast<const i32x4_t*>(cp + e0);
-    *reinterpret_cast<i32x4_t*>(cs + 4) = *reinterpret_cast<const i32x4_t*>(cp + e0 + 4);
-    *reinterpret_cast<i32x4_t*>(sn) = *reinterpret_cast<const i32x4_t*>(sp + e0);
-    *reinterpret_cast<i32x4_t*>(sn + 4) = *reinterpret_cast<const i32x4_t*>(sp + e0 + 4);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       v[i] = lower ? v[i] * cs[i] - vp[i] * sn[i] : v[i] * cs[i] + vp[i] * sn[i];
     }
   }
+}
+
+// The 8 cos and sin entries of chunk c of one token's table rows.
+__device__ __forceinline__ void
+load_rope_chunk(const float* cp, const float* sp, int c, float (&cs)[8],
+                float (&sn)[8])
+{
+  const int e0 = c * 8;
+  *reinterpret_cast<i32x4_t*>(cs) = *reinterpret_cast<const i32x4_t*>(cp + e0);
+  *reinterpret_cast<i32x4_t*>(cs + 4) = *reinterpret_cast<const i32x4_t*>(cp + e0 + 4);
+  *reinterpret_cast<i32x4_t*>(sn) = *reinterpret_cast<const i32x4_t*>(sp + e0);
+  *reinterpret_cast<i32x4_t*>(sn + 4) = *reinterpret_cast<const i32x4_t*>(sp + e0 + 4);
 }
 
 __device__ __forceinline__ void
@@ -1690,68 +1697,91 @@ split_norm_rope_vec_kernel(uint16_t* __restrict__ x,
   const i32x4_t raw = active ? *reinterpret_cast<const i32x4_t*>(p) : i32x4_t{0, 0, 0, 0};
   float v[8];
   unpack_bf16x8(raw, v);
-  const long long t = (active ? row : 0) / H;
-  norm_rope_chunk<NORM, ROPE>(v, c, D, d_t, d_h, eps, w_t, w_hw, cosf + t * D,
-                              sinf + t * D);
+  float cs[8], sn[8];
+  if constexpr (ROPE) {
+    const long long t = (active ? row : 0) / H;
+    load_rope_chunk(cosf + t * D, sinf + t * D, c, cs, sn);
+  }
+  norm_rope_chunk<NORM, ROPE>(v, c, D, d_t, d_h, eps, w_t, w_hw, cs, sn);
   if (!active) { return; }
   *reinterpret_cast<i32x4_t*>(p) = pack_bf16x8(v);
 }
 
 // The attention prologue of a two-group pass (PrologueArgs), one thread
-// per 16-byte chunk as above.  The grid is three runs of whole workgroups:
-// q rows (token-major [t][h], normed and rotated in place), k rows (normed
-// and rotated, stored to k_cache[h][offset + t]) and v rows (copied to
-// v_cache[h][offset + t]), so every branch below is uniform per workgroup.
-// Rows of tokens below m_und take the und norm weights.
+// per 16-byte chunk as above, each thread holding that chunk of RPT heads
+// of one token (the token's table entries loaded once for all of them).
+// The grid is three runs of whole workgroups: q rows (token-major [t][h],
+// normed and rotated in place), k rows (normed and rotated, stored to
+// k_cache[h][offset + t]) and v rows (copied to v_cache[h][offset + t]),
+// so every branch below is uniform per workgroup.  Rows of tokens below
+// m_und take the und norm weights.  RPT divides hq and hkv.
+template <int RPT>
 __global__ __launch_bounds__(256) void
 attention_prologue_kernel(const PrologueArgs a)
 {
   const int D = a.d;
   const int cpr = D >> 3;
-  const int rpb = 256 / cpr;                       // rows per workgroup
-  const long long nq = (long long)a.tokens * a.hq;
-  const long long nk = (long long)a.tokens * a.hkv;
-  const long long bq = (nq + rpb - 1) / rpb;
-  const long long bk = (nk + rpb - 1) / rpb;
+  const int gpb = 256 / cpr;                       // head groups per workgroup
+  const long long nq = (long long)a.tokens * (a.hq / RPT);
+  const long long nk = (long long)a.tokens * (a.hkv / RPT);
+  const long long bq = (nq + gpb - 1) / gpb;
+  const long long bk = (nk + gpb - 1) / gpb;
   long long blk = blockIdx.x;
   int part;                                        // 0 q, 1 k, 2 v
-  long long nrows;
+  long long ngroups;
   if (blk < bq) {
-    part = 0; nrows = nq;
+    part = 0; ngroups = nq;
   } else if (blk < bq + bk) {
-    part = 1; nrows = nk; blk -= bq;
+    part = 1; ngroups = nk; blk -= bq;
   } else {
-    part = 2; nrows = nk; blk -= bq + bk;
+    part = 2; ngroups = nk; blk -= bq + bk;
   }
-  const long long row = blk * rpb + threadIdx.x / cpr;
+  const long long grp = blk * gpb + threadIdx.x / cpr;
   const int c = threadIdx.x % cpr;
-  const bool active = row < nrows;
-  const long long rr = active ? row : 0;
+  const bool active = grp < ngroups;
+  const long long gg = active ? grp : 0;
   const int H = part == 0 ? a.hq : a.hkv;
-  const long long t = rr / H;
-  const int h = (int)(rr % H);
-  const uint16_t* src = part == 0 ? a.q : (part == 1 ? a.k : a.v);
-  const i32x4_t raw = active
-      ? *reinterpret_cast<const i32x4_t*>(src + rr * D + c * 8)
-      : i32x4_t{0, 0, 0, 0};
+  const long long t = gg / (H / RPT);
+  const int h0 = (int)(gg % (H / RPT)) * RPT;
+  const uint16_t* src = (part == 0 ? a.q : (part == 1 ? a.k : a.v)) +
+                        (t * H + h0) * D + c * 8;
+  i32x4_t raw[RPT];
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+    raw[j] = active ? *reinterpret_cast<const i32x4_t*>(src + j * D)
+                    : i32x4_t{0, 0, 0, 0};
+  }
   if (part == 2) {
     if (active) {
-      *reinterpret_cast<i32x4_t*>(
-          a.v_cache + ((long long)h * a.cap + a.offset + t) * D + c * 8) = raw;
+#pragma unroll
+      for (int j = 0; j < RPT; ++j) {
+        *reinterpret_cast<i32x4_t*>(
+            a.v_cache + ((long long)(h0 + j) * a.cap + a.offset + t) * D + c * 8) = raw[j];
+      }
     }
     return;
   }
-  float v[8];
-  unpack_bf16x8(raw, v);
+  float cs[8], sn[8];
+  load_rope_chunk(a.cosf + t * D, a.sinf + t * D, c, cs, sn);
   const int e = t < a.m_und ? 0 : 1;
-  norm_rope_chunk<true, true>(v, c, D, a.d_t, a.d_h, a.eps, a.w[e][2 * part],
-                              a.w[e][2 * part + 1], a.cosf + t * D,
-                              a.sinf + t * D);
+  const uint16_t* w_t = a.w[e][2 * part];
+  const uint16_t* w_hw = a.w[e][2 * part + 1];
+  i32x4_t out[RPT];
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+    float v[8];
+    unpack_bf16x8(raw[j], v);
+    norm_rope_chunk<true, true>(v, c, D, a.d_t, a.d_h, a.eps, w_t, w_hw, cs, sn);
+    out[j] = pack_bf16x8(v);
+  }
   if (!active) { return; }
-  uint16_t* dst = part == 0
-      ? a.q + rr * D
-      : a.k_cache + ((long long)h * a.cap + a.offset + t) * D;
-  *reinterpret_cast<i32x4_t*>(dst + c * 8) = pack_bf16x8(v);
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+    uint16_t* dst = part == 0
+        ? a.q + (t * H + h0 + j) * D
+        : a.k_cache + ((long long)(h0 + j) * a.cap + a.offset + t) * D;
+    *reinterpret_cast<i32x4_t*>(dst + c * 8) = out[j];
+  }
 }
 
 // ---- f16 -> bf16, the loader's conversion -----------------------------------
@@ -3276,17 +3306,30 @@ launch_split_norm_rope(uint16_t* x, const uint16_t* w_t, const uint16_t* w_hw,
   return hipGetLastError();
 }
 
+template <int RPT>
+static hipError_t
+launch_attention_prologue_rpt(const PrologueArgs& a, hipStream_t s)
+{
+  const int gpb = 256 / (a.d / 8);
+  const long long nq = (long long)a.tokens * (a.hq / RPT);
+  const long long nk = (long long)a.tokens * (a.hkv / RPT);
+  const long long blocks = (nq + gpb - 1) / gpb + 2 * ((nk + gpb - 1) / gpb);
+  hipLaunchKernelGGL(attention_prologue_kernel<RPT>, dim3((unsigned)blocks),
+                     dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
 hipError_t
-launch_attention_prologue(const PrologueArgs& a, hipStream_t s)
+launch_attention_prologue(const PrologueArgs& a, hipStream_t s, int max_rpt)
 {
   if (a.tokens <= 0) { return hipSuccess; }
-  const int rpb = 256 / (a.d / 8);
-  const long long nq = (long long)a.tokens * a.hq;
-  const long long nk = (long long)a.tokens * a.hkv;
-  const long long blocks = (nq + rpb - 1) / rpb + 2 * ((nk + rpb - 1) / rpb);
-  hipLaunchKernelGGL(attention_prologue_kernel, dim3((unsigned)blocks), dim3(256),
-                     0, s, a);
-  return hipGetLastError();
+  if (max_rpt >= 4 && a.hq % 4 == 0 && a.hkv % 4 == 0) {
+    return launch_attention_prologue_rpt<4>(a, s);
+  }
+  if (max_rpt >= 2 && a.hq % 2 == 0 && a.hkv % 2 == 0) {
+    return launch_attention_prologue_rpt<2>(a, s);
+  }
+  return launch_attention_prologue_rpt<1>(a, s);
 }
 
 hipError_t
@@ -3443,7 +3486,9 @@ kernels_loadable()
       reinterpret_cast<const void*>(&split_norm_rope_vec_kernel<true, true>),
       reinterpret_cast<const void*>(&split_norm_rope_vec_kernel<true, false>),
       reinterpret_cast<const void*>(&split_norm_rope_vec_kernel<false, true>),
-      reinterpret_cast<const void*>(&attention_prologue_kernel),
+      reinterpret_cast<const void*>(&attention_prologue_kernel<1>),
+      reinterpret_cast<const void*>(&attention_prologue_kernel<2>),
+      reinterpret_cast<const void*>(&attention_prologue_kernel<4>),
       reinterpret_cast<const void*>(&quant_rows_i8_waves_kernel<4, 1, 1>),
       reinterpret_cast<const void*>(&quant_rows_i8_waves_kernel<4, 2, 1>),
       reinterpret_cast<const void*>(&quant_rows_i8_waves_kernel<4, 4, 1>),
