@@ -359,6 +359,40 @@ def interleaved(torch, arms, steps, rounds):
             for n, v in samples.items()}
 
 
+def device_peaks(torch):
+    """The box's own figures (hipDeviceGetAttribute: compute units, peak
+    shader clock, memory clock and bus width) and the peaks they imply,
+    beside the published ones the rooflines use: MFMA 4096 bf16 FLOP (8192
+    int8 OPs) per CU per clock, and HBM bus bytes x memory clock x 2
+    transfers per clock."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    hip.hipDeviceGetAttribute.argtypes = [ctypes.POINTER(ctypes.c_int), ctypes.c_int,
+                                          ctypes.c_int]
+    dev = torch.cuda.current_device()
+
+    def attr(code):
+        v = ctypes.c_int()
+        return v.value if hip.hipDeviceGetAttribute(ctypes.byref(v), code, dev) == 0 else None
+
+    # hipDeviceAttribute_t: ClockRate 5, MemoryBusWidth 59,
+    # MemoryClockRate 60, MultiprocessorCount 63 (kHz, bits, kHz, count)
+    clk_khz, bus_bits, mclk_khz, cus = attr(5), attr(59), attr(60), attr(63)
+    props = torch.cuda.get_device_properties(dev)
+    out = {"name": props.name, "arch": props.gcnArchName, "cus": cus,
+           "clock_mhz": None if clk_khz is None else clk_khz / 1000,
+           "mem_clock_mhz": None if mclk_khz is None else mclk_khz / 1000,
+           "mem_bus_bits": bus_bits,
+           "published": {"bf16_tflops": PEAK_BF16, "int8_tops": PEAK_I8,
+                         "hbm_gbps": PEAK_HBM}}
+    if cus and clk_khz:
+        out["from_clock"] = {"bf16_tflops": round(cus * clk_khz * 1e3 * 4096 / 1e12, 1),
+                             "int8_tops": round(cus * clk_khz * 1e3 * 8192 / 1e12, 1)}
+        if bus_bits and mclk_khz:
+            out["from_clock"]["hbm_gbps"] = round(bus_bits / 8 * mclk_khz * 1e3 * 2 / 1e9, 1)
+    return out
+
+
 class HipEvents:
     """Raw HIP events (hipEventCreate / Record / ElapsedTime) from the HIP
     runtime the process already uses -- the library records one of them
@@ -1073,6 +1107,7 @@ def main(argv=None):
                    "entry": "u15h_stack_layer"},
         "pct_of_peak": bf16["pct_of_peak"],
         "roofline": dict(bf16["roofline"], profiled_pass_ms_per_step=round(pms16, 5)),
+        "device": device_peaks(torch),
     }
     if want_i8:
         result["int8"] = tier_result(work, ms8, k8, args.steps, True,
