@@ -362,6 +362,42 @@ u15h_status u15h_transpose_into_cache(u15h_ctx* ctx, u15h_stream stream,
                                       int offset);
 
 /* ------------------------------------------------------------------ */
+/* The layer norms and the residual add (either side of the projections) */
+/* ------------------------------------------------------------------ */
+
+/* Replaces MetalOps::rms_norm(enc, x, w, y, rows, dim, eps)
+ * (src/u15-metal-ops.h:158-166, .cc:494-505), the whole-row RMSNorm with
+ * gain that feeds q|k|v (input_layernorm) and gate|up
+ * (post_attention_layernorm) in U15Backbone::layer_step_
+ * (src/u15-backbone.cc:196, 249): y = bf16((x * inv) * w) with inv =
+ * 1/sqrt(mean(x^2) + eps), the sum in f32 (the reference's CPU form,
+ * src/u15-ref.cc:15-31, accumulates in double).  x, y [rows][dim], w [dim],
+ * bf16.  The reference's `fast` flag picks between two reductions of its
+ * library with one contract; there is one here.  Limits: dim % 8 == 0,
+ * dim <= 16384, 16-byte aligned operands, eps >= 0; y may equal x. */
+u15h_status u15h_rms_norm(u15h_ctx* ctx, u15h_stream stream,
+                          const u15h_bf16* x, const u15h_bf16* w,
+                          u15h_bf16* y, int rows, int dim, float eps);
+
+/* The int8 tier's input in the same pass: the norm above, then the row's
+ * bf16 results quantised per token (u15h_quant_rows_i8's scale and codes,
+ * bit for bit, as if it ran on y).  q [rows][dim] int8, s [rows] f32; y
+ * [rows][dim] is written only when not NULL.  No reference counterpart:
+ * it saves the quantiser's separate read of the normed rows.  Limits as
+ * u15h_rms_norm's. */
+u15h_status u15h_rms_norm_quant_i8(u15h_ctx* ctx, u15h_stream stream,
+                                   const u15h_bf16* x, const u15h_bf16* w,
+                                   int rows, int dim, float eps,
+                                   u15h_bf16* y, int8_t* q, float* s);
+
+/* Replaces MetalOps::add(enc, dst, src, n) (src/u15-metal-ops.h:361-363,
+ * .cc:974-982; kernel u15_add, src/u15-kernels.metal:496-504), the
+ * residual add of layer_step_ (src/u15-backbone.cc:245, 256):
+ * dst[i] = bf16(f32(dst[i]) + f32(src[i])).  Any n and alignment. */
+u15h_status u15h_add(u15h_ctx* ctx, u15h_stream stream, u15h_bf16* dst,
+                     const u15h_bf16* src, int64_t n);
+
+/* ------------------------------------------------------------------ */
 /* SwiGLU                                                              */
 /* ------------------------------------------------------------------ */
 

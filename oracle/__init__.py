@@ -107,6 +107,9 @@ def ref_lib():
                                           ctypes.c_int, ctypes.c_int,
                                           ctypes.c_double, ctypes.c_double,
                                           ctypes.c_double, vp],
+            "u15ref_decoder_layer": [vp, ctypes.POINTER(vp), sz, sz, sz, sz, sz,
+                                     ctypes.c_double, ctypes.c_double,
+                                     ctypes.c_double, vp, vp, vp, vp, sz, vp],
         }.items():
             getattr(R, n).restype = None
             getattr(R, n).argtypes = a
@@ -436,6 +439,38 @@ def ref_attention(q, k, v, mask, hkv):
         mask, pm = _c(mask, np.float32)
     out = np.empty((tq, hq * d), np.float32)
     R.u15ref_attention(pq, pk, pv, pm, hq, hkv, tq, tk, d, out.ctypes.data)
+    return out
+
+
+LAYER_WEIGHT_NAMES = ("input_layernorm", "post_attention_layernorm", "q_proj",
+                      "k_proj", "v_proj", "o_proj", "q_norm", "k_norm",
+                      "q_norm_hw", "k_norm_hw", "gate_proj", "up_proj", "down_proj")
+
+
+def ref_decoder_layer(x, w, heads, kv_heads, head_dim, pos_t, pos_h, pos_w,
+                      mask=None, eps=1e-6, theta_t=5000000.0, theta_hw=10000.0):
+    """u15::ref::decoder_layer (src/u15-ref.cc:242-311): one expert's whole
+    layer in f32, x [tokens][hidden] -> [tokens][hidden].  `w` maps
+    LAYER_WEIGHT_NAMES to f32 arrays ([out][in] for the projections);
+    `mask` [tokens][tokens] additive, or None (bidirectional)."""
+    R = ref_lib()
+    if R is None:
+        return None
+    x, px = _c(x, np.float32)
+    tokens, hidden = x.shape
+    arrs = [np.ascontiguousarray(w[n], np.float32) for n in LAYER_WEIGHT_NAMES]
+    ptrs = (ctypes.c_void_p * 13)(*[a.ctypes.data for a in arrs])
+    inter = arrs[10].shape[0]
+    t, pt = _c(pos_t, np.int32)
+    h, ph = _c(pos_h, np.int32)
+    ww, pw = _c(pos_w, np.int32)
+    pm = None
+    if mask is not None:
+        mask, pm = _c(mask, np.float32)
+    out = np.empty((tokens, hidden), np.float32)
+    R.u15ref_decoder_layer(px, ptrs, hidden, heads, kv_heads, head_dim, inter, eps,
+                           theta_t, theta_hw, pt, ph, pw, pm, tokens,
+                           out.ctypes.data)
     return out
 
 

@@ -8,6 +8,8 @@
 //   u15ref_rms_norm, u15ref_rope_inv_freq, u15ref_rope_half,
 //   u15ref_split_rope_project -> the RoPE/norm helpers (src/u15-ref.h:25-95)
 //   u15ref_attention, u15ref_block_causal_mask -> src/u15-ref.h:95-110
+//   u15ref_decoder_layer -> u15::ref::decoder_layer (src/u15-ref.h:114-147,
+//                           u15-ref.cc:242-311), one expert's whole layer
 #include "u15-ref.h"
 
 extern "C" void
@@ -80,4 +82,42 @@ u15ref_block_causal_mask(const int* t_index, std::size_t n, float* out)
   const std::vector<int> t(t_index, t_index + n);
   const std::vector<float> m = u15::ref::block_causal_mask(t);
   for (std::size_t i = 0; i < m.size(); ++i) { out[i] = m[i]; }
+}
+
+// w[13]: input_layernorm, post_attention_layernorm, q, k, v, o, q_norm,
+// k_norm, q_norm_hw, k_norm_hw, gate, up, down (LayerWeights' order)
+extern "C" void
+u15ref_decoder_layer(const float* x, const float* const* w, std::size_t hidden,
+                     std::size_t heads, std::size_t kv_heads,
+                     std::size_t head_dim, std::size_t inter, double eps,
+                     double theta_t, double theta_hw, const int* pos_t,
+                     const int* pos_h, const int* pos_w, const float* mask,
+                     std::size_t tokens, float* out)
+{
+  u15::ref::LayerWeights lw;
+  lw.input_layernorm = w[0];
+  lw.post_attention_layernorm = w[1];
+  lw.q_proj = w[2];
+  lw.k_proj = w[3];
+  lw.v_proj = w[4];
+  lw.o_proj = w[5];
+  lw.q_norm = w[6];
+  lw.k_norm = w[7];
+  lw.q_norm_hw = w[8];
+  lw.k_norm_hw = w[9];
+  lw.gate_proj = w[10];
+  lw.up_proj = w[11];
+  lw.down_proj = w[12];
+  u15::ref::LayerDims d;
+  d.hidden = hidden;
+  d.heads = heads;
+  d.kv_heads = kv_heads;
+  d.head_dim = head_dim;
+  d.intermediate = inter;
+  d.rms_eps = eps;
+  d.theta_t = theta_t;
+  d.theta_hw = theta_hw;
+  const std::vector<int> t(pos_t, pos_t + tokens), h(pos_h, pos_h + tokens),
+      ww(pos_w, pos_w + tokens);
+  u15::ref::decoder_layer(x, lw, d, t, h, ww, mask, tokens, out);
 }

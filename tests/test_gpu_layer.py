@@ -1,0 +1,216 @@
+"""The layer norms, the residual add, and a whole MoT decoder layer chained
+through the C ABI against the compiled reference.
+
+  * u15h_rms_norm against the reference's rms_norm (src/u15-ref.cc:15-31,
+    compiled; double sums) on the same bf16 inputs: every output within one
+    bf16 ulp of the reference's value rounded to bf16, nearly all equal.
+  * u15h_rms_norm_quant_i8: codes and scales bit-equal to u15h_rms_norm
+    followed by u15h_quant_rows_i8, and to the oracle's quantiser on the
+    normed rows.
+  * u15h_add: bit-exact against f32 addition rounded to bf16 (the reference
+    kernel u15_add, src/u15-kernels.metal:496-504), any length and offset.
+  * The whole layer of U15Backbone::layer_step_ (src/u15-backbone.cc:
+    193-257) for one expert's pass, as the reference runs it: rms_norm ->
+    q|k|v -> attention prologue -> attention (bidirectional for the gen
+    pass, block-causal for the und pass) -> o -> residual add -> rms_norm
+    -> gate|up with SwiGLU -> down -> residual add, against
+    u15::ref::decoder_layer (src/u15-ref.cc:242-311) in f32 from the same
+    bf16 values.  Bar: the reference's layer test, rel-L2 < 2e-2
+    (tests/u15-layer0-test.cc:293-299), on the output and on the layer's
+    change to x; the other expert's weights must miss it.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import u15h
+from helpers import host_bits, host_f32, max_rel, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+H, NH, KV, HD, I = 4096, 32, 8, 128, 12288
+D_T, D_H = HD // 2, HD // 4
+
+
+def _bf16(g, shape, std=1.0, mean=0.0):
+    return (torch.randn(*shape, generator=g, device="cuda") * std + mean).to(torch.bfloat16)
+
+
+def _f32(t):
+    return oracle.bf16_to_f32(host_bits(t))
+
+
+@pytest.mark.parametrize("rows,dim", [(4224, 4096), (37, 8), (5, 136), (64, 2048),
+                                      (9, 4104), (3, 8200), (2, 16384)])
+def test_rms_norm_vs_reference(ops, rows, dim):
+    if oracle.ref_lib() is None:
+        pytest.skip("the compiled reference (oracle/_ref) is not built")
+    g = torch.Generator(device="cuda").manual_seed(rows * 7 + dim)
+    x = _bf16(g, (rows, dim), 2.0)
+    w = _bf16(g, (dim,), 0.2, 1.0)
+    y = torch.full((rows, dim), float("nan"), dtype=torch.bfloat16, device="cuda")
+    ops.rms_norm(x, w, y)
+    torch.cuda.synchronize()
+    ref = oracle.ref_rms_norm(_f32(x), _f32(w))
+    got = host_bits(y)
+    want = oracle.f32_to_bf16(ref)
+    # one rounding from f32 sums against one from double sums: at most one
+    # bf16 step apart, and equal almost everywhere
+    step = np.abs(got.astype(np.int32) - want.astype(np.int32))
+    assert step.max() <= 1
+    assert np.mean(step == 0) > 0.99
+    assert rel_l2(oracle.bf16_to_f32(got), ref) < 4e-3
+    # in place
+    x2 = x.clone()
+    ops.rms_norm(x2, w, x2)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_bits(x2), got)
+
+
+@pytest.mark.parametrize("rows,dim", [(4224, 4096), (33, 8), (7, 2056), (5, 12288)])
+def test_rms_norm_quant_equals_norm_then_quantiser(ops, rows, dim):
+    g = torch.Generator(device="cuda").manual_seed(dim + 3)
+    x = _bf16(g, (rows, dim), 1.5)
+    x[0].zero_()                               # an all-zero row: scale 0
+    w = _bf16(g, (dim,), 0.2, 1.0)
+    y = torch.empty(rows, dim, dtype=torch.bfloat16, device="cuda")
+    ops.rms_norm(x, w, y)
+    q1 = torch.empty(rows, dim, dtype=torch.int8, device="cuda")
+    s1 = torch.empty(rows, dtype=torch.float32, device="cuda")
+    ops.quant_rows_i8(y, q1, s1)
+    q2 = torch.full((rows, dim), 99, dtype=torch.int8, device="cuda")
+    s2 = torch.full((rows,), -1.0, dtype=torch.float32, device="cuda")
+    y2 = torch.full((rows, dim), float("nan"), dtype=torch.bfloat16, device="cuda")
+    ops.rms_norm_quant_i8(x, w, q2, s2, y=y2)
+    q3 = torch.full((rows, dim), 99, dtype=torch.int8, device="cuda")
+    s3 = torch.full((rows,), -1.0, dtype=torch.float32, device="cuda")
+    ops.rms_norm_quant_i8(x, w, q3, s3)             # without y
+    torch.cuda.synchronize()
+    assert np.array_equal(host_bits(y2), host_bits(y))
+    for q, s in ((q2, s2), (q3, s3)):
+        assert torch.equal(q, q1) and torch.equal(s, s1)
+    qo, so = oracle.quant_rows_i8(host_bits(y))
+    assert np.array_equal(q2.cpu().numpy(), qo) and np.array_equal(s2.cpu().numpy(), so)
+    assert s2[0].item() == 0.0 and not torch.any(q2[0] != 0).item()
+
+
+@pytest.mark.parametrize("n,off", [(4224 * 4096, 0), (8, 0), (13, 0), (1001, 3), (65536 + 5, 1)])
+def test_add_bit_exact(ops, n, off):
+    g = torch.Generator(device="cuda").manual_seed(n % 1000 + off)
+    a = _bf16(g, (n + off,), 3.0)
+    b = _bf16(g, (n + off,), 0.5)
+    a0, b0 = host_bits(a), host_bits(b)
+    dst, src = a[off:], b[off:]                  # offset views: misaligned
+    ops.add(dst, src)
+    torch.cuda.synchronize()
+    want = oracle.f32_to_bf16(oracle.bf16_to_f32(a0[off:]) + oracle.bf16_to_f32(b0[off:]))
+    got = host_bits(a)
+    assert np.array_equal(got[off:], want)
+    assert np.array_equal(got[:off], a0[:off]) and np.array_equal(host_bits(b), b0)
+
+
+def test_norm_and_add_refuse_bad_shapes(ops):
+    x = torch.zeros(4, 12, dtype=torch.bfloat16, device="cuda")
+    w = torch.ones(12, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(u15h.U15hError, match="dim"):
+        ops.rms_norm(x, w, x)                    # 12 is not a multiple of 8
+    x = torch.zeros(4, 16, dtype=torch.bfloat16, device="cuda")
+    w = torch.ones(16, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(u15h.U15hError, match="eps"):
+        ops.rms_norm(x, w, x, eps=-1.0)
+    with pytest.raises(ValueError):
+        ops.add(x, torch.zeros(3, dtype=torch.bfloat16, device="cuda"))
+
+
+# ---- one whole decoder layer --------------------------------------------------
+
+def _expert(g):
+    w = {"input_layernorm": _bf16(g, (H,), 0.2, 1.0),
+         "post_attention_layernorm": _bf16(g, (H,), 0.2, 1.0),
+         "q_proj": _bf16(g, (NH * HD, H), 0.02), "k_proj": _bf16(g, (KV * HD, H), 0.02),
+         "v_proj": _bf16(g, (KV * HD, H), 0.02), "o_proj": _bf16(g, (H, NH * HD), 0.02),
+         "q_norm": _bf16(g, (HD // 2,), 0.2, 1.0), "k_norm": _bf16(g, (HD // 2,), 0.2, 1.0),
+         "q_norm_hw": _bf16(g, (HD // 2,), 0.2, 1.0), "k_norm_hw": _bf16(g, (HD // 2,), 0.2, 1.0),
+         "gate_proj": _bf16(g, (I, H), 0.02), "up_proj": _bf16(g, (I, H), 0.02),
+         "down_proj": _bf16(g, (H, I), 0.02)}
+    return w
+
+
+def _layer_gpu(ops, x, w, other, gen, pos, mode, t_index):
+    """layer_step_ for one expert's pass of T tokens: `w` is the pass's
+    expert, `other` the idle one (the grouped launches take both; every row
+    belongs to `w`)."""
+    T = x.shape[0]
+    Mu, Mg = (0, T) if gen else (T, 0)
+    und, gen_w = (other, w) if gen else (w, other)
+    dev = torch.device("cuda")
+
+    def proj(inp, K, names, outs):
+        ops.mot_linear(inp, Mu, Mg, K, [dict(w_und=und[n], w_gen=gen_w[n], y=y)
+                                        for n, y in zip(names, outs)])
+
+    normed = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    ops.rms_norm(x, w["input_layernorm"], normed)
+    q = torch.empty(T, NH * HD, dtype=torch.bfloat16, device=dev)
+    k = torch.empty(T, KV * HD, dtype=torch.bfloat16, device=dev)
+    v = torch.empty(T, KV * HD, dtype=torch.bfloat16, device=dev)
+    proj(normed, H, ("q_proj", "k_proj", "v_proj"), (q, k, v))
+    cs, sn = (torch.from_numpy(a).to(dev) for a in
+              u15h.build_rope_tables(*pos, HD, D_T, D_H))
+    kc = torch.empty(KV, T, HD, dtype=torch.bfloat16, device=dev)
+    vc = torch.empty(KV, T, HD, dtype=torch.bfloat16, device=dev)
+    norms = dict(q_t=w["q_norm"], q_hw=w["q_norm_hw"], k_t=w["k_norm"], k_hw=w["k_norm_hw"])
+    ops.mot_attention_prologue(q, k, v, None if gen else norms, norms if gen else None,
+                               cs, sn, Mu, Mg, NH, KV, HD, D_T, D_H, kc, vc)
+    attn = torch.empty(T, NH * HD, dtype=torch.bfloat16, device=dev)
+    ops.attention_token_major(q, kc, vc, attn, NH, KV, T, mode=mode, t_index=t_index)
+    h1 = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    proj(attn, NH * HD, ("o_proj",), (h1,))
+    ops.add(h1, x)                                   # proj = o + x
+    n2 = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    ops.rms_norm(h1, w["post_attention_layernorm"], n2)
+    ff = torch.empty(T, I, dtype=torch.bfloat16, device=dev)
+    ops.mot_gate_up_swiglu(n2, Mu, Mg, H, und["gate_proj"], und["up_proj"],
+                           gen_w["gate_proj"], gen_w["up_proj"], ff)
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    proj(ff, I, ("down_proj",), (out,))
+    ops.add(out, h1)                                 # out = proj + down
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("expert", ["gen", "und"])
+def test_decoder_layer_vs_reference(ops, expert):
+    if oracle.ref_lib() is None:
+        pytest.skip("the compiled reference (oracle/_ref) is not built")
+    gen = expert == "gen"
+    T = 64
+    g = torch.Generator(device="cuda").manual_seed(4100 + gen)
+    W = {"und": _expert(g), "gen": _expert(g)}
+    x = _bf16(g, (T, H))
+    if gen:      # an 8 x 8 patch grid sharing one temporal position
+        pos = (np.full(T, 17, np.int32), np.repeat(np.arange(8), 8).astype(np.int32),
+               np.tile(np.arange(8), 8).astype(np.int32))
+        mode, t_index, mask = 0, None, None
+    else:        # text: one position per token, block-causal = causal
+        pos = (np.arange(T, dtype=np.int32),) * 3
+        mode = 2
+        t_index = torch.from_numpy(pos[0]).cuda()
+        mask = oracle.ref_block_causal_mask(pos[0])
+    w, other = (W["gen"], W["und"]) if gen else (W["und"], W["gen"])
+    got = host_f32(_layer_gpu(ops, x, w, other, gen, pos, mode, t_index))
+    assert np.all(np.isfinite(got))
+
+    xf = _f32(x)
+
+    def ref(weights):
+        return oracle.ref_decoder_layer(xf, {n: _f32(t) for n, t in weights.items()},
+                                        NH, KV, HD, *pos, mask=mask)
+
+    want = ref(w)
+    assert rel_l2(got, want) < 2e-2
+    assert rel_l2(got - xf, want - xf) < 2e-2       # the layer's change to x
+    assert max_rel(got - xf, want - xf) <= 2e-2
+    # the pass's expert is load-bearing
+    assert rel_l2(got - xf, ref(other) - xf) > 2e-2

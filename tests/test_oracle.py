@@ -591,3 +591,59 @@ def test_attention_controls_and_closed_forms():
     # one key: the output is that key's value row
     one = oracle.attention(q, k, v, hkv, 1)
     assert np.allclose(one, np.repeat(v[:, :1], hq // hkv, axis=0).repeat(T, 1), atol=1e-7)
+
+
+def _tiny_layer(rng, hidden=64, heads=4, kv=2, hd=16, inter=96):
+    w = {"input_layernorm": 1 + 0.2 * rng.standard_normal(hidden),
+         "post_attention_layernorm": 1 + 0.2 * rng.standard_normal(hidden),
+         "q_proj": 0.1 * rng.standard_normal((heads * hd, hidden)),
+         "k_proj": 0.1 * rng.standard_normal((kv * hd, hidden)),
+         "v_proj": 0.1 * rng.standard_normal((kv * hd, hidden)),
+         "o_proj": 0.1 * rng.standard_normal((hidden, heads * hd)),
+         "q_norm": 1 + 0.2 * rng.standard_normal(hd // 2),
+         "k_norm": 1 + 0.2 * rng.standard_normal(hd // 2),
+         "q_norm_hw": 1 + 0.2 * rng.standard_normal(hd // 2),
+         "k_norm_hw": 1 + 0.2 * rng.standard_normal(hd // 2),
+         "gate_proj": 0.1 * rng.standard_normal((inter, hidden)),
+         "up_proj": 0.1 * rng.standard_normal((inter, hidden)),
+         "down_proj": 0.1 * rng.standard_normal((hidden, inter))}
+    return {k: v.astype(np.float32) for k, v in w.items()}
+
+
+@pytest.mark.skipif(not REF, reason="reference CPU path not built")
+@pytest.mark.parametrize("masked", [False, True])
+def test_decoder_layer_wrapper_is_the_reference_composition(masked):
+    """oracle.ref_decoder_layer (the compiled u15::ref::decoder_layer through
+    its C shim) against the same layer composed step by step from the
+    reference's own pieces (src/u15-ref.cc:242-311): rms_norm, the split
+    q/k projection, v, attention, o + residual, rms_norm, SwiGLU MLP +
+    residual.  Every step is f32 in the same order, so the two agree bit
+    for bit; a wrong argument order in the shim (a swapped weight, head
+    count or position array) does not."""
+    rng = np.random.default_rng(77)
+    T, hidden, heads, kv, hd, inter = 6, 64, 4, 2, 16, 96
+    w = _tiny_layer(rng, hidden, heads, kv, hd, inter)
+    x = rng.standard_normal((T, hidden)).astype(np.float32)
+    pt = np.array([0, 1, 2, 3, 3, 3], np.int32)
+    ph = np.array([0, 0, 0, 0, 1, 1], np.int32)
+    pw = np.array([0, 0, 0, 0, 0, 1], np.int32)
+    mask = oracle.ref_block_causal_mask(pt) if masked else None
+    got = oracle.ref_decoder_layer(x, w, heads, kv, hd, pt, ph, pw, mask)
+
+    normed = oracle.ref_rms_norm(x, w["input_layernorm"])
+    q = oracle.ref_split_rope_project(normed, w["q_proj"], w["q_norm"], w["q_norm_hw"],
+                                      pt, ph, pw, heads, hd)
+    k = oracle.ref_split_rope_project(normed, w["k_proj"], w["k_norm"], w["k_norm_hw"],
+                                      pt, ph, pw, kv, hd)
+    v = oracle.ref_linear(normed, w["v_proj"]).reshape(T, kv, hd).transpose(1, 0, 2)
+    att = oracle.ref_attention(q, k, np.ascontiguousarray(v), mask, kv)
+    proj = oracle.ref_linear(att, w["o_proj"]) + x
+    n2 = oracle.ref_rms_norm(proj, w["post_attention_layernorm"])
+    g = oracle.ref_silu(oracle.ref_linear(n2, w["gate_proj"]))
+    u = oracle.ref_linear(n2, w["up_proj"])
+    want = proj + oracle.ref_linear(g * u, w["down_proj"])
+    assert np.array_equal(got, want)
+    # the shim's weight order is load-bearing
+    w2 = dict(w, q_norm=w["k_norm"], k_norm=w["q_norm"])
+    assert not np.array_equal(oracle.ref_decoder_layer(x, w2, heads, kv, hd, pt, ph, pw, mask),
+                              got)

@@ -693,6 +693,72 @@ u15h_swiglu(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* gate,
                   "swiglu");
 }
 
+static u15h_status
+rms_norm_call(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
+              const u15h_bf16* w, int rows, int dim, float eps, u15h_bf16* y,
+              int8_t* q, float* s, const char* what)
+{
+  if (ctx == nullptr) { return U15H_EINVAL; }
+  if (rows < 0 || dim <= 0 || dim % 8 != 0 || dim > 16384) {
+    return fail(ctx, U15H_EINVAL, "%s: rows=%d dim=%d (dim %% 8 == 0, <= 16384)",
+                what, rows, dim);
+  }
+  if (!(eps >= 0.0f)) {
+    return fail(ctx, U15H_EINVAL, "%s: eps must be >= 0", what);
+  }
+  if (rows == 0) { ctx->err.clear(); return U15H_OK; }
+  const bool quant = q != nullptr || s != nullptr;
+  if (x == nullptr || w == nullptr || !aligned16(x) || !aligned16(w) ||
+      (!quant && y == nullptr) || (y != nullptr && !aligned16(y)) ||
+      (quant && (q == nullptr || s == nullptr || !aligned16(q) || !aligned16(s)))) {
+    return fail(ctx, U15H_EINVAL, "%s: null or misaligned operand", what);
+  }
+  u15h_status st = bind_device(ctx);
+  if (st != U15H_OK) { return st; }
+  return launched(ctx,
+                  u15h::launch_rms_norm(x, w, rows, dim, eps, y, q, s,
+                                        as_stream(stream)),
+                  what);
+}
+
+u15h_status
+u15h_rms_norm(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
+              const u15h_bf16* w, u15h_bf16* y, int rows, int dim, float eps)
+{
+  if (ctx != nullptr && y == nullptr && rows > 0) {
+    return fail(ctx, U15H_EINVAL, "rms_norm: null output");
+  }
+  return rms_norm_call(ctx, stream, x, w, rows, dim, eps, y, nullptr, nullptr,
+                       "rms_norm");
+}
+
+u15h_status
+u15h_rms_norm_quant_i8(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
+                       const u15h_bf16* w, int rows, int dim, float eps,
+                       u15h_bf16* y, int8_t* q, float* s)
+{
+  if (ctx != nullptr && rows > 0 && (q == nullptr || s == nullptr)) {
+    return fail(ctx, U15H_EINVAL, "rms_norm_quant_i8: null codes or scales");
+  }
+  return rms_norm_call(ctx, stream, x, w, rows, dim, eps, y, q, s,
+                       "rms_norm_quant_i8");
+}
+
+u15h_status
+u15h_add(u15h_ctx* ctx, u15h_stream stream, u15h_bf16* dst,
+         const u15h_bf16* src, int64_t n)
+{
+  if (ctx == nullptr) { return U15H_EINVAL; }
+  if (n < 0) { return fail(ctx, U15H_EINVAL, "add: n=%lld", (long long)n); }
+  if (n == 0) { ctx->err.clear(); return U15H_OK; }
+  if (dst == nullptr || src == nullptr) {
+    return fail(ctx, U15H_EINVAL, "add: null operand");
+  }
+  u15h_status st = bind_device(ctx);
+  if (st != U15H_OK) { return st; }
+  return launched(ctx, u15h::launch_add_bf16(dst, src, n, as_stream(stream)), "add");
+}
+
 u15h_status
 u15h_mot_gate_up_swiglu(u15h_ctx* ctx, u15h_stream stream,
                         const u15h_bf16* x, int M_und, int M_gen, int K,

@@ -152,6 +152,16 @@ hipError_t launch_quant_rows_i8(const uint16_t* x, int rows, int K,
                                 int8_t* q, float* sc, hipStream_t s,
                                 hipEvent_t start = nullptr,
                                 hipEvent_t end = nullptr);
+// Whole-row RMSNorm with gain, dim <= 16384, dim % 8 == 0, x, w, y
+// 16-byte aligned: y = bf16((x * inv) * w).  With q not null it also
+// quantises the row's bf16 results to int8 codes q and scale sc (y then
+// optional), equal to launch_quant_rows_i8 on y.
+hipError_t launch_rms_norm(const uint16_t* x, const uint16_t* w, int rows,
+                           int dim, float eps, uint16_t* y, int8_t* q,
+                           float* sc, hipStream_t s);
+// dst[i] = bf16(f32(dst[i]) + f32(src[i])), any n and alignment.
+hipError_t launch_add_bf16(uint16_t* dst, const uint16_t* src, int64_t n,
+                           hipStream_t s);
 hipError_t launch_swiglu(const uint16_t* g, const uint16_t* u, uint16_t* o,
                          int64_t n, hipStream_t s);
 hipError_t launch_dequant_affine(const uint32_t* codes, const uint16_t* sc,

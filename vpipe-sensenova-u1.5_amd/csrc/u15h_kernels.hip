@@ -1429,6 +1429,141 @@ quant_rows_i8_waves_kernel(const uint16_t* __restrict__ x, int rows, int K,
   }
 }
 
+// ---- RMSNorm with gain, and its int8 form -----------------------------------
+// Rows normalised by whole waves, the quantiser's layout: WPR waves per row
+// (one row per workgroup), each lane holding CPL 16-byte chunks of its row
+// in registers (dim <= 512 * WPR * CPL); chunk i of wave p, lane l is
+// chunk i * 64 * WPR + p * 64 + l.  Loads past the row read zeros through
+// the buffer resource's range and stores past it are dropped.
+//   y = bf16((x * inv) * w),  inv = rsqrt(sum(x^2) / dim + eps),
+// the sum in f32 (lane partials, then the wave and the row by xor shuffles
+// and LDS).  QUANT: the row's bf16 results, as they would be read back,
+// give its int8 scale and codes by the quantiser's own steps (absmax8,
+// quant8), so (q, sc) equal quant_rows_i8 applied to y bit for bit; y
+// itself is stored only when `y` is not null.  y may be x: every store of
+// a row depends on the row's sum, so all of its loads come first.
+template <int WPR, int CPL, bool QUANT>
+__global__ __launch_bounds__(64 * WPR) void
+rms_norm_rows_kernel(const uint16_t* x, const uint16_t* __restrict__ w, int dim,
+                     float eps, uint16_t* y, int8_t* __restrict__ q,
+                     float* __restrict__ sc)
+{
+  const int part = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x;
+  const __amdgpu_buffer_rsrc_t src = make_rsrc(x + (size_t)r * dim, dim * 2);
+  const __amdgpu_buffer_rsrc_t wsrc = make_rsrc(w, dim * 2);
+  u32x4_t v[CPL], g[CPL];
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = i * 64 * WPR + part * 64 + lane;
+    v[i] = __builtin_amdgcn_raw_buffer_load_b128(src, c * 16, 0, 0);
+    g[i] = __builtin_amdgcn_raw_buffer_load_b128(wsrc, c * 16, 0, 0);
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const uint32_t wv[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = __uint_as_float(wv[e] << 16);
+      const float hi = __uint_as_float(wv[e] & 0xffff0000u);
+      ss += lo * lo;
+      ss += hi * hi;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) { ss += __shfl_xor(ss, o); }
+  __shared__ float red[2][WPR];
+  if constexpr (WPR > 1) {
+    if (lane == 0) { red[0][part] = ss; }
+    __syncthreads();
+    ss = red[0][0];
+#pragma unroll
+    for (int p = 1; p < WPR; ++p) { ss += red[0][p]; }
+  }
+  const float inv = rsqrtf(ss / (float)dim + eps);
+  uint4 out[CPL];
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const uint32_t xv[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+    const uint32_t gv[4] = {g[i].x, g[i].y, g[i].z, g[i].w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = (__uint_as_float(xv[e] << 16) * inv) * __uint_as_float(gv[e] << 16);
+      const float hi = (__uint_as_float(xv[e] & 0xffff0000u) * inv) *
+                       __uint_as_float(gv[e] & 0xffff0000u);
+      o[e] = pack_bf16x2(lo, hi);
+    }
+    out[i] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+  if (!QUANT || y != nullptr) {
+    const __amdgpu_buffer_rsrc_t dst = make_rsrc(y + (size_t)r * dim, dim * 2);
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = i * 64 * WPR + part * 64 + lane;
+      __builtin_amdgcn_raw_buffer_store_b128(
+          (u32x4_t){out[i].x, out[i].y, out[i].z, out[i].w}, dst, c * 16, 0, 0);
+    }
+  }
+  if constexpr (QUANT) {
+    // chunks past the row hold bf16(0 * inv * 0) = 0: they leave the
+    // absmax alone and their codes are dropped by the range
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) { amax = absmax8(out[i], amax); }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) { amax = fmaxf(amax, __shfl_xor(amax, o)); }
+    if constexpr (WPR > 1) {
+      if (lane == 0) { red[1][part] = amax; }
+      __syncthreads();
+      amax = red[1][0];
+#pragma unroll
+      for (int p = 1; p < WPR; ++p) { amax = fmaxf(amax, red[1][p]); }
+    }
+    const float s = amax / 127.0f;
+    const float qinv = s != 0.0f ? 1.0f / s : 0.0f;
+    // 1/s overflows for rows with absmax below ~3.7e-37: division only.
+    const bool fast = qinv <= 3.4028234663852886e38f;
+    if (part == 0 && lane == 0) { sc[r] = s; }
+    const __amdgpu_buffer_rsrc_t qd = make_rsrc(q + (size_t)r * dim, dim);
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = i * 64 * WPR + part * 64 + lane;
+      const uint2 o = quant8(out[i], s, qinv, fast);
+      __builtin_amdgcn_raw_buffer_store_b64((u32x2_t){o.x, o.y}, qd, c * 8, 0, 0);
+    }
+  }
+}
+
+// ---- dst += src, the residual add (bf16, f32 add, one rounding) ------------
+// Eight elements per thread where both pointers are 16-byte aligned; the
+// tail (and misaligned operands) one element per thread.
+__global__ __launch_bounds__(256) void
+add_bf16_kernel(uint16_t* __restrict__ dst, const uint16_t* __restrict__ src,
+                int64_t n, int64_t nvec)
+{
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nvec; i += stride) {
+    const uint4 a = reinterpret_cast<const uint4*>(dst)[i];
+    const uint4 b = reinterpret_cast<const uint4*>(src)[i];
+    const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
+    const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o[e] = pack_bf16x2(__uint_as_float(aw[e] << 16) + __uint_as_float(bw[e] << 16),
+                         __uint_as_float(aw[e] & 0xffff0000u) +
+                             __uint_as_float(bw[e] & 0xffff0000u));
+    }
+    reinterpret_cast<uint4*>(dst)[i] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+  for (int64_t i = nvec * 8 + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
+    dst[i] = (uint16_t)bf16_bits(bf16_to_f32(dst[i]) + bf16_to_f32(src[i]));
+  }
+}
+
 // ---- elementwise SwiGLU: out = silu(g) * u ------------------------------
 __global__ __launch_bounds__(256) void
 swiglu_kernel(const uint4* __restrict__ g, const uint4* __restrict__ u,
@@ -3204,6 +3339,49 @@ launch_quant_rows_i8(const uint16_t* x, int rows, int K, int8_t* q,
 }
 
 hipError_t
+launch_rms_norm(const uint16_t* x, const uint16_t* w, int rows, int dim, float eps,
+                uint16_t* y, int8_t* q, float* sc, hipStream_t s)
+{
+  if (rows <= 0) { return hipSuccess; }
+  const bool quant = q != nullptr;
+  // one row per workgroup: four waves up to 8192 columns, eight above
+#define U15H_NORM(WPR, CPL)                                                   \
+  do {                                                                        \
+    if (quant) {                                                              \
+      hipLaunchKernelGGL((rms_norm_rows_kernel<WPR, CPL, true>), dim3(rows),  \
+                         dim3(64 * WPR), 0, s, x, w, dim, eps, y, q, sc);     \
+    } else {                                                                  \
+      hipLaunchKernelGGL((rms_norm_rows_kernel<WPR, CPL, false>), dim3(rows), \
+                         dim3(64 * WPR), 0, s, x, w, dim, eps, y, q, sc);     \
+    }                                                                         \
+  } while (0)
+  if (dim <= 2048) {
+    U15H_NORM(4, 1);
+  } else if (dim <= 4096) {
+    U15H_NORM(4, 2);
+  } else if (dim <= 8192) {
+    U15H_NORM(4, 4);
+  } else {
+    U15H_NORM(8, 4);
+  }
+#undef U15H_NORM
+  return hipGetLastError();
+}
+
+hipError_t
+launch_add_bf16(uint16_t* dst, const uint16_t* src, int64_t n, hipStream_t s)
+{
+  if (n <= 0) { return hipSuccess; }
+  const bool vec = (reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) % 16 == 0;
+  const int64_t nvec = vec ? n / 8 : 0;
+  const int64_t work = nvec > 0 ? nvec : n;
+  const int64_t want = (work + 255) / 256;
+  hipLaunchKernelGGL(add_bf16_kernel, dim3((unsigned)(want < 8192 ? want : 8192)),
+                     dim3(256), 0, s, dst, src, n, nvec);
+  return hipGetLastError();
+}
+
+hipError_t
 launch_swiglu(const uint16_t* g, const uint16_t* u, uint16_t* o, int64_t n,
               hipStream_t s)
 {
@@ -3487,6 +3665,15 @@ kernels_loadable()
       reinterpret_cast<const void*>(&split_norm_rope_vec_kernel<true, false>),
       reinterpret_cast<const void*>(&split_norm_rope_vec_kernel<false, true>),
       reinterpret_cast<const void*>(&attention_prologue_kernel<1>),
+      reinterpret_cast<const void*>(&rms_norm_rows_kernel<4, 1, false>),
+      reinterpret_cast<const void*>(&rms_norm_rows_kernel<4, 2, false>),
+      reinterpret_cast<const void*>(&rms_norm_rows_kernel<4, 4, false>),
+      reinterpret_cast<const void*>(&rms_norm_rows_kernel<8, 4, false>),
+      reinterpret_cast<const void*>(&rms_norm_rows_kernel<4, 1, true>),
+      reinterpret_cast<const void*>(&rms_norm_rows_kernel<4, 2, true>),
+      reinterpret_cast<const void*>(&rms_norm_rows_kernel<4, 4, true>),
+      reinterpret_cast<const void*>(&rms_norm_rows_kernel<8, 4, true>),
+      reinterpret_cast<const void*>(&add_bf16_kernel),
       reinterpret_cast<const void*>(&attention_prologue_kernel<2>),
       reinterpret_cast<const void*>(&attention_prologue_kernel<4>),
       reinterpret_cast<const void*>(&quant_rows_i8_waves_kernel<4, 1, 1>),

@@ -134,6 +134,10 @@ def load_library() -> ctypes.CDLL:
                                             ctypes.POINTER(_QkNorm), vp, vp,
                                             i, i, i, i, i, i, i,
                                             ctypes.c_float, vp, vp, i, i]),
+        "u15h_rms_norm": (i, [vp, vp, vp, vp, vp, i, i, ctypes.c_float]),
+        "u15h_rms_norm_quant_i8": (i, [vp, vp, vp, vp, i, i, ctypes.c_float,
+                                       vp, vp, vp]),
+        "u15h_add": (i, [vp, vp, vp, vp, i64]),
         "u15h_build_rope_tables": (i, [vp, vp, vp, i, i, i, i,
                                        ctypes.c_double, ctypes.c_double, vp,
                                        vp]),
@@ -808,6 +812,48 @@ class Ops:
             _ptr(cos), _ptr(sin), M_und, M_gen, hq, hkv, head_dim, d_t, d_h,
             eps, _ptr(k_cache), _ptr(v_cache), cap, offset)
         self._check(st, "u15h_mot_attention_prologue")
+
+    # ---- the layer norms and the residual add --------------------------
+    def rms_norm(self, x, w, y, eps=1e-6, stream=None):
+        """MetalOps::rms_norm: y [rows][dim] = bf16((x * inv) * w); y may
+        be x."""
+        if x.dim() != 2:
+            raise ValueError("x must be [rows][dim]")
+        rows, dim = x.shape
+        _need(x, torch.bfloat16, (rows, dim), "x")
+        _need(w, torch.bfloat16, (dim,), "w")
+        _need(y, torch.bfloat16, (rows, dim), "y")
+        st = self._lib.u15h_rms_norm(self._ctx, _stream(stream), _ptr(x), _ptr(w),
+                                     _ptr(y), rows, dim, eps)
+        self._check(st, "u15h_rms_norm")
+
+    def rms_norm_quant_i8(self, x, w, q, s, y=None, eps=1e-6, stream=None):
+        """The norm with the int8 tier's per-token quantisation of its bf16
+        results: q [rows][dim] int8, s [rows] f32 (and y when given)."""
+        if x.dim() != 2:
+            raise ValueError("x must be [rows][dim]")
+        rows, dim = x.shape
+        _need(x, torch.bfloat16, (rows, dim), "x")
+        _need(w, torch.bfloat16, (dim,), "w")
+        _need(q, torch.int8, (rows, dim), "q")
+        _need(s, torch.float32, (rows,), "s")
+        if y is not None:
+            _need(y, torch.bfloat16, (rows, dim), "y")
+        st = self._lib.u15h_rms_norm_quant_i8(self._ctx, _stream(stream), _ptr(x),
+                                              _ptr(w), rows, dim, eps, _ptr(y),
+                                              _ptr(q), _ptr(s))
+        self._check(st, "u15h_rms_norm_quant_i8")
+
+    def add(self, dst, src, stream=None):
+        """MetalOps::add: dst += src elementwise (bf16, f32 add)."""
+        if dst.numel() != src.numel():
+            raise ValueError("dst and src must have the same length")
+        for name, t in (("dst", dst), ("src", src)):
+            if t.dtype != torch.bfloat16 or not t.is_contiguous() or t.device.type != "cuda":
+                raise ValueError(f"{name} must be a contiguous bf16 GPU tensor")
+        st = self._lib.u15h_add(self._ctx, _stream(stream), _ptr(dst), _ptr(src),
+                                dst.numel())
+        self._check(st, "u15h_add")
 
     # ---- attention -------------------------------------------------------
     def sdpa(self, q, k, v, out, hkv, tk, causal=False, q_offset=0,
