@@ -115,7 +115,7 @@ def parse(argv=None):
     ap.add_argument("--no-stack", action="store_true",
                     help="skip the config-5 42-layer stack passes")
     ap.add_argument("--attn-only", action="store_true",
-                    help="only the attention and norm/RoPE measurements "
+                    help="only the attention, norm/RoPE and layer-op measurements "
                          "(--steps launches), printed as their own JSON object")
     ap.add_argument("--m-sweep", action="store_true",
                     help="only the M sweep of the dense / dequant-once / int8 "
@@ -833,6 +833,52 @@ def prologue_measure(torch, ops, gen, launches, cs, sn):
                          "unit": "GB/s", "frac": round(gbs / PEAK_HBM, 4)}}
 
 
+def layer_ops_measure(torch, ops, gen, launches):
+    """The ops either side of the projections at config 2's 4224 x 4096
+    rows: the layer RMSNorm (u15h_rms_norm), its int8 form that also
+    quantises the normed rows per token (u15h_rms_norm_quant_i8, against
+    the norm and the quantiser as two launches), and the residual add
+    (u15h_add).  All HBM-bound; bytes are each launch's reads and writes."""
+    T, Hd = 4224, HIDDEN
+    x = torch.randn(T, Hd, generator=gen, device="cuda").to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(Hd, generator=gen, device="cuda")).to(torch.bfloat16)
+    y = torch.empty_like(x)
+    r = torch.randn(T, Hd, generator=gen, device="cuda").to(torch.bfloat16)
+    q = torch.empty(T, Hd, dtype=torch.int8, device="cuda")
+    sx = torch.empty(T, dtype=torch.float32, device="cuda")
+    calls = {
+        "rms_norm": (lambda: ops.rms_norm(x, w, y), 2 * T * Hd * 2 + Hd * 2),
+        "rms_norm_quant_i8": (lambda: ops.rms_norm_quant_i8(x, w, q, sx),
+                              T * Hd * 2 + T * Hd + T * 4 + Hd * 2),
+        "rms_norm_then_quant_rows_i8": (
+            lambda: (ops.rms_norm(x, w, y), ops.quant_rows_i8(y, q, sx)),
+            2 * T * Hd * 2 + Hd * 2 + T * Hd * 2 + T * Hd + T * 4),
+        "add": (lambda: ops.add(y, r), 3 * T * Hd * 2),
+    }
+    hev = HipEvents()
+    stream = torch.cuda.current_stream()
+    out = {"shape": {"rows": T, "dim": Hd}}
+    for name, (fn, nbytes) in calls.items():
+        for _ in range(3):
+            fn()
+        e0, e1 = hev.create(), hev.create()
+        torch.cuda.synchronize()
+        hev.record(e0, stream)
+        for _ in range(launches):
+            fn()
+        hev.record(e1, stream)
+        torch.cuda.synchronize()
+        ms = hev.elapsed(e0, e1) / launches
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"avg_ms": round(ms, 5), "alg_bytes": nbytes,
+                     "achieved_GBps": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM, 4)}
+    hev.close()
+    out["kernels"] = {"rms_norm": "rms_norm_rows_kernel<4, 2, false>",
+                      "rms_norm_quant_i8": "rms_norm_rows_kernel<4, 2, true>",
+                      "add": "add_bf16_kernel"}
+    return out
+
+
 def norm_rope_measure(torch, ops, gen, launches):
     """Average launch time of the fused split q/k norm + split RoPE pass
     over config 2's q (32 heads) and k (8 heads) rows: 4224 tokens,
@@ -1046,6 +1092,7 @@ def main(argv=None):
         res = attention_measure(torch, ops, gen, args.steps)
         res["masks"] = attention_masks_measure(torch, ops, gen, args.steps)
         res["split_norm_rope"] = norm_rope_measure(torch, ops, gen, args.steps)
+        res["layer_ops"] = layer_ops_measure(torch, ops, gen, args.steps)
         print(json.dumps(res), flush=True)
         ops.close()
         return
@@ -1127,6 +1174,7 @@ def main(argv=None):
         result["attention"] = attention_measure(torch, ops, gen, args.steps)
         result["attention"]["masks"] = attention_masks_measure(torch, ops, gen, args.steps)
         result["split_norm_rope"] = norm_rope_measure(torch, ops, gen, args.steps)
+        result["layer_ops"] = layer_ops_measure(torch, ops, gen, args.steps)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
         side = args.cpu_seconds / 3

@@ -209,8 +209,12 @@ def test_decoder_layer_vs_reference(ops, expert):
                                         NH, KV, HD, *pos, mask=mask)
 
     want = ref(w)
+    bad = ref(other)
+    print(f"{expert}: rel-L2 {rel_l2(got, want):.3e}, of the change to x "
+          f"{rel_l2(got - xf, want - xf):.3e}, max-rel {max_rel(got - xf, want - xf):.3e}; "
+          f"other expert {rel_l2(got - xf, bad - xf):.3e}")
     assert rel_l2(got, want) < 2e-2
     assert rel_l2(got - xf, want - xf) < 2e-2       # the layer's change to x
     assert max_rel(got - xf, want - xf) <= 2e-2
     # the pass's expert is load-bearing
-    assert rel_l2(got - xf, ref(other) - xf) > 2e-2
+    assert rel_l2(got - xf, bad - xf) > 2e-2
