@@ -833,6 +833,115 @@ def prologue_measure(torch, ops, gen, launches, cs, sn):
                          "unit": "GB/s", "frac": round(gbs / PEAK_HBM, 4)}}
 
 
+def full_layer_measure(torch, ops, gen, launches):
+    """One whole decoder layer (U15Backbone::layer_step_, src/u15-backbone.cc:
+    193-257) at config 2 as one MoT pass of both groups through the ABI:
+    rms_norm (per group) -> q|k|v -> attention prologue -> block-causal
+    attention over the 4224 tokens (the 128 text tokens causal, the 4096
+    image tokens one block) -> o -> residual add -> rms_norm (per group) ->
+    gate|up with SwiGLU -> down -> residual add.  Random weights of the
+    layer's shapes.  `ms_per_layer` times `launches` whole layers between
+    two events; `ops_ms` times each step alone the same way."""
+    import numpy as np
+    Mu, Mg = 128, 4096
+    T = Mu + Mg
+    HD, NH, KVH = 128, NQ // 128, NKV // 128
+    dev = "cuda"
+
+    def rb(*shape, std=1.0, mean=0.0):
+        return (torch.randn(*shape, generator=gen, device=dev) * std + mean).to(torch.bfloat16)
+
+    W = {}
+    for e in ("und", "gen"):
+        W[e] = {"q": rb(NQ, HIDDEN, std=0.02), "k": rb(NKV, HIDDEN, std=0.02),
+                "v": rb(NKV, HIDDEN, std=0.02), "o": rb(HIDDEN, NQ, std=0.02),
+                "gate": rb(INTER, HIDDEN, std=0.02), "up": rb(INTER, HIDDEN, std=0.02),
+                "down": rb(HIDDEN, INTER, std=0.02),
+                "ln1": rb(HIDDEN, std=0.1, mean=1.0), "ln2": rb(HIDDEN, std=0.1, mean=1.0),
+                "norms": {f: rb(HD // 2, std=0.1, mean=1.0)
+                          for f in ("q_t", "q_hw", "k_t", "k_hw")}}
+    pos_t = np.array(list(range(Mu)) + [Mu] * Mg, np.int32)
+    pos_h = np.array([0] * Mu + [i // 64 for i in range(Mg)], np.int32)
+    pos_w = np.array([0] * Mu + [i % 64 for i in range(Mg)], np.int32)
+    import u15h
+    cs, sn = (torch.from_numpy(a).to(dev) for a in
+              u15h.build_rope_tables(pos_t, pos_h, pos_w, HD, 64, 32))
+    t_index = torch.from_numpy(pos_t).to(dev)
+    x = rb(T, HIDDEN)
+    normed = torch.empty(T, HIDDEN, dtype=torch.bfloat16, device=dev)
+    q = torch.empty(T, NQ, dtype=torch.bfloat16, device=dev)
+    k = torch.empty(T, NKV, dtype=torch.bfloat16, device=dev)
+    v = torch.empty(T, NKV, dtype=torch.bfloat16, device=dev)
+    kc = torch.empty(KVH, T, HD, dtype=torch.bfloat16, device=dev)
+    vc = torch.empty(KVH, T, HD, dtype=torch.bfloat16, device=dev)
+    attn = torch.empty(T, NQ, dtype=torch.bfloat16, device=dev)
+    h1 = torch.empty(T, HIDDEN, dtype=torch.bfloat16, device=dev)
+    ff = torch.empty(T, INTER, dtype=torch.bfloat16, device=dev)
+    out = torch.empty(T, HIDDEN, dtype=torch.bfloat16, device=dev)
+    und, gw = W["und"], W["gen"]
+
+    def norm(src, key):
+        ops.rms_norm(src[:Mu], und[key], normed[:Mu])
+        ops.rms_norm(src[Mu:], gw[key], normed[Mu:])
+
+    def lin(inp, K, pairs):
+        ops.mot_linear(inp, Mu, Mg, K, [dict(w_und=und[n], w_gen=gw[n], y=y)
+                                        for n, y in pairs])
+
+    steps = {
+        "rms_norm x2": lambda: norm(x, "ln1"),
+        "q|k|v": lambda: lin(normed, HIDDEN, (("q", q), ("k", k), ("v", v))),
+        "attention prologue": lambda: ops.mot_attention_prologue(
+            q, k, v, und["norms"], gw["norms"], cs, sn, Mu, Mg, NH, KVH, HD, 64, 32, kc, vc),
+        "attention": lambda: ops.attention_token_major(q, kc, vc, attn, NH, KVH, T, mode=2,
+                                                       t_index=t_index),
+        "o": lambda: lin(attn, NQ, (("o", h1),)),
+        "add": lambda: ops.add(h1, x),
+        "rms_norm x2 (post)": lambda: norm(h1, "ln2"),
+        "gate|up + swiglu": lambda: ops.mot_gate_up_swiglu(normed, Mu, Mg, HIDDEN, und["gate"],
+                                                          und["up"], gw["gate"], gw["up"], ff),
+        "down": lambda: lin(ff, INTER, (("down", out),)),
+        "add (out)": lambda: ops.add(out, h1),
+    }
+
+    def layer():
+        for fn in steps.values():
+            fn()
+
+    hev = HipEvents()
+    stream = torch.cuda.current_stream()
+
+    def timed(fn, n):
+        for _ in range(3):
+            fn()
+        e0, e1 = hev.create(), hev.create()
+        torch.cuda.synchronize()
+        hev.record(e0, stream)
+        for _ in range(n):
+            fn()
+        hev.record(e1, stream)
+        torch.cuda.synchronize()
+        return hev.elapsed(e0, e1) / n
+
+    ms = timed(layer, launches)
+    ops_ms = {name: round(timed(fn, launches), 5) for name, fn in steps.items()}
+    hev.close()
+    proj_flop = 385875968 * T                   # one expert per row
+    pairs = Mu * (Mu + 1) // 2 + Mg * T          # visible (query, key) pairs
+    attn_flop = 4 * NH * HD * pairs
+    total = proj_flop + attn_flop
+    return {"workload": "config 2 as one MoT pass: 128 text + 4096 image tokens, "
+                        "block-causal attention",
+            "ms_per_layer": round(ms, 5), "ops_ms": ops_ms,
+            "sum_of_ops_ms": round(sum(ops_ms.values()), 5),
+            "flop_per_layer": {"projections": proj_flop, "attention": attn_flop},
+            "value": round(total / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
+            "pct_of_peak": round(100 * total / (ms * 1e-3) / 1e12 / PEAK_BF16, 2),
+            "projection_share": round(sum(v for k_, v in ops_ms.items()
+                                          if k_ in ("q|k|v", "o", "gate|up + swiglu", "down"))
+                                      / sum(ops_ms.values()), 4)}
+
+
 def layer_ops_measure(torch, ops, gen, launches):
     """The ops either side of the projections at config 2's 4224 x 4096
     rows: the layer RMSNorm (u15h_rms_norm), its int8 form that also
@@ -1093,6 +1202,7 @@ def main(argv=None):
         res["masks"] = attention_masks_measure(torch, ops, gen, args.steps)
         res["split_norm_rope"] = norm_rope_measure(torch, ops, gen, args.steps)
         res["layer_ops"] = layer_ops_measure(torch, ops, gen, args.steps)
+        res["layer"] = full_layer_measure(torch, ops, gen, args.steps)
         print(json.dumps(res), flush=True)
         ops.close()
         return
@@ -1175,6 +1285,7 @@ def main(argv=None):
         result["attention"]["masks"] = attention_masks_measure(torch, ops, gen, args.steps)
         result["split_norm_rope"] = norm_rope_measure(torch, ops, gen, args.steps)
         result["layer_ops"] = layer_ops_measure(torch, ops, gen, args.steps)
+        result["layer"] = full_layer_measure(torch, ops, gen, args.steps)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
         side = args.cpu_seconds / 3

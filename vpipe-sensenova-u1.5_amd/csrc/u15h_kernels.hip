@@ -92,12 +92,6 @@ pack_bf16x2(float lo, float hi)
                             __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
 }
 
-__device__ __forceinline__ float
-bf16_round(float f)
-{
-  return __builtin_bit_cast(float, bf16_bits(f) << 16);
-}
-
 // Bit reinterpretation through a by-value copy: __builtin_bit_cast applied
 // directly to an element of an ext_vector_type accumulator reads the
 // vector's first element, not the indexed one.
@@ -250,8 +244,11 @@ store_dequant4(const GemmProblem& P, int m, int n, int a0, int a1, int a2,
 __device__ __forceinline__ float
 swiglu_f(float g, float u)
 {
-  const float gv = bf16_round(g);
-  const float uv = bf16_round(u);
+  // both rounded by one v_cvt_pk_bf16_f32 (RNE, as bf16_round for finite
+  // values): three VALU operations instead of eight
+  const uint32_t p = pack_bf16x2(g, u);
+  const float gv = __uint_as_float(p << 16);
+  const float uv = __uint_as_float(p & 0xffff0000u);
   const float e = __builtin_amdgcn_exp2f(gv * -1.4426950408889634f);
   return (gv * __builtin_amdgcn_rcpf(1.0f + e)) * uv;
 }
