@@ -925,6 +925,32 @@ def full_layer_measure(torch, ops, gen, launches):
 
     ms = timed(layer, launches)
     ops_ms = {name: round(timed(fn, launches), 5) for name, fn in steps.items()}
+
+    # The same layer with the ops either side of the projections fused: both
+    # groups' input norms in one launch, the o residual add with the post
+    # norms in one (u15h_mot_rms_norm), the final add alone (across layers
+    # it fuses with the next layer's input norm the same way).
+    xs = x.clone()
+    d1 = torch.empty(T, HIDDEN, dtype=torch.bfloat16, device=dev)
+    fused = {
+        "rms_norm (both groups)": lambda: ops.mot_rms_norm(xs, Mu, Mg, und["ln1"], gw["ln1"],
+                                                           y=normed),
+        "q|k|v": steps["q|k|v"],
+        "attention prologue": steps["attention prologue"],
+        "attention": steps["attention"],
+        "o": lambda: lin(attn, NQ, (("o", d1),)),
+        "add + rms_norm (both groups)": lambda: ops.mot_rms_norm(
+            xs, Mu, Mg, und["ln2"], gw["ln2"], y=normed, delta=d1),
+        "gate|up + swiglu": steps["gate|up + swiglu"],
+        "down": steps["down"],
+        "add (out)": lambda: ops.add(xs, out),
+    }
+
+    def layer_fused():
+        for fn in fused.values():
+            fn()
+
+    ms_fused = timed(layer_fused, launches)
     hev.close()
     proj_flop = 385875968 * T                   # one expert per row
     pairs = Mu * (Mu + 1) // 2 + Mg * T          # visible (query, key) pairs
@@ -934,6 +960,8 @@ def full_layer_measure(torch, ops, gen, launches):
                         "block-causal attention",
             "ms_per_layer": round(ms, 5), "ops_ms": ops_ms,
             "sum_of_ops_ms": round(sum(ops_ms.values()), 5),
+            "fused_ms_per_layer": round(ms_fused, 5),
+            "fused_value": round(total / (ms_fused * 1e-3) / 1e12, 2),
             "flop_per_layer": {"projections": proj_flop, "attention": attn_flop},
             "value": round(total / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
             "pct_of_peak": round(100 * total / (ms * 1e-3) / 1e12 / PEAK_BF16, 2),
@@ -963,6 +991,8 @@ def layer_ops_measure(torch, ops, gen, launches):
             lambda: (ops.rms_norm(x, w, y), ops.quant_rows_i8(y, q, sx)),
             2 * T * Hd * 2 + Hd * 2 + T * Hd * 2 + T * Hd + T * 4),
         "add": (lambda: ops.add(y, r), 3 * T * Hd * 2),
+        "mot_add_rms_norm": (lambda: ops.mot_rms_norm(y, 128, T - 128, w, w, y=x, delta=r),
+                             4 * T * Hd * 2 + 2 * Hd * 2),
     }
     hev = HipEvents()
     stream = torch.cuda.current_stream()
@@ -984,7 +1014,8 @@ def layer_ops_measure(torch, ops, gen, launches):
     hev.close()
     out["kernels"] = {"rms_norm": "rms_norm_rows_kernel<4, 2, false>",
                       "rms_norm_quant_i8": "rms_norm_rows_kernel<4, 2, true>",
-                      "add": "add_bf16_kernel"}
+                      "add": "add_bf16_kernel",
+                      "mot_add_rms_norm": "rms_norm_rows_kernel<4, 2, false, true>"}
     return out
 
 

@@ -390,6 +390,26 @@ u15h_status u15h_rms_norm_quant_i8(u15h_ctx* ctx, u15h_stream stream,
                                    int rows, int dim, float eps,
                                    u15h_bf16* y, int8_t* q, float* s);
 
+/* The norms of a two-group pass in one launch, with the residual add
+ * before them.  No reference counterpart as one call: U15Backbone::
+ * layer_step_ issues add(x, proj) and then rms_norm(x, post_ln)
+ * (src/u15-backbone.cc:245-249), and, across layers, the last add then
+ * the next layer's input norm (:256, :196), one expert per pass.  For rows
+ * [0, M_und) with w_und and the next M_gen rows with w_gen:
+ *   if delta: x <- bf16(x + delta)                 (the residual stream)
+ *   y <- bf16((x * inv) * w)  as u15h_rms_norm     (when y is not NULL)
+ *   q, s <- the per-token int8 codes of those bf16 values, as
+ *           u15h_rms_norm_quant_i8                 (when q is not NULL)
+ * Bits equal u15h_add, then u15h_rms_norm per group (and
+ * u15h_quant_rows_i8).  x, delta, y [M_und + M_gen][dim] bf16; q int8,
+ * s [rows] f32 (both or neither); at least one of y, q.  y must not be x
+ * when delta is given.  Limits as u15h_rms_norm's. */
+u15h_status u15h_mot_rms_norm(u15h_ctx* ctx, u15h_stream stream,
+                              u15h_bf16* x, const u15h_bf16* delta, int M_und,
+                              int M_gen, int dim, const u15h_bf16* w_und,
+                              const u15h_bf16* w_gen, float eps, u15h_bf16* y,
+                              int8_t* q, float* s);
+
 /* Replaces MetalOps::add(enc, dst, src, n) (src/u15-metal-ops.h:361-363,
  * .cc:974-982; kernel u15_add, src/u15-kernels.metal:496-504), the
  * residual add of layer_step_ (src/u15-backbone.cc:245, 256):

@@ -9,6 +9,9 @@ through the C ABI against the compiled reference.
     normed rows.
   * u15h_add: bit-exact against f32 addition rounded to bf16 (the reference
     kernel u15_add, src/u15-kernels.metal:496-504), any length and offset.
+  * u15h_mot_rms_norm (the residual add and both groups' norms, optionally
+    the int8 codes, in one launch): bit-equal to u15h_add, u15h_rms_norm
+    per group and u15h_quant_rows_i8.
   * The whole layer of U15Backbone::layer_step_ (src/u15-backbone.cc:
     193-257) for one expert's pass, as the reference runs it: rms_norm ->
     q|k|v -> attention prologue -> attention (bidirectional for the gen
@@ -110,6 +113,56 @@ def test_add_bit_exact(ops, n, off):
     assert np.array_equal(got[:off], a0[:off]) and np.array_equal(host_bits(b), b0)
 
 
+@pytest.mark.parametrize("Mu,Mg,dim", [(128, 4096, 4096), (0, 37, 4096), (5, 0, 2056),
+                                      (64, 192, 12288)])
+def test_mot_rms_norm_equals_add_then_norms(ops, Mu, Mg, dim):
+    """u15h_mot_rms_norm (the residual add and both groups' norms in one
+    launch, and the int8 codes) against u15h_add, u15h_rms_norm per group
+    and u15h_quant_rows_i8: every output bit for bit."""
+    T = Mu + Mg
+    g = torch.Generator(device="cuda").manual_seed(T + dim)
+    x = _bf16(g, (T, dim), 2.0)
+    d = _bf16(g, (T, dim), 1.0)
+    wu = _bf16(g, (dim,), 0.2, 1.0)
+    wg = _bf16(g, (dim,), 0.2, 1.0)
+
+    def norms(src, w_und, w_gen):
+        y = torch.empty(T, dim, dtype=torch.bfloat16, device="cuda")
+        if Mu:
+            ops.rms_norm(src[:Mu], w_und, y[:Mu])
+        if Mg:
+            ops.rms_norm(src[Mu:], w_gen, y[Mu:])
+        return y
+
+    x1 = x.clone()
+    ops.add(x1, d)
+    y1 = norms(x1, wu, wg)
+    q1 = torch.empty(T, dim, dtype=torch.int8, device="cuda")
+    s1 = torch.empty(T, dtype=torch.float32, device="cuda")
+    ops.quant_rows_i8(y1, q1, s1)
+
+    x2 = x.clone()
+    y2 = torch.full((T, dim), float("nan"), dtype=torch.bfloat16, device="cuda")
+    q2 = torch.full((T, dim), 99, dtype=torch.int8, device="cuda")
+    s2 = torch.full((T,), -1.0, dtype=torch.float32, device="cuda")
+    ops.mot_rms_norm(x2, Mu, Mg, wu, wg, y=y2, delta=d, q=q2, s=s2)
+    # without the residual: x is only read
+    x3 = x.clone()
+    y3 = torch.empty(T, dim, dtype=torch.bfloat16, device="cuda")
+    ops.mot_rms_norm(x3, Mu, Mg, wu, wg, y=y3)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_bits(x2), host_bits(x1))
+    assert np.array_equal(host_bits(y2), host_bits(y1))
+    assert torch.equal(q2, q1) and torch.equal(s2, s1)
+    assert np.array_equal(host_bits(x3), host_bits(x))
+    assert np.array_equal(host_bits(y3), host_bits(norms(x, wu, wg)))
+    if Mu and Mg:      # each group takes its own weights
+        y4 = torch.empty_like(y3)
+        ops.mot_rms_norm(x.clone(), Mu, Mg, wg, wu, y=y4)
+        torch.cuda.synchronize()
+        assert not np.array_equal(host_bits(y4), host_bits(y3))
+
+
 def test_norm_and_add_refuse_bad_shapes(ops):
     x = torch.zeros(4, 12, dtype=torch.bfloat16, device="cuda")
     w = torch.ones(12, dtype=torch.bfloat16, device="cuda")
@@ -121,6 +174,11 @@ def test_norm_and_add_refuse_bad_shapes(ops):
         ops.rms_norm(x, w, x, eps=-1.0)
     with pytest.raises(ValueError):
         ops.add(x, torch.zeros(3, dtype=torch.bfloat16, device="cuda"))
+    # the residual form keeps the sum in x, so y cannot be x
+    with pytest.raises(u15h.U15hError, match="y must not be x"):
+        ops.mot_rms_norm(x, 4, 0, w, None, y=x, delta=x.clone())
+    with pytest.raises(u15h.U15hError, match="no output"):
+        ops.mot_rms_norm(x, 4, 0, w, None)
 
 
 # ---- one whole decoder layer --------------------------------------------------

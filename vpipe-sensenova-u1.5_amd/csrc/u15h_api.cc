@@ -694,30 +694,43 @@ u15h_swiglu(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* gate,
 }
 
 static u15h_status
-rms_norm_call(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
-              const u15h_bf16* w, int rows, int dim, float eps, u15h_bf16* y,
-              int8_t* q, float* s, const char* what)
+rms_norm_call(u15h_ctx* ctx, u15h_stream stream, u15h_bf16* x,
+              const u15h_bf16* d, int M_und, int M_gen, int dim,
+              const u15h_bf16* w_und, const u15h_bf16* w_gen, float eps,
+              u15h_bf16* y, int8_t* q, float* s, const char* what)
 {
   if (ctx == nullptr) { return U15H_EINVAL; }
-  if (rows < 0 || dim <= 0 || dim % 8 != 0 || dim > 16384) {
-    return fail(ctx, U15H_EINVAL, "%s: rows=%d dim=%d (dim %% 8 == 0, <= 16384)",
-                what, rows, dim);
+  if (M_und < 0 || M_gen < 0 || (long long)M_und + M_gen > (1 << 30) ||
+      dim <= 0 || dim % 8 != 0 || dim > 16384) {
+    return fail(ctx, U15H_EINVAL, "%s: rows=%d+%d dim=%d (dim %% 8 == 0, <= 16384)",
+                what, M_und, M_gen, dim);
   }
   if (!(eps >= 0.0f)) {
     return fail(ctx, U15H_EINVAL, "%s: eps must be >= 0", what);
   }
+  const int rows = M_und + M_gen;
   if (rows == 0) { ctx->err.clear(); return U15H_OK; }
   const bool quant = q != nullptr || s != nullptr;
-  if (x == nullptr || w == nullptr || !aligned16(x) || !aligned16(w) ||
-      (!quant && y == nullptr) || (y != nullptr && !aligned16(y)) ||
+  if (x == nullptr || !aligned16(x) ||
+      (M_und > 0 && (w_und == nullptr || !aligned16(w_und))) ||
+      (M_gen > 0 && (w_gen == nullptr || !aligned16(w_gen))) ||
+      (d != nullptr && !aligned16(d)) || (y != nullptr && !aligned16(y)) ||
       (quant && (q == nullptr || s == nullptr || !aligned16(q) || !aligned16(s)))) {
     return fail(ctx, U15H_EINVAL, "%s: null or misaligned operand", what);
+  }
+  if (y == nullptr && !quant) {
+    return fail(ctx, U15H_EINVAL, "%s: no output (y or the int8 codes)", what);
+  }
+  if (d != nullptr && y == x) {
+    return fail(ctx, U15H_EINVAL, "%s: y must not be x when a residual is added "
+                "(x keeps the sum)", what);
   }
   u15h_status st = bind_device(ctx);
   if (st != U15H_OK) { return st; }
   return launched(ctx,
-                  u15h::launch_rms_norm(x, w, rows, dim, eps, y, q, s,
-                                        as_stream(stream)),
+                  u15h::launch_rms_norm(x, d, M_und > 0 ? w_und : w_gen,
+                                        M_gen > 0 ? w_gen : w_und, M_und, rows,
+                                        dim, eps, y, q, s, as_stream(stream)),
                   what);
 }
 
@@ -728,8 +741,9 @@ u15h_rms_norm(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
   if (ctx != nullptr && y == nullptr && rows > 0) {
     return fail(ctx, U15H_EINVAL, "rms_norm: null output");
   }
-  return rms_norm_call(ctx, stream, x, w, rows, dim, eps, y, nullptr, nullptr,
-                       "rms_norm");
+  // x is only read without a residual
+  return rms_norm_call(ctx, stream, const_cast<u15h_bf16*>(x), nullptr, rows, 0,
+                       dim, w, w, eps, y, nullptr, nullptr, "rms_norm");
 }
 
 u15h_status
@@ -740,8 +754,21 @@ u15h_rms_norm_quant_i8(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* x,
   if (ctx != nullptr && rows > 0 && (q == nullptr || s == nullptr)) {
     return fail(ctx, U15H_EINVAL, "rms_norm_quant_i8: null codes or scales");
   }
-  return rms_norm_call(ctx, stream, x, w, rows, dim, eps, y, q, s,
-                       "rms_norm_quant_i8");
+  return rms_norm_call(ctx, stream, const_cast<u15h_bf16*>(x), nullptr, rows, 0,
+                       dim, w, w, eps, y, q, s, "rms_norm_quant_i8");
+}
+
+u15h_status
+u15h_mot_rms_norm(u15h_ctx* ctx, u15h_stream stream, u15h_bf16* x,
+                  const u15h_bf16* delta, int M_und, int M_gen, int dim,
+                  const u15h_bf16* w_und, const u15h_bf16* w_gen, float eps,
+                  u15h_bf16* y, int8_t* q, float* s)
+{
+  if (ctx != nullptr && (q == nullptr) != (s == nullptr)) {
+    return fail(ctx, U15H_EINVAL, "mot_rms_norm: codes and scales go together");
+  }
+  return rms_norm_call(ctx, stream, x, delta, M_und, M_gen, dim, w_und, w_gen,
+                       eps, y, q, s, "mot_rms_norm");
 }
 
 u15h_status

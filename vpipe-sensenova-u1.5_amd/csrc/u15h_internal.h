@@ -152,13 +152,15 @@ hipError_t launch_quant_rows_i8(const uint16_t* x, int rows, int K,
                                 int8_t* q, float* sc, hipStream_t s,
                                 hipEvent_t start = nullptr,
                                 hipEvent_t end = nullptr);
-// Whole-row RMSNorm with gain, dim <= 16384, dim % 8 == 0, x, w, y
-// 16-byte aligned: y = bf16((x * inv) * w).  With q not null it also
-// quantises the row's bf16 results to int8 codes q and scale sc (y then
-// optional), equal to launch_quant_rows_i8 on y.
-hipError_t launch_rms_norm(const uint16_t* x, const uint16_t* w, int rows,
-                           int dim, float eps, uint16_t* y, int8_t* q,
-                           float* sc, hipStream_t s);
+// Whole-row RMSNorm with gain, dim <= 16384, dim % 8 == 0, operands
+// 16-byte aligned: with d not null x = bf16(x + d) first (stored back);
+// y = bf16((x * inv) * w), w = w_und for rows below m_und, else w_gen.
+// With q not null it also quantises the row's bf16 results to int8 codes q
+// and scale sc (y then optional), equal to launch_quant_rows_i8 on y.
+hipError_t launch_rms_norm(uint16_t* x, const uint16_t* d, const uint16_t* w_und,
+                           const uint16_t* w_gen, int m_und, int rows, int dim,
+                           float eps, uint16_t* y, int8_t* q, float* sc,
+                           hipStream_t s);
 // dst[i] = bf16(f32(dst[i]) + f32(src[i])), any n and alignment.
 hipError_t launch_add_bf16(uint16_t* dst, const uint16_t* src, int64_t n,
                            hipStream_t s);

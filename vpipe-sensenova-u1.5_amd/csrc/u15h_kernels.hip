@@ -1426,22 +1426,27 @@ quant_rows_i8_waves_kernel(const uint16_t* __restrict__ x, int rows, int K,
   }
 }
 
-// ---- RMSNorm with gain, and its int8 form -----------------------------------
+// ---- RMSNorm with gain, its int8 form, and the residual add before it --------
 // Rows normalised by whole waves, the quantiser's layout: WPR waves per row
 // (one row per workgroup), each lane holding CPL 16-byte chunks of its row
 // in registers (dim <= 512 * WPR * CPL); chunk i of wave p, lane l is
 // chunk i * 64 * WPR + p * 64 + l.  Loads past the row read zeros through
 // the buffer resource's range and stores past it are dropped.
+//   ADD:  x = bf16(x + d) first, stored back to x (the residual stream),
+//         and the row normalised from those bf16 values;
 //   y = bf16((x * inv) * w),  inv = rsqrt(sum(x^2) / dim + eps),
 // the sum in f32 (lane partials, then the wave and the row by xor shuffles
-// and LDS).  QUANT: the row's bf16 results, as they would be read back,
-// give its int8 scale and codes by the quantiser's own steps (absmax8,
-// quant8), so (q, sc) equal quant_rows_i8 applied to y bit for bit; y
-// itself is stored only when `y` is not null.  y may be x: every store of
-// a row depends on the row's sum, so all of its loads come first.
-template <int WPR, int CPL, bool QUANT>
+// and LDS); rows below m_und take w_und, the rest w_gen.  QUANT: the row's
+// bf16 results, as they would be read back, give its int8 scale and codes
+// by the quantiser's own steps (absmax8, quant8), so (q, sc) equal
+// quant_rows_i8 applied to y bit for bit; y itself is stored only when `y`
+// is not null.  y may be x: every store of a row depends on the row's sum,
+// so all of its loads come first.
+template <int WPR, int CPL, bool QUANT, bool ADD>
 __global__ __launch_bounds__(64 * WPR) void
-rms_norm_rows_kernel(const uint16_t* x, const uint16_t* __restrict__ w, int dim,
+rms_norm_rows_kernel(uint16_t* x, const uint16_t* __restrict__ d,
+                     const uint16_t* __restrict__ w_und,
+                     const uint16_t* __restrict__ w_gen, int m_und, int dim,
                      float eps, uint16_t* y, int8_t* __restrict__ q,
                      float* __restrict__ sc)
 {
@@ -1449,13 +1454,40 @@ rms_norm_rows_kernel(const uint16_t* x, const uint16_t* __restrict__ w, int dim,
   const int lane = threadIdx.x & 63;
   const int r = blockIdx.x;
   const __amdgpu_buffer_rsrc_t src = make_rsrc(x + (size_t)r * dim, dim * 2);
-  const __amdgpu_buffer_rsrc_t wsrc = make_rsrc(w, dim * 2);
+  const __amdgpu_buffer_rsrc_t wsrc = make_rsrc(r < m_und ? w_und : w_gen, dim * 2);
   u32x4_t v[CPL], g[CPL];
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
     const int c = i * 64 * WPR + part * 64 + lane;
     v[i] = __builtin_amdgcn_raw_buffer_load_b128(src, c * 16, 0, 0);
     g[i] = __builtin_amdgcn_raw_buffer_load_b128(wsrc, c * 16, 0, 0);
+  }
+  if constexpr (ADD) {
+    const __amdgpu_buffer_rsrc_t dsrc = make_rsrc(d + (size_t)r * dim, dim * 2);
+    u32x4_t dv[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = i * 64 * WPR + part * 64 + lane;
+      dv[i] = __builtin_amdgcn_raw_buffer_load_b128(dsrc, c * 16, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const uint32_t xv[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+      const uint32_t ev[4] = {dv[i].x, dv[i].y, dv[i].z, dv[i].w};
+      uint32_t o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        o[e] = pack_bf16x2(__uint_as_float(xv[e] << 16) + __uint_as_float(ev[e] << 16),
+                           __uint_as_float(xv[e] & 0xffff0000u) +
+                               __uint_as_float(ev[e] & 0xffff0000u));
+      }
+      v[i] = (u32x4_t){o[0], o[1], o[2], o[3]};
+    }
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = i * 64 * WPR + part * 64 + lane;
+      __builtin_amdgcn_raw_buffer_store_b128(v[i], src, c * 16, 0, 0);
+    }
   }
   float ss = 0.0f;
 #pragma unroll
@@ -3336,20 +3368,24 @@ launch_quant_rows_i8(const uint16_t* x, int rows, int K, int8_t* q,
 }
 
 hipError_t
-launch_rms_norm(const uint16_t* x, const uint16_t* w, int rows, int dim, float eps,
+launch_rms_norm(uint16_t* x, const uint16_t* d, const uint16_t* w_und,
+                const uint16_t* w_gen, int m_und, int rows, int dim, float eps,
                 uint16_t* y, int8_t* q, float* sc, hipStream_t s)
 {
   if (rows <= 0) { return hipSuccess; }
-  const bool quant = q != nullptr;
+  const int sel = (q != nullptr ? 1 : 0) | (d != nullptr ? 2 : 0);
   // one row per workgroup: four waves up to 8192 columns, eight above
+#define U15H_NORM1(WPR, CPL, QU, AD)                                          \
+  hipLaunchKernelGGL((rms_norm_rows_kernel<WPR, CPL, QU, AD>), dim3(rows),    \
+                     dim3(64 * WPR), 0, s, x, d, w_und, w_gen, m_und, dim,    \
+                     eps, y, q, sc)
 #define U15H_NORM(WPR, CPL)                                                   \
   do {                                                                        \
-    if (quant) {                                                              \
-      hipLaunchKernelGGL((rms_norm_rows_kernel<WPR, CPL, true>), dim3(rows),  \
-                         dim3(64 * WPR), 0, s, x, w, dim, eps, y, q, sc);     \
-    } else {                                                                  \
-      hipLaunchKernelGGL((rms_norm_rows_kernel<WPR, CPL, false>), dim3(rows), \
-                         dim3(64 * WPR), 0, s, x, w, dim, eps, y, q, sc);     \
+    switch (sel) {                                                            \
+      case 0: U15H_NORM1(WPR, CPL, false, false); break;                      \
+      case 1: U15H_NORM1(WPR, CPL, true, false); break;                       \
+      case 2: U15H_NORM1(WPR, CPL, false, true); break;                       \
+      default: U15H_NORM1(WPR, CPL, true, true); break;                       \
     }                                                                         \
   } while (0)
   if (dim <= 2048) {
@@ -3362,6 +3398,7 @@ launch_rms_norm(const uint16_t* x, const uint16_t* w, int rows, int dim, float e
     U15H_NORM(8, 4);
   }
 #undef U15H_NORM
+#undef U15H_NORM1
   return hipGetLastError();
 }
 
@@ -3662,14 +3699,22 @@ kernels_loadable()
       reinterpret_cast<const void*>(&split_norm_rope_vec_kernel<true, false>),
       reinterpret_cast<const void*>(&split_norm_rope_vec_kernel<false, true>),
       reinterpret_cast<const void*>(&attention_prologue_kernel<1>),
-      reinterpret_cast<const void*>(&rms_norm_rows_kernel<4, 1, false>),
-      reinterpret_cast<const void*>(&rms_norm_rows_kernel<4, 2, false>),
-      reinterpret_cast<const void*>(&rms_norm_rows_kernel<4, 4, false>),
-      reinterpret_cast<const void*>(&rms_norm_rows_kernel<8, 4, false>),
-      reinterpret_cast<const void*>(&rms_norm_rows_kernel<4, 1, true>),
-      reinterpret_cast<const void*>(&rms_norm_rows_kernel<4, 2, true>),
-      reinterpret_cast<const void*>(&rms_norm_rows_kernel<4, 4, true>),
-      reinterpret_cast<const void*>(&rms_norm_rows_kernel<8, 4, true>),
+      reinterpret_cast<const void*>(&rms_norm_rows_kernel<4, 1, false, false>),
+      reinterpret_cast<const void*>(&rms_norm_rows_kernel<4, 1, true, false>),
+      reinterpret_cast<const void*>(&rms_norm_rows_kernel<4, 1, false, true>),
+      reinterpret_cast<const void*>(&rms_norm_rows_kernel<4, 1, true, true>),
+      reinterpret_cast<const void*>(&rms_norm_rows_kernel<4, 2, false, false>),
+      reinterpret_cast<const void*>(&rms_norm_rows_kernel<4, 2, true, false>),
+      reinterpret_cast<const void*>(&rms_norm_rows_kernel<4, 2, false, true>),
+      reinterpret_cast<const void*>(&rms_norm_rows_kernel<4, 2, true, true>),
+      reinterpret_cast<const void*>(&rms_norm_rows_kernel<4, 4, false, false>),
+      reinterpret_cast<const void*>(&rms_norm_rows_kernel<4, 4, true, false>),
+      reinterpret_cast<const void*>(&rms_norm_rows_kernel<4, 4, false, true>),
+      reinterpret_cast<const void*>(&rms_norm_rows_kernel<4, 4, true, true>),
+      reinterpret_cast<const void*>(&rms_norm_rows_kernel<8, 4, false, false>),
+      reinterpret_cast<const void*>(&rms_norm_rows_kernel<8, 4, true, false>),
+      reinterpret_cast<const void*>(&rms_norm_rows_kernel<8, 4, false, true>),
+      reinterpret_cast<const void*>(&rms_norm_rows_kernel<8, 4, true, true>),
       reinterpret_cast<const void*>(&add_bf16_kernel),
       reinterpret_cast<const void*>(&attention_prologue_kernel<2>),
       reinterpret_cast<const void*>(&attention_prologue_kernel<4>),

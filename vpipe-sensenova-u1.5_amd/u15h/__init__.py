@@ -138,6 +138,8 @@ def load_library() -> ctypes.CDLL:
         "u15h_rms_norm_quant_i8": (i, [vp, vp, vp, vp, i, i, ctypes.c_float,
                                        vp, vp, vp]),
         "u15h_add": (i, [vp, vp, vp, vp, i64]),
+        "u15h_mot_rms_norm": (i, [vp, vp, vp, vp, i, i, i, vp, vp, ctypes.c_float,
+                                  vp, vp, vp]),
         "u15h_build_rope_tables": (i, [vp, vp, vp, i, i, i, i,
                                        ctypes.c_double, ctypes.c_double, vp,
                                        vp]),
@@ -843,6 +845,31 @@ class Ops:
                                               _ptr(w), rows, dim, eps, _ptr(y),
                                               _ptr(q), _ptr(s))
         self._check(st, "u15h_rms_norm_quant_i8")
+
+    def mot_rms_norm(self, x, M_und, M_gen, w_und, w_gen, y=None, delta=None,
+                     q=None, s=None, eps=1e-6, stream=None):
+        """u15h_mot_rms_norm: with `delta`, x += delta first (in place);
+        then y = the norm of x's rows (w_und for the first M_und, w_gen for
+        the rest) and/or its per-token int8 codes q and scales s."""
+        rows = M_und + M_gen
+        if x.dim() != 2 or x.shape[0] != rows:
+            raise ValueError(f"x must be [{rows}][dim]")
+        dim = x.shape[1]
+        _need(x, torch.bfloat16, (rows, dim), "x")
+        if M_und:
+            _need(w_und, torch.bfloat16, (dim,), "w_und")
+        if M_gen:
+            _need(w_gen, torch.bfloat16, (dim,), "w_gen")
+        for name, t, dt, shape in (("y", y, torch.bfloat16, (rows, dim)),
+                                   ("delta", delta, torch.bfloat16, (rows, dim)),
+                                   ("q", q, torch.int8, (rows, dim)),
+                                   ("s", s, torch.float32, (rows,))):
+            if t is not None:
+                _need(t, dt, shape, name)
+        st = self._lib.u15h_mot_rms_norm(self._ctx, _stream(stream), _ptr(x), _ptr(delta),
+                                         M_und, M_gen, dim, _ptr(w_und), _ptr(w_gen),
+                                         eps, _ptr(y), _ptr(q), _ptr(s))
+        self._check(st, "u15h_mot_rms_norm")
 
     def add(self, dst, src, stream=None):
         """MetalOps::add: dst += src elementwise (bf16, f32 add)."""
