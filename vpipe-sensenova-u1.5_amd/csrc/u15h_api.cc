@@ -21,6 +21,7 @@
 struct u15h_ctx {
   int device = 0;
   int num_cu = 256;
+  int gemm_cus = 256;        // CUs the tiled GEMM's rounds are planned for
   bool split_on = true;      // env U15H_SPLIT=0 turns the split-K tail off
   // env U15H_SKINNY=0 keeps batches of <= 128-row problems on the tiled GEMM
   bool skinny_on = true;
@@ -190,7 +191,7 @@ plan_split(u15h_ctx* ctx, GemmBatch& b, bool noalloc = false)
   b.split_begin = b.total_tiles;
   b.ws = nullptr;
   const int T = b.total_tiles;
-  const int C = ctx->num_cu;
+  const int C = ctx->gemm_cus;
   const int rem = T % C;
   if (!ctx->split_on || T <= 0 || rem == 0) { return U15H_OK; }
   const int nk = (b.kbytes + u15h::kKB - 1) / u15h::kKB;
@@ -523,7 +524,12 @@ u15h_create(int device, u15h_ctx** out)
   ctx->prologue_rpt = env_int("U15H_PROLOGUE_RPT", 2);
   ctx->q_min_m = std::max(0, std::min(u15h::kSkinnyMaxRows + 1, env_int("U15H_Q_MIN_M", 96)));
   ctx->gemm.waves = env_int("U15H_WAVES", 8) == 4 ? 4 : 8;
-  ctx->gemm.cus = env_int("U15H_PERSIST", 1) != 0 ? ctx->num_cu : 0;
+  // env U15H_GEMM_CUS caps the tiled GEMM's persistent grid (a multiple of
+  // 8, so each XCD keeps the same share), leaving CUs to work on another
+  // stream; the split-K planner then fills rounds of that many tiles
+  ctx->gemm_cus = std::max(8, std::min(ctx->num_cu,
+                                       env_int("U15H_GEMM_CUS", ctx->num_cu) / 8 * 8));
+  ctx->gemm.cus = env_int("U15H_PERSIST", 1) != 0 ? ctx->gemm_cus : 0;
   ctx->gemm.mfma16 = std::max(-1, std::min(1, env_int("U15H_MFMA16", 1)));
   ctx->i8_min_m = std::max(1, env_int("U15H_I8_MIN_M", 1024));
   *out = ctx;
