@@ -951,6 +951,53 @@ def full_layer_measure(torch, ops, gen, launches):
             fn()
 
     ms_fused = timed(layer_fused, launches)
+
+    # The int8 tier through the same layer: the norms emit the per-token
+    # int8 codes of their bf16 results directly (u15h_mot_rms_norm), the
+    # attention output and the SwiGLU output go through the quantiser, and
+    # every projection runs the int8 GEMM with the fused dequant.
+    Q = {}
+    for e in ("und", "gen"):
+        Q[e] = {}
+        for n in ("q", "k", "v", "o", "gate", "up", "down"):
+            wt = W[e][n]
+            wq = torch.empty(wt.shape, dtype=torch.int8, device=dev)
+            sw = torch.empty(wt.shape[0], dtype=torch.float32, device=dev)
+            ops.quant_rows_i8(wt, wq, sw)
+            Q[e][n] = (wq, sw)
+    xq = torch.empty(T, INTER, dtype=torch.int8, device=dev)
+    sx = torch.empty(T, dtype=torch.float32, device=dev)
+    xq4 = xq[:, :HIDDEN].contiguous()
+    gate = torch.empty(T, INTER, dtype=torch.bfloat16, device=dev)
+    up = torch.empty(T, INTER, dtype=torch.bfloat16, device=dev)
+
+    def lin8(src_q, K, pairs):
+        ops.mot_gemm_i8(src_q, sx, Mu, Mg, K, [
+            dict(wq_und=Q["und"][n][0], sw_und=Q["und"][n][1], wq_gen=Q["gen"][n][0],
+                 sw_gen=Q["gen"][n][1], y=y) for n, y in pairs])
+
+    int8_steps = {
+        "rms_norm -> int8 (both groups)": lambda: ops.mot_rms_norm(
+            xs, Mu, Mg, und["ln1"], gw["ln1"], q=xq4, s=sx),
+        "q|k|v": lambda: lin8(xq4, HIDDEN, (("q", q), ("k", k), ("v", v))),
+        "attention prologue": steps["attention prologue"],
+        "attention": steps["attention"],
+        "quantise attn": lambda: ops.quant_rows_i8(attn, xq4, sx),
+        "o": lambda: lin8(xq4, NQ, (("o", d1),)),
+        "add + rms_norm -> int8 (both groups)": lambda: ops.mot_rms_norm(
+            xs, Mu, Mg, und["ln2"], gw["ln2"], delta=d1, q=xq4, s=sx),
+        "gate|up": lambda: lin8(xq4, HIDDEN, (("gate", gate), ("up", up))),
+        "swiglu -> int8": lambda: ops.swiglu_quant_i8(gate, up, xq, sx),
+        "down": lambda: lin8(xq, INTER, (("down", out),)),
+        "add (out)": fused["add (out)"],
+    }
+
+    def layer_i8():
+        for fn in int8_steps.values():
+            fn()
+
+    ms_i8 = timed(layer_i8, launches)
+    i8_ops_ms = {name: round(timed(fn, launches), 5) for name, fn in int8_steps.items()}
     hev.close()
     proj_flop = 385875968 * T                   # one expert per row
     pairs = Mu * (Mu + 1) // 2 + Mg * T          # visible (query, key) pairs
@@ -962,6 +1009,11 @@ def full_layer_measure(torch, ops, gen, launches):
             "sum_of_ops_ms": round(sum(ops_ms.values()), 5),
             "fused_ms_per_layer": round(ms_fused, 5),
             "fused_value": round(total / (ms_fused * 1e-3) / 1e12, 2),
+            "int8": {"ms_per_layer": round(ms_i8, 5), "ops_ms": i8_ops_ms,
+                     "speedup_over_bf16_fused": round(ms_fused / ms_i8, 3),
+                     "note": "projections in the int8 tier (per-token x per-channel "
+                             "int8, int32 accumulate, fused dequant); attention and "
+                             "the norms in bf16"},
             "flop_per_layer": {"projections": proj_flop, "attention": attn_flop},
             "value": round(total / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
             "pct_of_peak": round(100 * total / (ms * 1e-3) / 1e12 / PEAK_BF16, 2),
@@ -971,11 +1023,14 @@ def full_layer_measure(torch, ops, gen, launches):
 
 
 def layer_ops_measure(torch, ops, gen, launches):
-    """The ops either side of the projections at config 2's 4224 x 4096
-    rows: the layer RMSNorm (u15h_rms_norm), its int8 form that also
-    quantises the normed rows per token (u15h_rms_norm_quant_i8, against
-    the norm and the quantiser as two launches), and the residual add
-    (u15h_add).  All HBM-bound; bytes are each launch's reads and writes."""
+    """The ops either side of the projections at config 2's 4224 rows: the
+    layer RMSNorm (u15h_rms_norm), its int8 form that also quantises the
+    normed rows per token (u15h_rms_norm_quant_i8, against the norm and the
+    quantiser as two launches), the residual add (u15h_add), the residual
+    with both groups' norms (u15h_mot_rms_norm), and SwiGLU with the int8
+    codes of its output at 12288 columns (u15h_swiglu_quant_i8, against
+    u15h_swiglu and the quantiser).  All HBM-bound; bytes are each launch's
+    reads and writes."""
     T, Hd = 4224, HIDDEN
     x = torch.randn(T, Hd, generator=gen, device="cuda").to(torch.bfloat16)
     w = (1 + 0.1 * torch.randn(Hd, generator=gen, device="cuda")).to(torch.bfloat16)
@@ -983,6 +1038,10 @@ def layer_ops_measure(torch, ops, gen, launches):
     r = torch.randn(T, Hd, generator=gen, device="cuda").to(torch.bfloat16)
     q = torch.empty(T, Hd, dtype=torch.int8, device="cuda")
     sx = torch.empty(T, dtype=torch.float32, device="cuda")
+    g_ = torch.randn(T, INTER, generator=gen, device="cuda").to(torch.bfloat16)
+    u_ = torch.randn(T, INTER, generator=gen, device="cuda").to(torch.bfloat16)
+    h_ = torch.empty_like(g_)
+    q_i = torch.empty(T, INTER, dtype=torch.int8, device="cuda")
     calls = {
         "rms_norm": (lambda: ops.rms_norm(x, w, y), 2 * T * Hd * 2 + Hd * 2),
         "rms_norm_quant_i8": (lambda: ops.rms_norm_quant_i8(x, w, q, sx),
@@ -993,6 +1052,11 @@ def layer_ops_measure(torch, ops, gen, launches):
         "add": (lambda: ops.add(y, r), 3 * T * Hd * 2),
         "mot_add_rms_norm": (lambda: ops.mot_rms_norm(y, 128, T - 128, w, w, y=x, delta=r),
                              4 * T * Hd * 2 + 2 * Hd * 2),
+        "swiglu_quant_i8": (lambda: ops.swiglu_quant_i8(g_, u_, q_i, sx),
+                            2 * T * INTER * 2 + T * INTER + T * 4),
+        "swiglu_then_quant_rows_i8": (
+            lambda: (ops.swiglu(g_, u_, h_), ops.quant_rows_i8(h_, q_i, sx)),
+            3 * T * INTER * 2 + T * INTER * 2 + T * INTER + T * 4),
     }
     hev = HipEvents()
     stream = torch.cuda.current_stream()
@@ -1015,7 +1079,8 @@ def layer_ops_measure(torch, ops, gen, launches):
     out["kernels"] = {"rms_norm": "rms_norm_rows_kernel<4, 2, false>",
                       "rms_norm_quant_i8": "rms_norm_rows_kernel<4, 2, true>",
                       "add": "add_bf16_kernel",
-                      "mot_add_rms_norm": "rms_norm_rows_kernel<4, 2, false, true>"}
+                      "mot_add_rms_norm": "rms_norm_rows_kernel<4, 2, false, true>",
+                      "swiglu_quant_i8": "swiglu_quant_rows_kernel<8, 3>"}
     return out
 
 

@@ -428,6 +428,17 @@ u15h_status u15h_swiglu(u15h_ctx* ctx, u15h_stream stream,
                         const u15h_bf16* gate, const u15h_bf16* up,
                         u15h_bf16* out, int64_t n);
 
+/* The int8 tier's input to the down projection in one pass: h =
+ * swiglu(gate, up) as u15h_swiglu, then its per-token int8 codes q
+ * [rows][inter] and scales s [rows] as u15h_quant_rows_i8 on h (bit for
+ * bit).  h [rows][inter] is written only when not NULL.  No reference
+ * counterpart: it saves writing h and reading it back.  Limits: inter %
+ * 8 == 0, inter <= 16384, 16-byte aligned operands. */
+u15h_status u15h_swiglu_quant_i8(u15h_ctx* ctx, u15h_stream stream,
+                                 const u15h_bf16* gate, const u15h_bf16* up,
+                                 int rows, int inter, u15h_bf16* h, int8_t* q,
+                                 float* s);
+
 /* Replaces MetalOps::swiglu_fused(enc, x, w_fused, y, M, K, inter)
  * (src/u15-metal-ops.h:121-135, src/u15-metal-ops.cc:470-491) with the
  * reference's weight layout: w_fused[2*inter][K] ROW-INTERLEAVED, row 2i =

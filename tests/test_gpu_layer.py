@@ -9,6 +9,8 @@ through the C ABI against the compiled reference.
     normed rows.
   * u15h_add: bit-exact against f32 addition rounded to bf16 (the reference
     kernel u15_add, src/u15-kernels.metal:496-504), any length and offset.
+  * u15h_swiglu_quant_i8: h and its int8 codes and scales bit-equal to
+    u15h_swiglu then u15h_quant_rows_i8.
   * u15h_mot_rms_norm (the residual add and both groups' norms, optionally
     the int8 codes, in one launch): bit-equal to u15h_add, u15h_rms_norm
     per group and u15h_quant_rows_i8.
@@ -161,6 +163,36 @@ def test_mot_rms_norm_equals_add_then_norms(ops, Mu, Mg, dim):
         ops.mot_rms_norm(x.clone(), Mu, Mg, wg, wu, y=y4)
         torch.cuda.synchronize()
         assert not np.array_equal(host_bits(y4), host_bits(y3))
+
+
+@pytest.mark.parametrize("rows,inter", [(4224, 12288), (33, 8), (7, 2056), (5, 16384),
+                                        (3, 4104)])
+def test_swiglu_quant_equals_swiglu_then_quantiser(ops, rows, inter):
+    """u15h_swiglu_quant_i8 against u15h_swiglu then u15h_quant_rows_i8, bit
+    for bit (h, codes and scales), and against the oracle's quantiser."""
+    g = torch.Generator(device="cuda").manual_seed(rows + inter)
+    gate = _bf16(g, (rows, inter), 2.0)
+    up = _bf16(g, (rows, inter), 1.5)
+    gate[0].zero_()                            # swiglu(0, u) = 0: scale 0
+    h1 = torch.empty(rows, inter, dtype=torch.bfloat16, device="cuda")
+    ops.swiglu(gate, up, h1)
+    q1 = torch.empty(rows, inter, dtype=torch.int8, device="cuda")
+    s1 = torch.empty(rows, dtype=torch.float32, device="cuda")
+    ops.quant_rows_i8(h1, q1, s1)
+    h2 = torch.full((rows, inter), float("nan"), dtype=torch.bfloat16, device="cuda")
+    q2 = torch.full((rows, inter), 99, dtype=torch.int8, device="cuda")
+    s2 = torch.full((rows,), -1.0, dtype=torch.float32, device="cuda")
+    ops.swiglu_quant_i8(gate, up, q2, s2, h=h2)
+    q3 = torch.full((rows, inter), 99, dtype=torch.int8, device="cuda")
+    s3 = torch.full((rows,), -1.0, dtype=torch.float32, device="cuda")
+    ops.swiglu_quant_i8(gate, up, q3, s3)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_bits(h2), host_bits(h1))
+    for q, s in ((q2, s2), (q3, s3)):
+        assert torch.equal(q, q1) and torch.equal(s, s1)
+    qo, so = oracle.quant_rows_i8(host_bits(h1))
+    assert np.array_equal(q2.cpu().numpy(), qo) and np.array_equal(s2.cpu().numpy(), so)
+    assert s2[0].item() == 0.0
 
 
 def test_norm_and_add_refuse_bad_shapes(ops):

@@ -793,6 +793,30 @@ u15h_add(u15h_ctx* ctx, u15h_stream stream, u15h_bf16* dst,
 }
 
 u15h_status
+u15h_swiglu_quant_i8(u15h_ctx* ctx, u15h_stream stream, const u15h_bf16* gate,
+                     const u15h_bf16* up, int rows, int inter, u15h_bf16* h,
+                     int8_t* q, float* s)
+{
+  if (ctx == nullptr) { return U15H_EINVAL; }
+  if (rows < 0 || inter <= 0 || inter % 8 != 0 || inter > 16384) {
+    return fail(ctx, U15H_EINVAL, "swiglu_quant_i8: rows=%d inter=%d (inter %% 8 "
+                "== 0, <= 16384)", rows, inter);
+  }
+  if (rows == 0) { ctx->err.clear(); return U15H_OK; }
+  if (gate == nullptr || up == nullptr || q == nullptr || s == nullptr ||
+      !aligned16(gate) || !aligned16(up) || !aligned16(q) || !aligned16(s) ||
+      (h != nullptr && !aligned16(h))) {
+    return fail(ctx, U15H_EINVAL, "swiglu_quant_i8: null or misaligned operand");
+  }
+  u15h_status st = bind_device(ctx);
+  if (st != U15H_OK) { return st; }
+  return launched(ctx,
+                  u15h::launch_swiglu_quant(gate, up, rows, inter, h, q, s,
+                                            as_stream(stream)),
+                  "swiglu_quant_i8");
+}
+
+u15h_status
 u15h_mot_gate_up_swiglu(u15h_ctx* ctx, u15h_stream stream,
                         const u15h_bf16* x, int M_und, int M_gen, int K,
                         const u15h_bf16* wg_und, const u15h_bf16* wu_und,

@@ -161,6 +161,12 @@ hipError_t launch_rms_norm(uint16_t* x, const uint16_t* d, const uint16_t* w_und
                            const uint16_t* w_gen, int m_und, int rows, int dim,
                            float eps, uint16_t* y, int8_t* q, float* sc,
                            hipStream_t s);
+// h = swiglu(gate, up) rows [rows][dim] and their per-token int8 codes q,
+// scale sc (equal to launch_swiglu then launch_quant_rows_i8); h optional.
+// dim % 8 == 0, dim <= 16384, operands 16-byte aligned.
+hipError_t launch_swiglu_quant(const uint16_t* gate, const uint16_t* up, int rows,
+                               int dim, uint16_t* h, int8_t* q, float* sc,
+                               hipStream_t s);
 // dst[i] = bf16(f32(dst[i]) + f32(src[i])), any n and alignment.
 hipError_t launch_add_bf16(uint16_t* dst, const uint16_t* src, int64_t n,
                            hipStream_t s);

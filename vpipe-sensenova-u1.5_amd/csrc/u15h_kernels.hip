@@ -1566,6 +1566,81 @@ rms_norm_rows_kernel(uint16_t* x, const uint16_t* __restrict__ d,
   }
 }
 
+// ---- SwiGLU with the int8 tier's per-token quantisation ---------------------
+// The down projection's int8 input in one pass: h = swiglu(gate, up) per
+// element (swiglu_f, the elementwise kernel's arithmetic), then the row's
+// absmax, scale and codes by the quantiser's own steps, so (q, sc) equal
+// quant_rows_i8 on swiglu's output bit for bit; h is stored only when not
+// null.  The rows' layout is rms_norm_rows_kernel's (dim <= 512 * WPR * CPL).
+template <int WPR, int CPL>
+__global__ __launch_bounds__(64 * WPR) void
+swiglu_quant_rows_kernel(const uint16_t* __restrict__ gate,
+                         const uint16_t* __restrict__ up, int dim,
+                         uint16_t* __restrict__ h, int8_t* __restrict__ q,
+                         float* __restrict__ sc)
+{
+  const int part = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x;
+  const __amdgpu_buffer_rsrc_t gs = make_rsrc(gate + (size_t)r * dim, dim * 2);
+  const __amdgpu_buffer_rsrc_t us = make_rsrc(up + (size_t)r * dim, dim * 2);
+  u32x4_t gv[CPL], uv[CPL];
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = i * 64 * WPR + part * 64 + lane;
+    gv[i] = __builtin_amdgcn_raw_buffer_load_b128(gs, c * 16, 0, 0);
+    uv[i] = __builtin_amdgcn_raw_buffer_load_b128(us, c * 16, 0, 0);
+  }
+  uint4 out[CPL];
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const uint32_t ga[4] = {gv[i].x, gv[i].y, gv[i].z, gv[i].w};
+    const uint32_t ua[4] = {uv[i].x, uv[i].y, uv[i].z, uv[i].w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o[e] = pack_bf16x2(swiglu_f(bf16_to_f32(ga[e] & 0xffffu), bf16_to_f32(ua[e] & 0xffffu)),
+                         swiglu_f(bf16_to_f32(ga[e] >> 16), bf16_to_f32(ua[e] >> 16)));
+    }
+    out[i] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+  if (h != nullptr) {
+    const __amdgpu_buffer_rsrc_t hd = make_rsrc(h + (size_t)r * dim, dim * 2);
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = i * 64 * WPR + part * 64 + lane;
+      __builtin_amdgcn_raw_buffer_store_b128(
+          (u32x4_t){out[i].x, out[i].y, out[i].z, out[i].w}, hd, c * 16, 0, 0);
+    }
+  }
+  // chunks past the row hold swiglu(0, 0) = 0 and leave the absmax alone
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) { amax = absmax8(out[i], amax); }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) { amax = fmaxf(amax, __shfl_xor(amax, o)); }
+  if constexpr (WPR > 1) {
+    __shared__ float red[WPR];
+    if (lane == 0) { red[part] = amax; }
+    __syncthreads();
+    amax = red[0];
+#pragma unroll
+    for (int p = 1; p < WPR; ++p) { amax = fmaxf(amax, red[p]); }
+  }
+  const float s = amax / 127.0f;
+  const float qinv = s != 0.0f ? 1.0f / s : 0.0f;
+  // 1/s overflows for rows with absmax below ~3.7e-37: division only.
+  const bool fast = qinv <= 3.4028234663852886e38f;
+  if (part == 0 && lane == 0) { sc[r] = s; }
+  const __amdgpu_buffer_rsrc_t qd = make_rsrc(q + (size_t)r * dim, dim);
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = i * 64 * WPR + part * 64 + lane;
+    const uint2 o = quant8(out[i], s, qinv, fast);
+    __builtin_amdgcn_raw_buffer_store_b64((u32x2_t){o.x, o.y}, qd, c * 8, 0, 0);
+  }
+}
+
 // ---- dst += src, the residual add (bf16, f32 add, one rounding) ------------
 // Eight elements per thread where both pointers are 16-byte aligned; the
 // tail (and misaligned operands) one element per thread.
@@ -3403,6 +3478,29 @@ launch_rms_norm(uint16_t* x, const uint16_t* d, const uint16_t* w_und,
 }
 
 hipError_t
+launch_swiglu_quant(const uint16_t* gate, const uint16_t* up, int rows, int dim,
+                    uint16_t* h, int8_t* q, float* sc, hipStream_t s)
+{
+  if (rows <= 0) { return hipSuccess; }
+#define U15H_SWQ(WPR, CPL)                                                    \
+  hipLaunchKernelGGL((swiglu_quant_rows_kernel<WPR, CPL>), dim3(rows),        \
+                     dim3(64 * WPR), 0, s, gate, up, dim, h, q, sc)
+  if (dim <= 2048) {
+    U15H_SWQ(4, 1);
+  } else if (dim <= 4096) {
+    U15H_SWQ(4, 2);
+  } else if (dim <= 8192) {
+    U15H_SWQ(4, 4);
+  } else if (dim <= 12288) {
+    U15H_SWQ(8, 3);
+  } else {
+    U15H_SWQ(8, 4);
+  }
+#undef U15H_SWQ
+  return hipGetLastError();
+}
+
+hipError_t
 launch_add_bf16(uint16_t* dst, const uint16_t* src, int64_t n, hipStream_t s)
 {
   if (n <= 0) { return hipSuccess; }
@@ -3716,6 +3814,11 @@ kernels_loadable()
       reinterpret_cast<const void*>(&rms_norm_rows_kernel<8, 4, false, true>),
       reinterpret_cast<const void*>(&rms_norm_rows_kernel<8, 4, true, true>),
       reinterpret_cast<const void*>(&add_bf16_kernel),
+      reinterpret_cast<const void*>(&swiglu_quant_rows_kernel<4, 1>),
+      reinterpret_cast<const void*>(&swiglu_quant_rows_kernel<4, 2>),
+      reinterpret_cast<const void*>(&swiglu_quant_rows_kernel<4, 4>),
+      reinterpret_cast<const void*>(&swiglu_quant_rows_kernel<8, 3>),
+      reinterpret_cast<const void*>(&swiglu_quant_rows_kernel<8, 4>),
       reinterpret_cast<const void*>(&attention_prologue_kernel<2>),
       reinterpret_cast<const void*>(&attention_prologue_kernel<4>),
       reinterpret_cast<const void*>(&quant_rows_i8_waves_kernel<4, 1, 1>),

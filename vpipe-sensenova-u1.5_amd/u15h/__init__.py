@@ -138,6 +138,7 @@ def load_library() -> ctypes.CDLL:
         "u15h_rms_norm_quant_i8": (i, [vp, vp, vp, vp, i, i, ctypes.c_float,
                                        vp, vp, vp]),
         "u15h_add": (i, [vp, vp, vp, vp, i64]),
+        "u15h_swiglu_quant_i8": (i, [vp, vp, vp, vp, i, i, vp, vp, vp]),
         "u15h_mot_rms_norm": (i, [vp, vp, vp, vp, i, i, i, vp, vp, ctypes.c_float,
                                   vp, vp, vp]),
         "u15h_build_rope_tables": (i, [vp, vp, vp, i, i, i, i,
@@ -630,6 +631,23 @@ class Ops:
         st = self._lib.u15h_swiglu(self._ctx, _stream(stream), _ptr(gate),
                                    _ptr(up), _ptr(out), n)
         self._check(st, "u15h_swiglu")
+
+    def swiglu_quant_i8(self, gate, up, q, s, h=None, stream=None):
+        """h = swiglu(gate, up) and its per-token int8 codes q, scales s in
+        one pass (h written only when given)."""
+        if gate.dim() != 2:
+            raise ValueError("gate must be [rows][inter]")
+        rows, inter = gate.shape
+        _need(gate, torch.bfloat16, (rows, inter), "gate")
+        _need(up, torch.bfloat16, (rows, inter), "up")
+        _need(q, torch.int8, (rows, inter), "q")
+        _need(s, torch.float32, (rows,), "s")
+        if h is not None:
+            _need(h, torch.bfloat16, (rows, inter), "h")
+        st = self._lib.u15h_swiglu_quant_i8(self._ctx, _stream(stream), _ptr(gate),
+                                            _ptr(up), rows, inter, _ptr(h), _ptr(q),
+                                            _ptr(s))
+        self._check(st, "u15h_swiglu_quant_i8")
 
     def mot_gate_up_swiglu(self, x, M_und, M_gen, K, wg_und, wu_und, wg_gen,
                            wu_gen, h, stream=None):
