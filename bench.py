@@ -363,8 +363,9 @@ def device_peaks(torch):
     """The box's own figures (hipDeviceGetAttribute: compute units, peak
     shader clock, memory clock and bus width) and the peaks they imply,
     beside the published ones the rooflines use: MFMA 4096 bf16 FLOP (8192
-    int8 OPs) per CU per clock, and HBM bus bytes x memory clock x 2
-    transfers per clock."""
+    int8 OPs) per CU per clock, and HBM bus bytes x memory clock x 4 (the
+    memory clock HIP reports for HBM moves 4 bits per pin: 2.0 GHz and 8
+    Gb/s per pin on MI355X)."""
     import ctypes
     hip = ctypes.CDLL("libamdhip64.so.7")
     hip.hipDeviceGetAttribute.argtypes = [ctypes.POINTER(ctypes.c_int), ctypes.c_int,
@@ -389,7 +390,7 @@ def device_peaks(torch):
         out["from_clock"] = {"bf16_tflops": round(cus * clk_khz * 1e3 * 4096 / 1e12, 1),
                              "int8_tops": round(cus * clk_khz * 1e3 * 8192 / 1e12, 1)}
         if bus_bits and mclk_khz:
-            out["from_clock"]["hbm_gbps"] = round(bus_bits / 8 * mclk_khz * 1e3 * 2 / 1e9, 1)
+            out["from_clock"]["hbm_gbps"] = round(bus_bits / 8 * mclk_khz * 1e3 * 4 / 1e9, 1)
     return out
 
 
