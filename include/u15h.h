@@ -648,6 +648,98 @@ u15h_status u15h_stack_forward(u15h_ctx* ctx, u15h_stream stream,
                                const u15h_stack* st, const u15h_layer_io* io,
                                int M_und, int M_gen, int tier, int flags);
 
+/* ---- the whole layer ------------------------------------------------ */
+
+/* The six norm vectors of an expert layer (ExpertLayer's input_ln,
+ * post_ln, q_norm, k_norm, q_norm_hw, k_norm_hw; src/u15-weights.h:97-110):
+ * input_ln and post_ln [hidden], the head norms [head_dim / 2]. */
+typedef enum {
+  U15H_NORM_INPUT = 0, U15H_NORM_POST = 1, U15H_NORM_Q = 2, U15H_NORM_K = 3,
+  U15H_NORM_Q_HW = 4, U15H_NORM_K_HW = 5, U15H_NNORM = 6
+} u15h_norm_id;
+
+/* Maps a reference norm name to its slot, by the layer binder's rule
+ * (src/u15-weights.cc:549-566):
+ *   language_model.model.layers.<i>.input_layernorm[_mot_gen]
+ *   language_model.model.layers.<i>.post_attention_layernorm[_mot_gen]
+ *   language_model.model.layers.<i>.self_attn.{q,k}_norm[_hw][_mot_gen]
+ * each optionally followed by ".weight" (the layernorms suffix the
+ * MODULE, the head norms the TENSOR).  Host only; EINVAL for any other
+ * name. */
+u15h_status u15h_norm_slot(const char* name, int* layer, int* expert,
+                           int* which);
+/* Binds a bf16 norm vector (device memory, 16-byte aligned) by name or by
+ * index. */
+u15h_status u15h_stack_bind_norm(u15h_stack* st, const char* name,
+                                 const u15h_bf16* w);
+u15h_status u15h_stack_set_norm(u15h_stack* st, int layer, int expert,
+                                int which, const u15h_bf16* w);
+/* ExpertLayer::complete (src/u15-weights.cc:333-339) in full: the seven
+ * matrices (bf16, or the int8 copies for tier 1) and the six norm vectors
+ * of every layer, for the und and/or gen expert.  On EINVAL `missing`
+ * receives the first missing reference name. */
+u15h_status u15h_stack_check_full(const u15h_stack* st, int need_und,
+                                  int need_gen, int tier, char* missing,
+                                  size_t missing_cap);
+
+/* The buffers of one whole layer: the residual stream, the reference's
+ * layer scratch, and the layer's K/V cache with the pass's position in it
+ * (the state U15Backbone::layer_step_ reads, src/u15-backbone.cc:174-257).
+ * Rows [0, M_und) und, then M_gen gen; M = M_und + M_gen. */
+typedef struct {
+  u15h_bf16*     x;        /* [M][hidden] the layer's input; on return
+                              its output (x + attention + MLP)          */
+  u15h_bf16*     normed;   /* [M][hidden] scratch (bf16 tier)            */
+  u15h_bf16*     q;        /* [M][heads*head_dim] scratch                */
+  u15h_bf16*     k;        /* [M][kv_heads*head_dim] scratch             */
+  u15h_bf16*     v;        /* [M][kv_heads*head_dim] scratch             */
+  u15h_bf16*     attn;     /* [M][heads*head_dim] scratch                */
+  u15h_bf16*     proj;     /* [M][hidden] scratch (o, then down)         */
+  u15h_bf16*     h;        /* [M][inter] scratch: SwiGLU output (bf16
+                              tier); the gate output (int8 tier)         */
+  u15h_bf16*     up;       /* [M][inter] scratch: the up output (int8
+                              tier only)                                 */
+  int8_t*        xq;       /* int8 tier: [M][max(hidden, heads*head_dim,
+                              inter)] activation codes                   */
+  float*         sx;       /* int8 tier: [M] per-token scales            */
+  u15h_bf16*     k_cache;  /* this layer's [kv_heads][cap][head_dim]     */
+  u15h_bf16*     v_cache;
+  int            cap;      /* cache capacity in tokens                   */
+  int            kv_off;   /* the pass's first position in the cache     */
+  int            kv_len;   /* keys attended, kv_off + M <= kv_len <= cap */
+  int            mode;     /* attention mask: 0 bidirectional, 1 causal,
+                              2 block-causal                             */
+  const int32_t* t_index;  /* block-causal: [max(kv_len, kv_off + M)]    */
+  const float*   cos_tab;  /* [M][head_dim] f32, u15h_build_rope_tables  */
+  const float*   sin_tab;
+  int            d_t, d_h; /* the RoPE ranges [t | h | w]                */
+  float          eps;      /* the norms' epsilon                         */
+} u15h_layer_full_io;
+
+/* One whole decoder layer, both experts per launch: U15Backbone::
+ * layer_step_ (src/u15-backbone.cc:174-257) for a pass of M_und und and
+ * M_gen gen tokens.  The steps, in launches:
+ *   normed = rms_norm(x) (each group its input_ln)    u15h_mot_rms_norm
+ *   q | k | v                                         u15h_mot_linear
+ *   q, k norm + RoPE; k, v into the cache at kv_off   u15h_mot_attention_prologue
+ *   attn = attention(q, cache[0, kv_len))             u15h_attention_token_major
+ *   proj = o(attn)                                    u15h_mot_linear
+ *   x += proj; normed = rms_norm(x) (post_ln)         u15h_mot_rms_norm
+ *   h = silu(gate) * up                               u15h_mot_gate_up_swiglu
+ *   proj = down(h); x += proj                         u15h_mot_linear, u15h_add
+ * Tier 1 (int8): the norms write the activation codes (u15h_mot_rms_norm
+ * with codes), attn is quantised, gate|up write gate and up, and SwiGLU
+ * writes the down projection's codes (u15h_swiglu_quant_i8); every
+ * projection is u15h_mot_gemm_i8.  Requires the one-launch prologue's
+ * shapes (u15h_mot_attention_prologue) and the stack complete for the
+ * experts with rows (u15h_stack_check_full).  Every argument is checked
+ * before the first launch.  No reference counterpart as one call; the
+ * layer loop with its per-layer stop stays with the caller. */
+u15h_status u15h_stack_layer_full(u15h_ctx* ctx, u15h_stream stream,
+                                  const u15h_stack* st, int layer,
+                                  const u15h_layer_full_io* io, int M_und,
+                                  int M_gen, int tier);
+
 /* ------------------------------------------------------------------ */
 /* profiling                                                           */
 /* ------------------------------------------------------------------ */

@@ -137,6 +137,76 @@ def test_weight_slot_round_trip_over_the_stack():
                 assert u15h.weight_slot(u15h.slot_name(layer, e, p)) == (layer, e, p)
 
 
+def test_norm_slot_reference_names():
+    """The layer binder's norm names (src/u15-weights.cc:549-566): the
+    layernorms suffix the module, the head norms the tensor, and the _hw
+    norms are not read as their shorter prefixes."""
+    ns = u15h.norm_slot
+    assert ns("language_model.model.layers.0.input_layernorm.weight") == (0, u15h.UND, 0)
+    assert ns("language_model.model.layers.3.input_layernorm_mot_gen.weight") == (3, u15h.GEN, 0)
+    assert ns("language_model.model.layers.41.post_attention_layernorm_mot_gen") == \
+        (41, u15h.GEN, 1)
+    assert ns("language_model.model.layers.2.self_attn.q_norm.weight") == (2, u15h.UND, 2)
+    assert ns("language_model.model.layers.2.self_attn.k_norm_mot_gen.weight") == (2, u15h.GEN, 3)
+    assert ns("language_model.model.layers.9.self_attn.q_norm_hw.weight") == (9, u15h.UND, 4)
+    assert ns("language_model.model.layers.9.self_attn.k_norm_hw_mot_gen") == (9, u15h.GEN, 5)
+
+
+@pytest.mark.parametrize("bad", [
+    "language_model.model.layers.3.self_attn.q_proj.weight",        # a matrix
+    "language_model.model.layers.3.self_attn.q_norm.bias",
+    "language_model.model.layers.3.self_attn.q_norm_mot_gen_hw.weight",   # suffix order
+    "language_model.model.layers.3.self_attn_mot_gen.q_norm.weight",
+    "language_model.model.layers.3.input_layernorm.weightx",
+    "language_model.model.layers.03.input_layernorm.weight",
+    "language_model.model.norm.weight",
+    "language_model.model.layers.3.mlp.input_layernorm.weight",
+    "",
+])
+def test_norm_slot_refuses_other_names(bad):
+    with pytest.raises(u15h.U15hError):
+        u15h.norm_slot(bad)
+
+
+def test_norm_slot_round_trip_and_weight_slot_keeps_refusing_norms():
+    for layer in (0, 7, 41):
+        for e in (u15h.UND, u15h.GEN):
+            for w in range(6):
+                name = u15h.norm_slot_name(layer, e, w)
+                assert u15h.norm_slot(name) == (layer, e, w)
+                with pytest.raises(u15h.U15hError):
+                    u15h.weight_slot(name)
+
+
+def test_stack_check_full_names_the_first_missing_norm():
+    """With every matrix bound (fake aligned device addresses: the check
+    reads pointers only), check_full names the first unbound norm."""
+    lib = u15h.load_library()
+    st = u15h.Stack(2)
+    for layer in range(2):
+        for e in (u15h.UND, u15h.GEN):
+            for p_ in range(7):
+                assert lib.u15h_stack_set(st._h, layer, e, p_, ctypes.c_void_p(4096),
+                                          None, None) == u15h.OK
+    assert st.check() is None
+    assert st.check_full() == "language_model.model.layers.0.input_layernorm.weight"
+    assert st.check_full(need_und=False) == \
+        "language_model.model.layers.0.input_layernorm_mot_gen.weight"
+    for layer in range(2):
+        for w in range(6):
+            assert lib.u15h_stack_set_norm(st._h, layer, u15h.UND, w,
+                                           ctypes.c_void_p(8192)) == u15h.OK
+    assert st.check_full(need_gen=False) is None
+    assert st.check_full() == "language_model.model.layers.0.input_layernorm_mot_gen.weight"
+    assert lib.u15h_stack_set_norm(st._h, 0, u15h.GEN, 6, ctypes.c_void_p(8192)) == u15h.EINVAL
+    assert lib.u15h_stack_set_norm(st._h, 2, u15h.GEN, 0, ctypes.c_void_p(8192)) == u15h.EINVAL
+    assert lib.u15h_stack_set_norm(st._h, 0, u15h.GEN, 0, ctypes.c_void_p(8)) == u15h.EINVAL
+    io = u15h._LayerFullIO()
+    assert lib.u15h_stack_layer_full(None, None, st._h, 0, ctypes.byref(io), 0, 1,
+                                     0) == u15h.EINVAL
+    st.close()
+
+
 def test_stack_check_names_the_first_missing_matrix():
     st = u15h.Stack(3)
     assert st.check() == "language_model.model.layers.0.self_attn.q_proj.weight"

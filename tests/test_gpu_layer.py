@@ -308,3 +308,204 @@ def test_decoder_layer_vs_reference(ops, expert):
     assert max_rel(got - xf, want - xf) <= 2e-2
     # the pass's expert is load-bearing
     assert rel_l2(got - xf, bad - xf) > 2e-2
+
+
+# ---- the whole layer through the stack ----------------------------------------
+
+def _bind_layer(st, layer, W):
+    """Bind one MotLayer by the reference's tensor names."""
+    proj_names = {"q_proj": "q", "k_proj": "k", "v_proj": "v", "o_proj": "o",
+                  "gate_proj": "gate", "up_proj": "up", "down_proj": "down"}
+    for e, ex in ((u15h.UND, W["und"]), (u15h.GEN, W["gen"])):
+        for rn, pn in proj_names.items():
+            st.bind(u15h.slot_name(layer, e, u15h.PROJ_NAMES.index(pn)), ex[rn])
+        for which, rn in enumerate(u15h.NORM_NAMES):
+            st.bind_norm(u15h.norm_slot_name(layer, e, which), ex[rn])
+
+
+@pytest.mark.parametrize("expert", ["gen", "und"])
+def test_stack_layer_full_two_layers_vs_reference(ops, expert):
+    """u15h_stack_layer_full over two stacked layers (matrices and norms bound
+    by the reference's names) for one expert's pass, against two chained
+    u15::ref::decoder_layer calls in f32 (forward_many's loop,
+    src/u15-backbone.cc:386-426).  The bf16 residual stream between the
+    layers is the only extra rounding.  Bar: rel-L2 < 2e-2 on the output
+    and on its change; the layers taken in the other order must miss."""
+    if oracle.ref_lib() is None:
+        pytest.skip("the compiled reference (oracle/_ref) is not built")
+    gen = expert == "gen"
+    T = 64
+    g = torch.Generator(device="cuda").manual_seed(5200 + gen)
+    Ws = [{"und": _expert(g), "gen": _expert(g)} for _ in range(2)]
+    st = u15h.Stack(2)
+    for layer in range(2):
+        _bind_layer(st, layer, Ws[layer])
+    assert st.check_full() is None
+    x = _bf16(g, (T, H))
+    if gen:
+        pos = (np.full(T, 17, np.int32), np.repeat(np.arange(8), 8).astype(np.int32),
+               np.tile(np.arange(8), 8).astype(np.int32))
+        mode, t_index, mask = 0, None, None
+    else:
+        pos = (np.arange(T, dtype=np.int32),) * 3
+        mode = 2
+        t_index = torch.from_numpy(pos[0]).cuda()
+        mask = oracle.ref_block_causal_mask(pos[0])
+    cs, sn = (torch.from_numpy(a).cuda() for a in u15h.build_rope_tables(*pos, HD, D_T, D_H))
+    Mu, Mg = (0, T) if gen else (T, 0)
+    xs = x.clone()
+    scratch = None
+    for layer in range(2):
+        kc = torch.empty(KV, T, HD, dtype=torch.bfloat16, device="cuda")
+        vc = torch.empty_like(kc)
+        scratch = ops.stack_layer_full(st, layer, Mu, Mg, xs, kc, vc, cs, sn, mode=mode,
+                                       t_index=t_index, scratch=scratch)
+    torch.cuda.synchronize()
+    got = host_f32(xs)
+    assert np.all(np.isfinite(got))
+
+    xf = _f32(x)
+
+    def ref(order):
+        y = xf
+        for layer in order:
+            w = {n: _f32(t) for n, t in Ws[layer][expert].items()}
+            y = oracle.ref_decoder_layer(y, w, NH, KV, HD, *pos, mask=mask)
+        return y
+
+    want = ref((0, 1))
+    swapped = ref((1, 0))
+    print(f"{expert}: two layers rel-L2 {rel_l2(got, want):.3e}, of the change "
+          f"{rel_l2(got - xf, want - xf):.3e}; layers swapped {rel_l2(got - xf, swapped - xf):.3e}")
+    assert rel_l2(got, want) < 2e-2
+    assert rel_l2(got - xf, want - xf) < 2e-2
+    assert rel_l2(got - xf, swapped - xf) > 2e-2
+    st.close()
+
+
+@pytest.mark.parametrize("tier", [u15h.TIER_BF16, u15h.TIER_I8])
+def test_stack_layer_full_mot_pass_equals_the_ops(ops, tier):
+    """A two-group MoT pass through u15h_stack_layer_full, after a cached
+    prefix (kv_off 16, block-causal), bit-equal to the same sequence of
+    public calls: the stack's orchestration adds nothing and drops nothing
+    (output, and both caches, slot for slot)."""
+    Mu, Mg, pre = 64, 192, 16
+    T = Mu + Mg
+    cap = pre + T + 8
+    g = torch.Generator(device="cuda").manual_seed(5300 + tier)
+    W = {"und": _expert(g), "gen": _expert(g)}
+    st = u15h.Stack(1)
+    _bind_layer(st, 0, W)
+    for e in ("und", "gen"):
+        for n in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj"):
+            wq = torch.empty(W[e][n].shape, dtype=torch.int8, device="cuda")
+            sw = torch.empty(W[e][n].shape[0], dtype=torch.float32, device="cuda")
+            ops.quant_rows_i8(W[e][n], wq, sw)
+            W[e][n + "_i8"] = (wq, sw)
+            pn = n.split("_")[0]
+            st.bind_i8(u15h.slot_name(0, u15h.UND if e == "und" else u15h.GEN,
+                                      u15h.PROJ_NAMES.index(pn)), wq, sw)
+    assert st.check_full(tier=tier) is None
+    pos_t = np.array(list(range(pre + Mu)) + [pre + Mu] * Mg, np.int32)
+    pos_h = np.array([0] * (pre + Mu) + [i // 16 for i in range(Mg)], np.int32)
+    pos_w = np.array([0] * (pre + Mu) + [i % 16 for i in range(Mg)], np.int32)
+    cs, sn = (torch.from_numpy(a).cuda() for a in
+              u15h.build_rope_tables(pos_t[pre:], pos_h[pre:], pos_w[pre:], HD, D_T, D_H))
+    t_index = torch.from_numpy(pos_t).cuda()
+    x = _bf16(g, (T, H))
+    kc0 = torch.full((KV, cap, HD), float("nan"), dtype=torch.bfloat16, device="cuda")
+    kc0[:, :pre] = _bf16(g, (KV, pre, HD))
+    vc0 = kc0.clone()
+    vc0[:, :pre] = _bf16(g, (KV, pre, HD))
+
+    # the stack
+    x1, kc1, vc1 = x.clone(), kc0.clone(), vc0.clone()
+    ops.stack_layer_full(st, 0, Mu, Mg, x1, kc1, vc1, cs, sn, kv_off=pre, mode=2,
+                         t_index=t_index, tier=tier)
+
+    # the public calls
+    x2, kc2, vc2 = x.clone(), kc0.clone(), vc0.clone()
+    sc = u15h.layer_scratch(st, T, tier)
+    und, gw = W["und"], W["gen"]
+    norms = {e: dict(q_t=W[e]["q_norm"], q_hw=W[e]["q_norm_hw"], k_t=W[e]["k_norm"],
+                     k_hw=W[e]["k_norm_hw"]) for e in ("und", "gen")}
+
+    def lin(inp, K, pairs):
+        ops.mot_linear(inp, Mu, Mg, K, [dict(w_und=und[n], w_gen=gw[n], y=y) for n, y in pairs])
+
+    def lin8(K, pairs):
+        ops.mot_gemm_i8(xq_view(K), sc["sx"], Mu, Mg,
+                        K, [dict(wq_und=und[n + "_i8"][0], sw_und=und[n + "_i8"][1],
+                                 wq_gen=gw[n + "_i8"][0], sw_gen=gw[n + "_i8"][1], y=y)
+                            for n, y in pairs])
+
+    def xq_view(K):
+        # the stack keeps the codes as [M][K] rows at the start of xq
+        return sc["xq"].view(-1)[:T * K].view(T, K)
+
+    if tier == u15h.TIER_I8:
+        ops.mot_rms_norm(x2, Mu, Mg, und["input_layernorm"], gw["input_layernorm"],
+                         q=xq_view(H), s=sc["sx"])
+        lin8(H, (("q_proj", sc["q"]), ("k_proj", sc["k"]), ("v_proj", sc["v"])))
+    else:
+        ops.mot_rms_norm(x2, Mu, Mg, und["input_layernorm"], gw["input_layernorm"],
+                         y=sc["normed"])
+        lin(sc["normed"], H, (("q_proj", sc["q"]), ("k_proj", sc["k"]), ("v_proj", sc["v"])))
+    ops.mot_attention_prologue(sc["q"], sc["k"], sc["v"], norms["und"], norms["gen"], cs, sn,
+                               Mu, Mg, NH, KV, HD, D_T, D_H, kc2, vc2, offset=pre)
+    ops.attention_token_major(sc["q"], kc2, vc2, sc["attn"], NH, KV, pre + T, mode=2,
+                              t_index=t_index, q_offset=pre)
+    if tier == u15h.TIER_I8:
+        ops.quant_rows_i8(sc["attn"], xq_view(NH * HD), sc["sx"])
+        lin8(NH * HD, (("o_proj", sc["proj"]),))
+        ops.mot_rms_norm(x2, Mu, Mg, und["post_attention_layernorm"],
+                         gw["post_attention_layernorm"], delta=sc["proj"], q=xq_view(H),
+                         s=sc["sx"])
+        lin8(H, (("gate_proj", sc["h"]), ("up_proj", sc["up"])))
+        ops.swiglu_quant_i8(sc["h"], sc["up"], xq_view(I), sc["sx"])
+        lin8(I, (("down_proj", sc["proj"]),))
+    else:
+        lin(sc["attn"], NH * HD, (("o_proj", sc["proj"]),))
+        ops.mot_rms_norm(x2, Mu, Mg, und["post_attention_layernorm"],
+                         gw["post_attention_layernorm"], delta=sc["proj"], y=sc["normed"])
+        ops.mot_gate_up_swiglu(sc["normed"], Mu, Mg, H, und["gate_proj"], und["up_proj"],
+                               gw["gate_proj"], gw["up_proj"], sc["h"])
+        lin(sc["h"], I, (("down_proj", sc["proj"]),))
+    ops.add(x2, sc["proj"])
+    torch.cuda.synchronize()
+    assert np.all(np.isfinite(host_f32(x1)))
+    assert np.array_equal(host_bits(x1), host_bits(x2))
+    assert np.array_equal(host_bits(kc1), host_bits(kc2))
+    assert np.array_equal(host_bits(vc1), host_bits(vc2))
+    st.close()
+
+
+def test_stack_layer_full_refuses_before_launching(ops):
+    """Refusals of u15h_stack_layer_full launch nothing: an unbound norm, a
+    cache too small for the pass, block-causal without t_index."""
+    st = u15h.Stack(1)
+    g = torch.Generator(device="cuda").manual_seed(3)
+    W = {"und": _expert(g), "gen": _expert(g)}
+    for e, ex in ((u15h.UND, W["und"]), (u15h.GEN, W["gen"])):
+        for pn, rn in zip(u15h.PROJ_NAMES, ("q_proj", "k_proj", "v_proj", "o_proj",
+                                             "gate_proj", "up_proj", "down_proj")):
+            st.bind(u15h.slot_name(0, e, u15h.PROJ_NAMES.index(pn)), ex[rn])
+    T = 16
+    x = _bf16(g, (T, H))
+    x0 = host_bits(x)
+    kc = torch.zeros(KV, T, HD, dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros_like(kc)
+    cs = torch.zeros(T, HD, dtype=torch.float32, device="cuda")
+    sn = torch.zeros_like(cs)
+    with pytest.raises(u15h.U15hError, match="norm"):
+        ops.stack_layer_full(st, 0, 0, T, x, kc, vc, cs, sn)
+    for which, rn in enumerate(u15h.NORM_NAMES):
+        st.bind_norm(u15h.norm_slot_name(0, u15h.GEN, which), W["gen"][rn])
+    with pytest.raises(u15h.U15hError, match="kv_off"):
+        ops.stack_layer_full(st, 0, 0, T, x, kc, vc, cs, sn, kv_off=4)
+    with pytest.raises(ValueError, match="t_index"):
+        ops.stack_layer_full(st, 0, 0, T, x, kc, vc, cs, sn, mode=2)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_bits(x), x0)
+    assert not torch.any(kc.view(torch.int16) != 0).item()
+    st.close()

@@ -13,6 +13,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <initializer_list>
 #include <string>
 #include <vector>
 
@@ -21,6 +22,17 @@
 struct u15h_stack {
   int n_layers = 0;
   int hidden = 0, qdim = 0, kvdim = 0, inter = 0;
+  int heads = 0, kv_heads = 0, head_dim = 0;
+  // [layer][expert][which] the six norm vectors of ExpertLayer
+  std::vector<const u15h_bf16*> norms;
+  const u15h_bf16*& norm(int l, int e, int w)
+  {
+    return norms[((size_t)l * 2 + e) * U15H_NNORM + w];
+  }
+  const u15h_bf16* norm(int l, int e, int w) const
+  {
+    return norms[((size_t)l * 2 + e) * U15H_NNORM + w];
+  }
   struct Slot {
     const u15h_bf16* w = nullptr;
     const int8_t* wq = nullptr;
@@ -84,6 +96,22 @@ slot_name(int l, int e, int p)
     return pre + "self_attn." + kProjName[p] + "_proj" + sfx + ".weight";
   }
   return pre + "mlp" + sfx + "." + kProjName[p] + "_proj.weight";
+}
+
+// The reference's name of a norm slot (for u15h_stack_check_full).
+std::string
+norm_name(int l, int w, int e)
+{
+  const std::string pre = "language_model.model.layers." + std::to_string(l) + ".";
+  const std::string sfx = e == U15H_GEN ? "_mot_gen" : "";
+  switch (w) {
+    case U15H_NORM_INPUT: return pre + "input_layernorm" + sfx + ".weight";
+    case U15H_NORM_POST: return pre + "post_attention_layernorm" + sfx + ".weight";
+    case U15H_NORM_Q: return pre + "self_attn.q_norm" + sfx + ".weight";
+    case U15H_NORM_K: return pre + "self_attn.k_norm" + sfx + ".weight";
+    case U15H_NORM_Q_HW: return pre + "self_attn.q_norm_hw" + sfx + ".weight";
+    default: return pre + "self_attn.k_norm_hw" + sfx + ".weight";
+  }
 }
 
 // Weights of every step in `steps` are bound for the experts with rows.
@@ -250,6 +278,101 @@ check_call(const u15h_stack* st, const u15h_layer_io* io, int M_und,
   return nullptr;
 }
 
+// "language_model.model.layers.<i>." with <i> a decimal layer index as
+// std::to_string writes it: no sign, no leading zero (except "0"), at most
+// 9 digits.
+bool
+eat_layer(const char** sp, long long* li)
+{
+  const char* s = *sp;
+  if (!eat(&s, "language_model.model.layers.")) { return false; }
+  if (*s < '0' || *s > '9' || (s[0] == '0' && s[1] >= '0' && s[1] <= '9')) {
+    return false;
+  }
+  long long v = 0;
+  int nd = 0;
+  while (*s >= '0' && *s <= '9') {
+    v = v * 10 + (*s - '0');
+    ++s;
+    if (++nd > 9) { return false; }
+  }
+  if (!eat(&s, ".")) { return false; }
+  *sp = s;
+  *li = v;
+  return true;
+}
+
+bool
+is_pow2(int v)
+{
+  return v > 0 && (v & (v - 1)) == 0;
+}
+
+// Arguments of a whole-layer call; nullptr if acceptable, else why not.
+const char*
+check_full_call(const u15h_stack* st, int layer, const u15h_layer_full_io* io,
+                int M_und, int M_gen, int tier)
+{
+  if (st == nullptr || io == nullptr) { return "null stack or io"; }
+  if (layer < 0 || layer >= st->n_layers) { return "layer index outside the stack"; }
+  if (M_und < 0 || M_gen < 0 || (long long)M_und + M_gen > (1 << 24)) {
+    return "row counts out of range";
+  }
+  if (tier != U15H_TIER_BF16 && tier != U15H_TIER_I8) { return "bad tier"; }
+  const int M = M_und + M_gen;
+  if (M == 0) { return nullptr; }
+  if (tier == U15H_TIER_I8) {
+    if (const char* why = i8_widths_error(st)) { return why; }
+  }
+  const int hd = st->head_dim;
+  if (hd != 32 && hd != 64 && hd != 128) {
+    return "whole layer: head_dim must be 32, 64 or 128 (the attention kernel's)";
+  }
+  if (io->d_t <= 0 || io->d_h <= 0 || io->d_t + 2 * io->d_h != hd ||
+      io->d_t % 16 || io->d_h % 16 || !is_pow2(io->d_t / 16) ||
+      !is_pow2(io->d_h / 16) || io->d_t % io->d_h) {
+    return "whole layer: the RoPE ranges must split head_dim as [t | h | w] with "
+           "d_t/16 and d_h/16 powers of two and d_h dividing d_t";
+  }
+  if (st->hidden > 16384 || (tier == U15H_TIER_I8 && st->inter > 16384)) {
+    return "whole layer: the norms take rows of at most 16384";
+  }
+  if (!(io->eps >= 0.0f)) { return "whole layer: eps must be >= 0"; }
+  if (io->mode < 0 || io->mode > 2) { return "whole layer: bad attention mode"; }
+  if (io->cap <= 0 || io->kv_off < 0 || (long long)io->kv_off + M > io->kv_len ||
+      io->kv_len > io->cap) {
+    return "whole layer: needs kv_off + M <= kv_len <= cap";
+  }
+  if ((long long)io->cap * hd * 2 >= (1LL << 31)) {
+    return "whole layer: one kv head's cache must stay below 2 GiB";
+  }
+  auto ok = [](const void* p) { return p != nullptr && aligned16(p); };
+  if (!(ok(io->x) && ok(io->q) && ok(io->k) && ok(io->v) && ok(io->attn) &&
+        ok(io->proj) && ok(io->h) && ok(io->k_cache) && ok(io->v_cache) &&
+        ok(io->cos_tab) && ok(io->sin_tab))) {
+    return "whole layer: an io buffer is null or not 16-byte aligned";
+  }
+  if (tier == U15H_TIER_BF16 ? !ok(io->normed)
+                             : !(ok(io->up) && ok(io->xq) && ok(io->sx))) {
+    return "whole layer: a tier buffer is null or not 16-byte aligned";
+  }
+  if (io->mode == 2 && io->t_index == nullptr) {
+    return "whole layer: block-causal attention needs t_index";
+  }
+  if (!step_weights_ok(st, layer, U15H_STEP_ALL, tier, M_und > 0, M_gen > 0)) {
+    return "a matrix the layer needs is not bound (u15h_stack_check_full names it)";
+  }
+  for (int e = 0; e < 2; ++e) {
+    if ((e == U15H_UND ? M_und : M_gen) == 0) { continue; }
+    for (int w = 0; w < U15H_NNORM; ++w) {
+      if (st->norm(layer, e, w) == nullptr) {
+        return "a norm the layer needs is not bound (u15h_stack_check_full names it)";
+      }
+    }
+  }
+  return nullptr;
+}
+
 }  // namespace
 
 extern "C" {
@@ -278,7 +401,11 @@ u15h_stack_create(int n_layers, int hidden, int heads, int kv_heads,
   st->qdim = (int)qd;
   st->kvdim = (int)kvd;
   st->inter = inter;
+  st->heads = heads;
+  st->kv_heads = kv_heads;
+  st->head_dim = head_dim;
   st->slots.resize((size_t)n_layers * 2 * U15H_NPROJ);
+  st->norms.assign((size_t)n_layers * 2 * U15H_NNORM, nullptr);
   *out = st;
   return U15H_OK;
 }
@@ -296,20 +423,8 @@ u15h_weight_slot(const char* name, int* layer, int* expert, int* proj)
     return U15H_EINVAL;
   }
   const char* s = name;
-  if (!eat(&s, "language_model.model.layers.")) { return U15H_EINVAL; }
-  // A decimal layer index as std::to_string writes it: no sign, no
-  // leading zero (except "0"), at most 9 digits.
-  if (*s < '0' || *s > '9' || (s[0] == '0' && s[1] >= '0' && s[1] <= '9')) {
-    return U15H_EINVAL;
-  }
   long long li = 0;
-  int nd = 0;
-  while (*s >= '0' && *s <= '9') {
-    li = li * 10 + (*s - '0');
-    ++s;
-    if (++nd > 9) { return U15H_EINVAL; }
-  }
-  if (!eat(&s, ".")) { return U15H_EINVAL; }
+  if (!eat_layer(&s, &li)) { return U15H_EINVAL; }
   int e = U15H_UND, p = -1;
   if (eat(&s, "self_attn.")) {
     // The attention suffixes the TENSOR: q_proj_mot_gen.
@@ -468,6 +583,186 @@ u15h_stack_forward(u15h_ctx* ctx, u15h_stream stream, const u15h_stack* st,
       if (r != U15H_OK) { return r; }
     }
   }
+  return U15H_OK;
+}
+
+u15h_status
+u15h_norm_slot(const char* name, int* layer, int* expert, int* which)
+{
+  if (name == nullptr || layer == nullptr || expert == nullptr || which == nullptr) {
+    return U15H_EINVAL;
+  }
+  const char* s = name;
+  long long li = 0;
+  if (!eat_layer(&s, &li)) { return U15H_EINVAL; }
+  int e = U15H_UND, w = -1;
+  if (eat(&s, "input_layernorm")) {
+    w = U15H_NORM_INPUT;          // the layernorms suffix the MODULE
+  } else if (eat(&s, "post_attention_layernorm")) {
+    w = U15H_NORM_POST;
+  } else if (eat(&s, "self_attn.")) {
+    // the head norms suffix the TENSOR: q_norm_hw_mot_gen (longest first)
+    if (eat(&s, "q_norm_hw")) {
+      w = U15H_NORM_Q_HW;
+    } else if (eat(&s, "k_norm_hw")) {
+      w = U15H_NORM_K_HW;
+    } else if (eat(&s, "q_norm")) {
+      w = U15H_NORM_Q;
+    } else if (eat(&s, "k_norm")) {
+      w = U15H_NORM_K;
+    } else {
+      return U15H_EINVAL;
+    }
+  } else {
+    return U15H_EINVAL;
+  }
+  if (eat(&s, "_mot_gen")) { e = U15H_GEN; }
+  (void)eat(&s, ".weight");
+  if (*s != '\0') { return U15H_EINVAL; }
+  *layer = (int)li;
+  *expert = e;
+  *which = w;
+  return U15H_OK;
+}
+
+u15h_status
+u15h_stack_set_norm(u15h_stack* st, int layer, int expert, int which,
+                    const u15h_bf16* w)
+{
+  if (st == nullptr || layer < 0 || layer >= st->n_layers ||
+      (expert != U15H_UND && expert != U15H_GEN) || which < 0 ||
+      which >= U15H_NNORM || w == nullptr || !aligned16(w)) {
+    return U15H_EINVAL;
+  }
+  st->norm(layer, expert, which) = w;
+  return U15H_OK;
+}
+
+u15h_status
+u15h_stack_bind_norm(u15h_stack* st, const char* name, const u15h_bf16* w)
+{
+  int l = 0, e = 0, k = 0;
+  if (st == nullptr || w == nullptr) { return U15H_EINVAL; }
+  u15h_status r = u15h_norm_slot(name, &l, &e, &k);
+  if (r != U15H_OK) { return r; }
+  return u15h_stack_set_norm(st, l, e, k, w);
+}
+
+u15h_status
+u15h_stack_check_full(const u15h_stack* st, int need_und, int need_gen,
+                      int tier, char* missing, size_t missing_cap)
+{
+  u15h_status r = u15h_stack_check(st, need_und, need_gen, tier, missing,
+                                   missing_cap);
+  if (r != U15H_OK) { return r; }
+  for (int l = 0; l < st->n_layers; ++l) {
+    for (int e = 0; e < 2; ++e) {
+      if ((e == U15H_UND && !need_und) || (e == U15H_GEN && !need_gen)) { continue; }
+      for (int w = 0; w < U15H_NNORM; ++w) {
+        if (st->norm(l, e, w) == nullptr) {
+          if (missing != nullptr && missing_cap > 0) {
+            std::snprintf(missing, missing_cap, "%s", norm_name(l, w, e).c_str());
+          }
+          return U15H_EINVAL;
+        }
+      }
+    }
+  }
+  return U15H_OK;
+}
+
+u15h_status
+u15h_stack_layer_full(u15h_ctx* ctx, u15h_stream stream, const u15h_stack* st,
+                      int layer, const u15h_layer_full_io* io, int M_und,
+                      int M_gen, int tier)
+{
+  if (ctx == nullptr) { return U15H_EINVAL; }
+  if (const char* why = check_full_call(st, layer, io, M_und, M_gen, tier)) {
+    return u15h::set_error(ctx, U15H_EINVAL, why);
+  }
+  const int M = M_und + M_gen;
+  if (M == 0) { return u15h::set_error(ctx, U15H_OK, ""); }
+  const bool i8 = tier == U15H_TIER_I8;
+  const u15h_bf16* const* nu = &st->norms[((size_t)layer * 2 + U15H_UND) * U15H_NNORM];
+  const u15h_bf16* const* ng = &st->norms[((size_t)layer * 2 + U15H_GEN) * U15H_NNORM];
+  const int H = st->hidden, I = st->inter;
+  u15h_status r = U15H_OK;
+#define U15H_RUN(call)                     \
+  do {                                     \
+    r = (call);                            \
+    if (r != U15H_OK) { return r; }        \
+  } while (0)
+  auto proj = [&](const u15h_bf16* in, int K, std::initializer_list<int> ids,
+                  std::initializer_list<u15h_bf16*> outs) {
+    u15h_mot_proj p[3];
+    int n = 0;
+    auto o = outs.begin();
+    for (int id : ids) { p[n++] = bf16_proj(st, layer, id, *o++); }
+    return u15h_mot_linear(ctx, stream, in, M_und, M_gen, K, p, n);
+  };
+  auto proj8 = [&](int K, std::initializer_list<int> ids,
+                   std::initializer_list<u15h_bf16*> outs) {
+    u15h_mot_proj_i8 p[3];
+    int n = 0;
+    auto o = outs.begin();
+    for (int id : ids) { p[n++] = i8_proj(st, layer, id, *o++); }
+    return u15h_mot_gemm_i8(ctx, stream, io->xq, io->sx, M_und, M_gen, K, p, n);
+  };
+  // attention: the input norm, q|k|v, the prologue, attention, o
+  if (i8) {
+    U15H_RUN(u15h_mot_rms_norm(ctx, stream, io->x, nullptr, M_und, M_gen, H,
+                               nu[U15H_NORM_INPUT], ng[U15H_NORM_INPUT], io->eps,
+                               nullptr, io->xq, io->sx));
+    U15H_RUN(proj8(H, {U15H_PROJ_Q, U15H_PROJ_K, U15H_PROJ_V}, {io->q, io->k, io->v}));
+  } else {
+    U15H_RUN(u15h_mot_rms_norm(ctx, stream, io->x, nullptr, M_und, M_gen, H,
+                               nu[U15H_NORM_INPUT], ng[U15H_NORM_INPUT], io->eps,
+                               io->normed, nullptr, nullptr));
+    U15H_RUN(proj(io->normed, H, {U15H_PROJ_Q, U15H_PROJ_K, U15H_PROJ_V},
+                  {io->q, io->k, io->v}));
+  }
+  const u15h_qk_norm qn_u = {nu[U15H_NORM_Q], nu[U15H_NORM_Q_HW], nu[U15H_NORM_K],
+                             nu[U15H_NORM_K_HW]};
+  const u15h_qk_norm qn_g = {ng[U15H_NORM_Q], ng[U15H_NORM_Q_HW], ng[U15H_NORM_K],
+                             ng[U15H_NORM_K_HW]};
+  U15H_RUN(u15h_mot_attention_prologue(ctx, stream, io->q, io->k, io->v,
+                                       M_und > 0 ? &qn_u : nullptr,
+                                       M_gen > 0 ? &qn_g : nullptr, io->cos_tab,
+                                       io->sin_tab, M_und, M_gen, st->heads,
+                                       st->kv_heads, st->head_dim, io->d_t, io->d_h,
+                                       io->eps, io->k_cache, io->v_cache, io->cap,
+                                       io->kv_off));
+  U15H_RUN(u15h_attention_token_major(ctx, stream, io->q, io->k_cache, io->v_cache,
+                                      io->attn, io->t_index, st->heads, st->kv_heads,
+                                      M, io->kv_len, st->head_dim, io->cap,
+                                      io->kv_off, io->mode));
+  if (i8) {
+    U15H_RUN(u15h_quant_rows_i8(ctx, stream, io->attn, M, st->qdim, io->xq, io->sx));
+    U15H_RUN(proj8(st->qdim, {U15H_PROJ_O}, {io->proj}));
+    // x += o; the post norm's codes
+    U15H_RUN(u15h_mot_rms_norm(ctx, stream, io->x, io->proj, M_und, M_gen, H,
+                               nu[U15H_NORM_POST], ng[U15H_NORM_POST], io->eps,
+                               nullptr, io->xq, io->sx));
+    U15H_RUN(proj8(H, {U15H_PROJ_GATE, U15H_PROJ_UP}, {io->h, io->up}));
+    U15H_RUN(u15h_swiglu_quant_i8(ctx, stream, io->h, io->up, M, I, nullptr, io->xq,
+                                  io->sx));
+    U15H_RUN(proj8(I, {U15H_PROJ_DOWN}, {io->proj}));
+  } else {
+    U15H_RUN(proj(io->attn, st->qdim, {U15H_PROJ_O}, {io->proj}));
+    // x += o; normed = the post norm
+    U15H_RUN(u15h_mot_rms_norm(ctx, stream, io->x, io->proj, M_und, M_gen, H,
+                               nu[U15H_NORM_POST], ng[U15H_NORM_POST], io->eps,
+                               io->normed, nullptr, nullptr));
+    const auto& gu = st->at(layer, U15H_UND, U15H_PROJ_GATE);
+    const auto& uu = st->at(layer, U15H_UND, U15H_PROJ_UP);
+    const auto& gg = st->at(layer, U15H_GEN, U15H_PROJ_GATE);
+    const auto& ug = st->at(layer, U15H_GEN, U15H_PROJ_UP);
+    U15H_RUN(u15h_mot_gate_up_swiglu(ctx, stream, io->normed, M_und, M_gen, H, gu.w,
+                                     uu.w, gg.w, ug.w, io->h, I));
+    U15H_RUN(proj(io->h, I, {U15H_PROJ_DOWN}, {io->proj}));
+  }
+  U15H_RUN(u15h_add(ctx, stream, io->x, io->proj, (int64_t)M * H));
+#undef U15H_RUN
   return U15H_OK;
 }
 

@@ -63,6 +63,16 @@ class _QkNorm(ctypes.Structure):
                 ("k_t", ctypes.c_void_p), ("k_hw", ctypes.c_void_p)]
 
 
+class _LayerFullIO(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in
+                ("x", "normed", "q", "k", "v", "attn", "proj", "h", "up", "xq",
+                 "sx", "k_cache", "v_cache")] + \
+               [(n, ctypes.c_int) for n in ("cap", "kv_off", "kv_len", "mode")] + \
+               [("t_index", ctypes.c_void_p), ("cos_tab", ctypes.c_void_p),
+                ("sin_tab", ctypes.c_void_p), ("d_t", ctypes.c_int),
+                ("d_h", ctypes.c_int), ("eps", ctypes.c_float)]
+
+
 class _QWeight(ctypes.Structure):
     _fields_ = [("codes", ctypes.c_void_p), ("scales", ctypes.c_void_p),
                 ("biases", ctypes.c_void_p), ("bits", ctypes.c_int),
@@ -160,6 +170,13 @@ def load_library() -> ctypes.CDLL:
         "u15h_stack_bind_i8": (i, [vp, ctypes.c_char_p, vp, vp]),
         "u15h_stack_set": (i, [vp, i, i, i, vp, vp, vp]),
         "u15h_stack_check": (i, [vp, i, i, i, ctypes.c_char_p, ctypes.c_size_t]),
+        "u15h_norm_slot": (i, [ctypes.c_char_p, ctypes.POINTER(i), ctypes.POINTER(i),
+                               ctypes.POINTER(i)]),
+        "u15h_stack_bind_norm": (i, [vp, ctypes.c_char_p, vp]),
+        "u15h_stack_set_norm": (i, [vp, i, i, i, vp]),
+        "u15h_stack_check_full": (i, [vp, i, i, i, ctypes.c_char_p, ctypes.c_size_t]),
+        "u15h_stack_layer_full": (i, [vp, vp, vp, i, ctypes.POINTER(_LayerFullIO), i, i,
+                                      i]),
         "u15h_stack_layer": (i, [vp, vp, vp, i, ctypes.POINTER(_LayerIO), i,
                                  i, i, i, i]),
         "u15h_stack_forward": (i, [vp, vp, vp, ctypes.POINTER(_LayerIO), i,
@@ -223,6 +240,33 @@ def slot_name(layer: int, expert: int, proj: int) -> str:
     return f"{pre}mlp{sfx}.{n}_proj.weight"
 
 
+NORM_NAMES = ("input_layernorm", "post_attention_layernorm", "q_norm", "k_norm",
+              "q_norm_hw", "k_norm_hw")
+
+
+def norm_slot(name: str) -> tuple[int, int, int]:
+    """(layer, expert, norm index) of a reference norm name, by the layer
+    binder's rule (src/u15-weights.cc:549-566); U15hError otherwise."""
+    lib = load_library()
+    l, e, w = ctypes.c_int(0), ctypes.c_int(0), ctypes.c_int(0)
+    st = lib.u15h_norm_slot(name.encode(), ctypes.byref(l), ctypes.byref(e),
+                            ctypes.byref(w))
+    if st != OK:
+        raise U15hError(st, f"not a layer norm name: {name!r}")
+    return l.value, e.value, w.value
+
+
+def norm_slot_name(layer: int, expert: int, which: int) -> str:
+    """The reference's tensor name of a norm slot (the inverse of norm_slot):
+    the layernorms suffix the module, the head norms the tensor."""
+    pre = f"language_model.model.layers.{layer}."
+    sfx = "_mot_gen" if expert == GEN else ""
+    n = NORM_NAMES[which]
+    if which <= 1:
+        return f"{pre}{n}{sfx}.weight"
+    return f"{pre}self_attn.{n}{sfx}.weight"
+
+
 class Stack:
     """u15h_stack: n_layers MotLayers of device-pointer bindings (the
     reference's MotLayer{und, gen}, src/u15-weights.h:97-117).  Holds a
@@ -238,6 +282,7 @@ class Stack:
             raise U15hError(st, "u15h_stack_create: invalid shape")
         self._h = h
         self.n_layers = n_layers
+        self.heads, self.kv_heads, self.head_dim = heads, kv_heads, head_dim
         self.hidden, self.qdim = hidden, heads * head_dim
         self.kvdim, self.inter = kv_heads * head_dim, inter
         self._keep = {}
@@ -267,6 +312,22 @@ class Stack:
         if st != OK:
             raise U15hError(st, f"u15h_stack_bind_i8({name})")
         self._keep[(l, e, p, "q")] = (wq, sw)
+
+    def bind_norm(self, name, w):
+        l, e, k = norm_slot(name)
+        _need(w, torch.bfloat16, (self.hidden if k <= 1 else self.head_dim // 2,), name)
+        st = self._lib.u15h_stack_bind_norm(self._h, name.encode(), _ptr(w))
+        if st != OK:
+            raise U15hError(st, f"u15h_stack_bind_norm({name})")
+        self._keep[(l, e, k, "n")] = w
+
+    def check_full(self, need_und=True, need_gen=True, tier=TIER_BF16):
+        """None if every matrix and norm of the pass is bound, else the first
+        missing reference name."""
+        buf = ctypes.create_string_buffer(256)
+        st = self._lib.u15h_stack_check_full(self._h, int(need_und), int(need_gen),
+                                             tier, buf, 256)
+        return None if st == OK else buf.value.decode()
 
     def check(self, need_und=True, need_gen=True, tier=TIER_BF16):
         """None if the pass's matrices are bound, else the first missing
@@ -470,6 +531,22 @@ def _need(t, dtype, shape, name):
         raise ValueError(f"{name} must be contiguous")
     if t.device.type != "cuda":
         raise ValueError(f"{name} must be on the GPU")
+
+
+def layer_scratch(stack, M, tier=TIER_BF16, device="cuda"):
+    """The scratch buffers of u15h_stack_layer_full for M rows."""
+    def bf(n):
+        return torch.empty(M, n, dtype=torch.bfloat16, device=device)
+    sc = dict(q=bf(stack.qdim), k=bf(stack.kvdim), v=bf(stack.kvdim),
+              attn=bf(stack.qdim), proj=bf(stack.hidden), h=bf(stack.inter))
+    if tier == TIER_I8:
+        sc["up"] = bf(stack.inter)
+        sc["xq"] = torch.empty(M, max(stack.hidden, stack.qdim, stack.inter),
+                               dtype=torch.int8, device=device)
+        sc["sx"] = torch.empty(M, dtype=torch.float32, device=device)
+    else:
+        sc["normed"] = bf(stack.hidden)
+    return sc
 
 
 class Ops:
@@ -832,6 +909,42 @@ class Ops:
             _ptr(cos), _ptr(sin), M_und, M_gen, hq, hkv, head_dim, d_t, d_h,
             eps, _ptr(k_cache), _ptr(v_cache), cap, offset)
         self._check(st, "u15h_mot_attention_prologue")
+
+    def stack_layer_full(self, stack, layer, M_und, M_gen, x, k_cache, v_cache,
+                         cos, sin, kv_off=0, kv_len=None, mode=0, t_index=None,
+                         d_t=None, d_h=None, eps=1e-6, tier=TIER_BF16, scratch=None,
+                         stream=None):
+        """u15h_stack_layer_full: one whole decoder layer of the stack on
+        the residual stream x [M][hidden] (updated in place), attending this
+        layer's caches [kv_heads][cap][head_dim] over keys [0, kv_len) with
+        the pass at kv_off.  `scratch` (a dict from layer_scratch) is made
+        when not given and returned."""
+        M = M_und + M_gen
+        hd = stack.head_dim
+        d_t = hd // 2 if d_t is None else d_t
+        d_h = hd // 4 if d_h is None else d_h
+        kv_len = kv_off + M if kv_len is None else kv_len
+        _need(x, torch.bfloat16, (M, stack.hidden), "x")
+        cap = k_cache.shape[1]
+        _need(k_cache, torch.bfloat16, (stack.kv_heads, cap, hd), "k_cache")
+        _need(v_cache, torch.bfloat16, (stack.kv_heads, cap, hd), "v_cache")
+        _need(cos, torch.float32, (M, hd), "cos")
+        _need(sin, torch.float32, (M, hd), "sin")
+        if mode == 2 and (t_index is None or t_index.dtype != torch.int32 or
+                          t_index.numel() < max(kv_len, kv_off + M)):
+            raise ValueError("t_index: int32 covering max(kv_len, kv_off + M)")
+        if scratch is None:
+            scratch = layer_scratch(stack, M, tier)
+        sc = scratch
+        io = _LayerFullIO(
+            _ptr(x), _ptr(sc.get("normed")), _ptr(sc["q"]), _ptr(sc["k"]), _ptr(sc["v"]),
+            _ptr(sc["attn"]), _ptr(sc["proj"]), _ptr(sc["h"]), _ptr(sc.get("up")),
+            _ptr(sc.get("xq")), _ptr(sc.get("sx")), _ptr(k_cache), _ptr(v_cache),
+            cap, kv_off, kv_len, mode, _ptr(t_index), _ptr(cos), _ptr(sin), d_t, d_h, eps)
+        st = self._lib.u15h_stack_layer_full(self._ctx, _stream(stream), stack._h, layer,
+                                             ctypes.byref(io), M_und, M_gen, tier)
+        self._check(st, "u15h_stack_layer_full")
+        return scratch
 
     # ---- the layer norms and the residual add --------------------------
     def rms_norm(self, x, w, y, eps=1e-6, stream=None):
