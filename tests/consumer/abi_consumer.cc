@@ -11,7 +11,14 @@
 //   3. the layer stack: all 14 matrices bound by the reference's tensor
 //      names, u15h_stack_layer over the four steps;
 // and checks sampled rows of every output against the oracle's restatement
-// of ref::linear (max-rel <= 1e-2, rel-L2 < 4e-3).  Exit status 0 = pass.
+// of ref::linear (max-rel <= 1e-2, rel-L2 < 4e-3); then
+//   4. the whole layer: the 12 norm vectors bound by their names too, one
+//      u15h_stack_layer_full call (both groups, block-causal attention over
+//      the layer's cache), checked bit for bit against the same layer made
+//      of the public calls (u15h_mot_rms_norm, u15h_mot_linear,
+//      u15h_mot_attention_prologue, u15h_attention_token_major,
+//      u15h_mot_gate_up_swiglu, u15h_add).
+// Exit status 0 = pass.
 #include <hip/hip_runtime_api.h>
 
 #include <cmath>
@@ -49,6 +56,18 @@ randn_bf16(uint32_t seed, size_t n, float stddev)
 {
   std::vector<float> f(n);
   u15o_randn_mt(seed, stddev, n, f.data());
+  std::vector<uint16_t> b(n);
+  u15o_f32_to_bf16_n(f.data(), n, b.data());
+  return b;
+}
+
+// Host bf16 bits ~N(mean, std): the norm gains.
+std::vector<uint16_t>
+randn_bf16_mean(uint32_t seed, size_t n, float mean, float stddev)
+{
+  std::vector<float> f(n);
+  u15o_randn_mt(seed, stddev, n, f.data());
+  for (float& v : f) { v += mean; }
   std::vector<uint16_t> b(n);
   u15o_f32_to_bf16_n(f.data(), n, b.data());
   return b;
@@ -221,6 +240,108 @@ main()
              M, H, I);
   check_rows("stack down", download(down, (size_t)M * H), hh, wh[0][6], wh[1][6],
              Mu, M, I, H);
+
+  // ---- 4. the whole layer: norms bound by name, one call --------------
+  static const char* kNorm[U15H_NNORM] = {"input_layernorm", "post_attention_layernorm",
+                                          "self_attn.q_norm", "self_attn.k_norm",
+                                          "self_attn.q_norm_hw", "self_attn.k_norm_hw"};
+  Dev* nd[2][U15H_NNORM];
+  for (int e = 0; e < 2; ++e) {
+    const std::string sfx = e ? "_mot_gen" : "";
+    for (int n = 0; n < U15H_NNORM; ++n) {
+      const size_t len = n < 2 ? (size_t)H : (size_t)HD / 2;
+      nd[e][n] = upload(randn_bf16_mean(300u + 10u * e + n, len, 1.0f, 0.2f));
+      const std::string name = "language_model.model.layers.0." + std::string(kNorm[n]) +
+                               sfx + ".weight";
+      if (u15h_stack_bind_norm(stk, name.c_str(), nd[e][n]->as<const u15h_bf16>()) !=
+          U15H_OK) {
+        check(false, "bind " + name);
+      }
+    }
+  }
+  check(u15h_stack_check_full(stk, 1, 1, U15H_TIER_BF16, missing, sizeof missing) ==
+            U15H_OK, "ExpertLayer complete: 13 tensors per expert bound");
+  // positions: 64 text tokens, then a 12 x 16 image block on one t
+  std::vector<int32_t> pt(M), ph(M), pw(M);
+  for (int i = 0; i < M; ++i) {
+    pt[i] = i < Mu ? i : Mu;
+    ph[i] = i < Mu ? 0 : (i - Mu) / 16;
+    pw[i] = i < Mu ? 0 : (i - Mu) % 16;
+  }
+  std::vector<float> cs((size_t)M * HD), sn((size_t)M * HD);
+  check(u15h_build_rope_tables(pt.data(), ph.data(), pw.data(), M, HD, 64, 32, 5.0e6,
+                               1.0e4, cs.data(), sn.data()) == U15H_OK, "rope tables");
+  Dev csd(cs.size() * 4), snd(sn.size() * 4), tid((size_t)M * 4);
+  HIP_OK(hipMemcpy(csd.p, cs.data(), csd.bytes, hipMemcpyHostToDevice));
+  HIP_OK(hipMemcpy(snd.p, sn.data(), snd.bytes, hipMemcpyHostToDevice));
+  HIP_OK(hipMemcpy(tid.p, pt.data(), tid.bytes, hipMemcpyHostToDevice));
+  Dev xa((size_t)M * H * 2), xb((size_t)M * H * 2), normed((size_t)M * H * 2),
+      proj((size_t)M * H * 2), hh2((size_t)M * I * 2),
+      kca((size_t)KV * M * HD * 2), vca((size_t)KV * M * HD * 2),
+      kcb((size_t)KV * M * HD * 2), vcb((size_t)KV * M * HD * 2);
+  HIP_OK(hipMemcpy(xa.p, x->p, xa.bytes, hipMemcpyDeviceToDevice));
+  HIP_OK(hipMemcpy(xb.p, x->p, xb.bytes, hipMemcpyDeviceToDevice));
+  u15h_layer_full_io fio = {};
+  fio.x = xa.as<u15h_bf16>();
+  fio.normed = normed.as<u15h_bf16>();
+  fio.q = q.as<u15h_bf16>();
+  fio.k = k.as<u15h_bf16>();
+  fio.v = v.as<u15h_bf16>();
+  fio.attn = o.as<u15h_bf16>();
+  fio.proj = proj.as<u15h_bf16>();
+  fio.h = hh2.as<u15h_bf16>();
+  fio.k_cache = kca.as<u15h_bf16>();
+  fio.v_cache = vca.as<u15h_bf16>();
+  fio.cap = M;
+  fio.kv_off = 0;
+  fio.kv_len = M;
+  fio.mode = 2;
+  fio.t_index = tid.as<const int32_t>();
+  fio.cos_tab = csd.as<const float>();
+  fio.sin_tab = snd.as<const float>();
+  fio.d_t = 64;
+  fio.d_h = 32;
+  fio.eps = 1e-6f;
+  st = u15h_stack_layer_full(ctx, stream, stk, 0, &fio, Mu, Mg, U15H_TIER_BF16);
+  check(st == U15H_OK, std::string("u15h_stack_layer_full: ") + u15h_last_error(ctx));
+  // the same layer from the public calls, on xb and the second cache pair
+  auto N = [&](int e, int n) { return nd[e][n]->as<const u15h_bf16>(); };
+  bool calls_ok = true;
+  auto run = [&](u15h_status r) { calls_ok = calls_ok && r == U15H_OK; };
+  run(u15h_mot_rms_norm(ctx, stream, xb.as<u15h_bf16>(), nullptr, Mu, Mg, H, N(0, 0),
+                        N(1, 0), 1e-6f, normed.as<u15h_bf16>(), nullptr, nullptr));
+  run(u15h_mot_linear(ctx, stream, normed.as<u15h_bf16>(), Mu, Mg, H, qkv, 3));
+  const u15h_qk_norm qn[2] = {{N(0, 2), N(0, 4), N(0, 3), N(0, 5)},
+                              {N(1, 2), N(1, 4), N(1, 3), N(1, 5)}};
+  run(u15h_mot_attention_prologue(ctx, stream, q.as<u15h_bf16>(), k.as<u15h_bf16>(),
+                                  v.as<u15h_bf16>(), &qn[0], &qn[1], csd.as<const float>(),
+                                  snd.as<const float>(), Mu, Mg, NH, KV, HD, 64, 32, 1e-6f,
+                                  kcb.as<u15h_bf16>(), vcb.as<u15h_bf16>(), M, 0));
+  run(u15h_attention_token_major(ctx, stream, q.as<u15h_bf16>(), kcb.as<u15h_bf16>(),
+                                 vcb.as<u15h_bf16>(), o.as<u15h_bf16>(),
+                                 tid.as<const int32_t>(), NH, KV, M, M, HD, M, 0, 2));
+  u15h_mot_proj po = {W(0, 3), W(1, 3), nullptr, nullptr, proj.as<u15h_bf16>(), H};
+  run(u15h_mot_linear(ctx, stream, o.as<u15h_bf16>(), Mu, Mg, NH * HD, &po, 1));
+  run(u15h_mot_rms_norm(ctx, stream, xb.as<u15h_bf16>(), proj.as<u15h_bf16>(), Mu, Mg, H,
+                        N(0, 1), N(1, 1), 1e-6f, normed.as<u15h_bf16>(), nullptr, nullptr));
+  run(u15h_mot_gate_up_swiglu(ctx, stream, normed.as<u15h_bf16>(), Mu, Mg, H, W(0, 4),
+                              W(0, 5), W(1, 4), W(1, 5), hh2.as<u15h_bf16>(), I));
+  u15h_mot_proj pd = {W(0, 6), W(1, 6), nullptr, nullptr, proj.as<u15h_bf16>(), H};
+  run(u15h_mot_linear(ctx, stream, hh2.as<u15h_bf16>(), Mu, Mg, I, &pd, 1));
+  run(u15h_add(ctx, stream, xb.as<u15h_bf16>(), proj.as<u15h_bf16>(), (int64_t)M * H));
+  check(calls_ok, std::string("the layer from the public calls: ") + u15h_last_error(ctx));
+  HIP_OK(hipStreamSynchronize(stream));
+  const std::vector<uint16_t> ya = download(xa, (size_t)M * H);
+  const std::vector<uint16_t> yb = download(xb, (size_t)M * H);
+  bool finite = true;
+  for (uint16_t b : ya) { finite = finite && (b & 0x7f80u) != 0x7f80u; }
+  check(finite && ya != xh, "whole layer: finite output that differs from its input");
+  check(ya == yb && download(kca, kca.bytes / 2) == download(kcb, kcb.bytes / 2) &&
+            download(vca, vca.bytes / 2) == download(vcb, vcb.bytes / 2),
+        "whole layer: bit-equal to the public calls (output and both caches)");
+  for (auto& row : nd) {
+    for (Dev* d : row) { delete d; }
+  }
   u15h_stack_destroy(stk);
 
   for (auto& row : wd) {
