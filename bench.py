@@ -586,7 +586,65 @@ def stack_passes(torch, u15h, ops, model, gen, args, want_i8):
                 one[tier]["hbm_frac"] = round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM, 4)
         res[f"m{mu}_{mg}"] = one
         del t, io
+    res["whole_layers"] = stack_full_pass(torch, u15h, ops, model, gen, args, want_i8)
     return res
+
+
+def stack_full_pass(torch, u15h, ops, model, gen, args, want_i8):
+    """forward_many's pass over all the resident layers, whole layers this
+    time: u15h_stack_layer_full per layer (norms, projections, attention
+    prologue, block-causal attention over that layer's own K/V cache,
+    residuals) at 128 + 4096 tokens as one MoT pass, both tiers.  The norm
+    vectors are bound by their reference names beside the matrices."""
+    import numpy as np
+    L, Mu, Mg = model.n_layers, 128, 4096
+    T = Mu + Mg
+    HD, KVH = 128, NKV // 128
+    st = model.stack
+    for layer in range(L):
+        for e in (u15h.UND, u15h.GEN):
+            for which in range(6):
+                n = HIDDEN if which <= 1 else HD // 2
+                w = (1 + 0.1 * torch.randn(n, generator=gen, device="cuda")).to(torch.bfloat16)
+                st.bind_norm(u15h.norm_slot_name(layer, e, which), w)
+    pos_t = np.array(list(range(Mu)) + [Mu] * Mg, np.int32)
+    pos_h = np.array([0] * Mu + [i // 64 for i in range(Mg)], np.int32)
+    pos_w = np.array([0] * Mu + [i % 64 for i in range(Mg)], np.int32)
+    cs, sn = (torch.from_numpy(a).cuda() for a in
+              u15h.build_rope_tables(pos_t, pos_h, pos_w, HD, 64, 32))
+    t_index = torch.from_numpy(pos_t).cuda()
+    caches = [(torch.empty(KVH, T, HD, dtype=torch.bfloat16, device="cuda"),
+               torch.empty(KVH, T, HD, dtype=torch.bfloat16, device="cuda"))
+              for _ in range(L)]
+    x = torch.randn(T, HIDDEN, generator=gen, device="cuda").to(torch.bfloat16)
+    tiers = [("bf16", u15h.TIER_BF16)] + ([("int8", u15h.TIER_I8)] if want_i8 else [])
+    scratch = {name: u15h.layer_scratch(st, T, tier) for name, tier in tiers}
+
+    def run(tier, name):
+        def f():
+            for layer in range(L):
+                kc, vc = caches[layer]
+                ops.stack_layer_full(st, layer, Mu, Mg, x, kc, vc, cs, sn, mode=2,
+                                     t_index=t_index, tier=tier, scratch=scratch[name])
+        return f
+
+    arms = {name: [run(tier, name)] for name, tier in tiers}
+    got = interleaved(torch, arms, 2, max(3, args.rounds // 2))
+    pairs = Mu * (Mu + 1) // 2 + Mg * T
+    flop = (FLOP_PER_ROW * T + 4 * NQ * pairs) * L
+    out = {"workload": f"{L} whole layers, {Mu} text + {Mg} image tokens as one MoT "
+                       "pass, block-causal attention over each layer's cache",
+           "flop_per_pass": {"projections": FLOP_PER_ROW * T * L,
+                             "attention": 4 * NQ * pairs * L}}
+    for name, g in got.items():
+        ms = g["median_ms"]
+        rate = flop / (ms * 1e-3) / 1e12
+        out[name] = {"ms_per_pass": ms, "ms_per_layer": round(ms / L, 4),
+                     "value": round(rate, 2), "unit": "TFLOP/s",
+                     "pct_of_bf16_peak": round(100 * rate / PEAK_BF16, 2),
+                     "min_ms": g["min_ms"], "max_ms": g["max_ms"]}
+    del caches, scratch
+    return out
 
 
 def ab_compare(torch, u15h, ops, spec, model, io, args, want_i8):
