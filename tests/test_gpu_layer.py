@@ -570,3 +570,51 @@ def test_stack_layer_full_int8_tracks_the_reference(ops, expert):
     assert r_near < 6e-2
     assert r_far > 10 * r_near
     st.close()
+
+
+def test_stack_layer_full_prefix_then_generation_equals_one_pass(ops):
+    """The reference generator's flow (src/u15-generator.cc:379, 537-548):
+    a prefill pass of the und prefix fills the layer's cache, then a
+    generation pass of the gen tokens at kv_off = the prefix attends the
+    frozen prefix.  With the block-causal mask the prefix never sees the
+    image, so the two passes must give the joint pass's outputs and cache.
+    The passes take other GEMM routes (the 64-row prefix the skinny one),
+    so the sums differ in order only: rel-L2 < 4e-3 and max-rel <= 1e-2
+    (the reference's kernel bar)."""
+    Mu, Mg = 64, 192
+    T = Mu + Mg
+    g = torch.Generator(device="cuda").manual_seed(5500)
+    W = {"und": _expert(g), "gen": _expert(g)}
+    st = u15h.Stack(1)
+    _bind_layer(st, 0, W)
+    pos_t = np.array(list(range(Mu)) + [Mu] * Mg, np.int32)
+    pos_h = np.array([0] * Mu + [i // 16 for i in range(Mg)], np.int32)
+    pos_w = np.array([0] * Mu + [i % 16 for i in range(Mg)], np.int32)
+    cs, sn = (torch.from_numpy(a).cuda() for a in
+              u15h.build_rope_tables(pos_t, pos_h, pos_w, HD, D_T, D_H))
+    t_index = torch.from_numpy(pos_t).cuda()
+    x = _bf16(g, (T, H))
+
+    def caches():
+        return (torch.full((KV, T, HD), float("nan"), dtype=torch.bfloat16, device="cuda"),
+                torch.full((KV, T, HD), float("nan"), dtype=torch.bfloat16, device="cuda"))
+
+    xj = x.clone()
+    kj, vj = caches()
+    ops.stack_layer_full(st, 0, Mu, Mg, xj, kj, vj, cs, sn, mode=2, t_index=t_index)
+    xp, xg = x[:Mu].clone(), x[Mu:].clone()
+    ks, vs = caches()
+    ops.stack_layer_full(st, 0, Mu, 0, xp, ks, vs, cs[:Mu], sn[:Mu], kv_off=0, kv_len=Mu,
+                         mode=2, t_index=t_index)
+    ops.stack_layer_full(st, 0, 0, Mg, xg, ks, vs, cs[Mu:], sn[Mu:], kv_off=Mu, kv_len=T,
+                         mode=2, t_index=t_index)
+    torch.cuda.synchronize()
+    got = np.concatenate([host_f32(xp), host_f32(xg)])
+    want = host_f32(xj)
+    xf = _f32(x)
+    for name, a, b in (("output", got, want), ("change", got - xf, want - xf),
+                       ("k cache", host_f32(ks), host_f32(kj)),
+                       ("v cache", host_f32(vs), host_f32(vj))):
+        print(f"{name}: rel-L2 {rel_l2(a, b):.2e}, max-rel {max_rel(a, b):.2e}")
+        assert rel_l2(a, b) < 4e-3 and max_rel(a, b) <= 1e-2, name
+    st.close()
