@@ -131,6 +131,11 @@ def parse(argv=None):
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy 5 times "
                          "(calibrates rocprof FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--vendor", action="store_true",
+                    help="only compare u15h_linear with hipBLASLt (torch's bf16 "
+                         "linear) on plain GEMMs")
+    ap.add_argument("--vendor-shape", default=None,
+                    help="MxNxK: restrict --vendor to one shape")
     a = ap.parse_args(argv)
     mu, mg, layers, _ = WORKLOADS[a.workload]
     a.m_und = mu if a.m_und is None else a.m_und
@@ -679,6 +684,56 @@ def ab_compare(torch, u15h, ops, spec, model, io, args, want_i8):
                                           / got["a_int8"]["median_ms"], 4)
     ops_b.close()
     return out
+
+
+# Plain GEMMs y[M][N] = x[M][K] . w[N][K]^T for the vendor comparison: the
+# gen group's gate|up, down and q|k|v, one full round of 256 tiles, a
+# square case, and down over the und + gen rows as one matrix.
+VENDOR_SHAPES = [(4096, 24576, 4096), (4096, 4096, 12288), (4096, 4096, 8192),
+                 (4096, 6144, 4096), (8192, 8192, 8192), (4224, 4096, 12288)]
+
+
+def vendor_compare(torch, ops, gen, calls, rounds, only=None):
+    """u15h_linear against hipBLASLt, the library torch's bf16 linear runs on
+    ROCm, on plain GEMMs: N(0,1) activations, N(0,0.02) weights, two weight
+    copies alternated, `calls` calls per sample, medians of `rounds`
+    interleaved samples per arm.  `max_abs_diff` compares the two outputs
+    of the last call."""
+    shapes = VENDOR_SHAPES
+    if only:
+        shapes = [tuple(int(v) for v in only.lower().split("x"))]
+    rows = []
+    for M, N, K in shapes:
+        x = torch.randn(M, K, generator=gen, device="cuda").to(torch.bfloat16)
+        ws = [(torch.randn(N, K, generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+              for _ in range(2)]
+        y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+        ref = {}
+
+        def ours(i):
+            ops.linear(x, ws[i % 2], None, y, M, K, N)
+
+        def vendor(i):
+            ref["y"] = torch.nn.functional.linear(x, ws[i % 2])
+        arms = {"u15h": [lambda i=i: ours(i) for i in range(2)],
+                "hipblaslt": [lambda i=i: vendor(i) for i in range(2)]}
+        for runs in arms.values():
+            warm(torch, runs, 5, 200.0)
+        got = interleaved(torch, arms, max(1, calls // 2), rounds)
+        torch.cuda.synchronize()
+        flop = 2.0 * M * N * K
+        row = {"M": M, "N": N, "K": K}
+        for name, g in got.items():
+            ms = g["median_ms"] / 2
+            row[name] = {"ms_per_call": round(ms, 5),
+                         "TFLOP_s": round(flop / (ms * 1e-3) / 1e12, 1)}
+        row["u15h_over_vendor"] = round(row["u15h"]["TFLOP_s"] / row["hipblaslt"]["TFLOP_s"], 3)
+        row["max_abs_diff"] = float((y.float() - ref["y"].float()).abs().max())
+        rows.append(row)
+        del x, ws, y, ref
+    return {"vendor": {"library": "hipBLASLt via torch.nn.functional.linear",
+                       "calls_per_sample": max(1, calls // 2) * 2,
+                       "rounds": rounds, "rows": rows}}
 
 
 def m_sweep(torch, u15h, ops, gen, rounds):
@@ -1363,6 +1418,11 @@ def main(argv=None):
         return
     if args.m_sweep:
         print(json.dumps(m_sweep(torch, u15h, ops, gen, args.rounds)), flush=True)
+        ops.close()
+        return
+    if args.vendor:
+        print(json.dumps(vendor_compare(torch, ops, gen, args.steps, args.rounds,
+                                        args.vendor_shape)), flush=True)
         ops.close()
         return
     want_i8 = not args.no_int8

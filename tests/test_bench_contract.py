@@ -239,3 +239,18 @@ def test_tier_result_checks_that_the_kernels_fit_the_step(int8):
     assert ok["avg_launch_ms"] * 4 + ok["split_reduce_ms_per_step"] <= per_step * 1.01
     bad = bench.tier_result(w, per_step * 0.97, k, steps, int8, None)["roofline"]
     assert not bad["fits_step"]
+
+
+def test_vendor_shapes_are_the_gen_groups_projections():
+    """--vendor times plain GEMMs at the gen group's own shapes: gate|up
+    (N = 2I), down (K = I) and q|k|v (N = q + 2 kv) over the 4096 gen
+    rows, and down over the und + gen rows as one matrix."""
+    H, I, NQ, NKV = bench.HIDDEN, bench.INTER, bench.NQ, bench.NKV
+    shapes = set(bench.VENDOR_SHAPES)
+    assert (4096, 2 * I, H) in shapes
+    assert (4096, H, I) in shapes
+    assert (4096, NQ + 2 * NKV, H) in shapes
+    assert (4224, H, I) in shapes
+    a = bench.parse(["--vendor", "--vendor-shape", "4096x24576x4096"])
+    assert a.vendor and a.vendor_shape == "4096x24576x4096"
+    assert not bench.parse([]).vendor
