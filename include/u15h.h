@@ -740,6 +740,26 @@ u15h_status u15h_stack_layer_full(u15h_ctx* ctx, u15h_stream stream,
                                   const u15h_layer_full_io* io, int M_und,
                                   int M_gen, int tier);
 
+/* Whole layers [first, first + count) in order, one pass through each:
+ * forward_many's layer loop (src/u15-backbone.cc:386-426) over
+ * u15h_stack_layer_full, on one io.  Layer first + i attends its own cache,
+ * k_caches[i] / v_caches[i] ([kv_heads][cap][head_dim] each; the io's
+ * k_cache and v_cache are not read); cap, kv_off, kv_len, mode and the
+ * RoPE tables are the pass's, the same for every layer.  Between two
+ * layers, the first's residual add and the second's input norm run as one
+ * pass (u15h_mot_rms_norm with the down output as the residual), which
+ * gives the same bits as count calls of u15h_stack_layer_full.  Every
+ * layer's arguments are checked before the first launch.  There is no
+ * stop hook between layers: a caller that needs the reference's
+ * cooperative per-layer stop (src/u15-backbone.cc:394-397) loops
+ * u15h_stack_layer_full itself. */
+u15h_status u15h_stack_forward_full(u15h_ctx* ctx, u15h_stream stream,
+                                    const u15h_stack* st, int first, int count,
+                                    const u15h_layer_full_io* io,
+                                    u15h_bf16* const* k_caches,
+                                    u15h_bf16* const* v_caches, int M_und,
+                                    int M_gen, int tier);
+
 /* ------------------------------------------------------------------ */
 /* profiling                                                           */
 /* ------------------------------------------------------------------ */

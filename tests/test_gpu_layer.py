@@ -480,6 +480,118 @@ def test_stack_layer_full_mot_pass_equals_the_ops(ops, tier):
     st.close()
 
 
+def _stack_of(ops, n, seed):
+    """A stack of n whole layers (matrices, their int8 copies and the norms
+    bound by the reference's names) with random weights."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    st = u15h.Stack(n)
+    for layer in range(n):
+        W = {"und": _expert(g), "gen": _expert(g)}
+        _bind_layer(st, layer, W)
+        for e in ("und", "gen"):
+            for rn in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj",
+                       "down_proj"):
+                wq = torch.empty(W[e][rn].shape, dtype=torch.int8, device="cuda")
+                sw = torch.empty(W[e][rn].shape[0], dtype=torch.float32, device="cuda")
+                ops.quant_rows_i8(W[e][rn], wq, sw)
+                st.bind_i8(u15h.slot_name(layer, u15h.UND if e == "und" else u15h.GEN,
+                                          u15h.PROJ_NAMES.index(rn.split("_")[0])), wq, sw)
+    return st, g
+
+
+@pytest.mark.parametrize("tier", [u15h.TIER_BF16, u15h.TIER_I8])
+def test_stack_forward_full_equals_the_layer_calls(ops, tier):
+    """u15h_stack_forward_full over layers [0, 3) and over [1, 3) of a
+    3-layer stack, a two-group MoT pass after a cached prefix (kv_off 16,
+    block-causal): bit-equal to u15h_stack_layer_full layer by layer (the
+    residual add fused with the next layer's input norm gives the same
+    bits), the output and every layer's two caches slot for slot."""
+    n, Mu, Mg, pre = 3, 64, 192, 16
+    T = Mu + Mg
+    cap = pre + T + 8
+    st, g = _stack_of(ops, n, 5600 + tier)
+    assert st.check_full(tier=tier) is None
+    pos_t = np.array(list(range(pre + Mu)) + [pre + Mu] * Mg, np.int32)
+    pos_h = np.array([0] * (pre + Mu) + [i // 16 for i in range(Mg)], np.int32)
+    pos_w = np.array([0] * (pre + Mu) + [i % 16 for i in range(Mg)], np.int32)
+    cs, sn = (torch.from_numpy(a).cuda() for a in
+              u15h.build_rope_tables(pos_t[pre:], pos_h[pre:], pos_w[pre:], HD, D_T, D_H))
+    t_index = torch.from_numpy(pos_t).cuda()
+    x = _bf16(g, (T, H))
+    caches0 = []
+    for _ in range(n):
+        kc = torch.full((KV, cap, HD), float("nan"), dtype=torch.bfloat16, device="cuda")
+        kc[:, :pre] = _bf16(g, (KV, pre, HD))
+        vc = kc.clone()
+        vc[:, :pre] = _bf16(g, (KV, pre, HD))
+        caches0.append((kc, vc))
+    for first in (0, 1):
+        count = n - first
+        x1 = x.clone()
+        c1 = [(k.clone(), v.clone()) for k, v in caches0[first:]]
+        ops.stack_forward_full(st, first, count, Mu, Mg, x1, [k for k, _ in c1],
+                               [v for _, v in c1], cs, sn, kv_off=pre, mode=2,
+                               t_index=t_index, tier=tier)
+        x2 = x.clone()
+        c2 = [(k.clone(), v.clone()) for k, v in caches0[first:]]
+        for i in range(count):
+            ops.stack_layer_full(st, first + i, Mu, Mg, x2, c2[i][0], c2[i][1], cs, sn,
+                                 kv_off=pre, mode=2, t_index=t_index, tier=tier)
+        torch.cuda.synchronize()
+        assert np.all(np.isfinite(host_f32(x1)))
+        assert not np.array_equal(host_bits(x1), host_bits(x))
+        assert np.array_equal(host_bits(x1), host_bits(x2)), first
+        for (ka, va), (kb, vb) in zip(c1, c2):
+            assert np.array_equal(host_bits(ka), host_bits(kb))
+            assert np.array_equal(host_bits(va), host_bits(vb))
+    st.close()
+
+
+def test_stack_forward_full_refuses_before_launching(ops):
+    """Refusals of u15h_stack_forward_full launch nothing: a layer range
+    outside the stack, a later layer with a norm unbound (the message names
+    the layer), a scratch buffer that is x, a cache count that does not
+    match."""
+    n, T = 2, 16
+    st, g = _stack_of(ops, n, 5700)
+    x = _bf16(g, (T, H))
+    x0 = host_bits(x)
+    caches = [(torch.zeros(KV, T, HD, dtype=torch.bfloat16, device="cuda"),
+               torch.zeros(KV, T, HD, dtype=torch.bfloat16, device="cuda")) for _ in range(n)]
+    ks, vs = [c[0] for c in caches], [c[1] for c in caches]
+    cs = torch.zeros(T, HD, dtype=torch.float32, device="cuda")
+    sn = torch.zeros_like(cs)
+    with pytest.raises(u15h.U15hError, match="outside the stack"):
+        ops.stack_forward_full(st, 1, 2, 0, T, x, ks, vs, cs, sn)
+    with pytest.raises(ValueError, match="caches"):
+        ops.stack_forward_full(st, 0, 2, 0, T, x, ks[:1], vs[:1], cs, sn)
+    sc = u15h.layer_scratch(st, T, u15h.TIER_BF16)
+    bad = dict(sc, proj=x)
+    with pytest.raises(u15h.U15hError, match="scratch buffer is x"):
+        ops.stack_forward_full(st, 0, 2, 0, T, x, ks, vs, cs, sn, scratch=bad)
+    # layer 1's gen input norm gone: refused, naming layer 1, before layer 0 runs
+    st2 = u15h.Stack(n)
+    g2 = torch.Generator(device="cuda").manual_seed(5701)
+    for layer in range(n):
+        W = {"und": _expert(g2), "gen": _expert(g2)}
+        for e, ex in ((u15h.UND, W["und"]), (u15h.GEN, W["gen"])):
+            for pn, rn in zip(u15h.PROJ_NAMES, ("q_proj", "k_proj", "v_proj", "o_proj",
+                                                 "gate_proj", "up_proj", "down_proj")):
+                st2.bind(u15h.slot_name(layer, e, u15h.PROJ_NAMES.index(pn)), ex[rn])
+            for which, rn in enumerate(u15h.NORM_NAMES):
+                if not (layer == 1 and e == u15h.GEN and which == 0):
+                    st2.bind_norm(u15h.norm_slot_name(layer, e, which), ex[rn])
+    with pytest.raises(u15h.U15hError, match="layer 1: .*norm"):
+        ops.stack_forward_full(st2, 0, 2, 0, T, x, ks, vs, cs, sn)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_bits(x), x0)
+    for k, v in caches:
+        assert not torch.any(k.view(torch.int16) != 0).item()
+        assert not torch.any(v.view(torch.int16) != 0).item()
+    st.close()
+    st2.close()
+
+
 def test_stack_layer_full_refuses_before_launching(ops):
     """Refusals of u15h_stack_layer_full launch nothing: an unbound norm, a
     cache too small for the pass, block-causal without t_index."""

@@ -359,6 +359,13 @@ check_full_call(const u15h_stack* st, int layer, const u15h_layer_full_io* io,
   if (io->mode == 2 && io->t_index == nullptr) {
     return "whole layer: block-causal attention needs t_index";
   }
+  // the residual stream keeps its sum: no scratch buffer may be x (the
+  // post-attention norm would refuse it after the layer's first launches)
+  for (const void* p : {(const void*)io->normed, (const void*)io->q, (const void*)io->k,
+                        (const void*)io->v, (const void*)io->attn, (const void*)io->proj,
+                        (const void*)io->h, (const void*)io->up}) {
+    if (p == io->x) { return "whole layer: a scratch buffer is x"; }
+  }
   if (!step_weights_ok(st, layer, U15H_STEP_ALL, tier, M_und > 0, M_gen > 0)) {
     return "a matrix the layer needs is not bound (u15h_stack_check_full names it)";
   }
@@ -372,6 +379,113 @@ check_full_call(const u15h_stack* st, int layer, const u15h_layer_full_io* io,
   }
   return nullptr;
 }
+
+// One whole layer, its arguments already checked (check_full_call) and M >
+// 0.  `input_normed`: the input norm's output (normed, or xq and sx for
+// the int8 tier) is already in io, written by the previous layer's last
+// pass.  `next` >= 0: instead of the residual add, that pass is the add
+// and layer `next`'s input norm together (u15h_mot_rms_norm with the down
+// output as delta), the same bits as u15h_add then the norm.
+u15h_status
+run_full_layer(u15h_ctx* ctx, u15h_stream stream, const u15h_stack* st, int layer,
+               const u15h_layer_full_io* io, int M_und, int M_gen, int tier,
+               bool input_normed, int next)
+{
+  const int M = M_und + M_gen;
+  const bool i8 = tier == U15H_TIER_I8;
+  const u15h_bf16* const* nu = &st->norms[((size_t)layer * 2 + U15H_UND) * U15H_NNORM];
+  const u15h_bf16* const* ng = &st->norms[((size_t)layer * 2 + U15H_GEN) * U15H_NNORM];
+  const int H = st->hidden, I = st->inter;
+  u15h_status r = U15H_OK;
+#define U15H_RUN(call)                     \
+  do {                                     \
+    r = (call);                            \
+    if (r != U15H_OK) { return r; }        \
+  } while (0)
+  auto proj = [&](const u15h_bf16* in, int K, std::initializer_list<int> ids,
+                  std::initializer_list<u15h_bf16*> outs) {
+    u15h_mot_proj p[3];
+    int n = 0;
+    auto o = outs.begin();
+    for (int id : ids) { p[n++] = bf16_proj(st, layer, id, *o++); }
+    return u15h_mot_linear(ctx, stream, in, M_und, M_gen, K, p, n);
+  };
+  auto proj8 = [&](int K, std::initializer_list<int> ids,
+                   std::initializer_list<u15h_bf16*> outs) {
+    u15h_mot_proj_i8 p[3];
+    int n = 0;
+    auto o = outs.begin();
+    for (int id : ids) { p[n++] = i8_proj(st, layer, id, *o++); }
+    return u15h_mot_gemm_i8(ctx, stream, io->xq, io->sx, M_und, M_gen, K, p, n);
+  };
+  // attention: the input norm, q|k|v, the prologue, attention, o
+  if (!input_normed) {
+    U15H_RUN(u15h_mot_rms_norm(ctx, stream, io->x, nullptr, M_und, M_gen, H,
+                               nu[U15H_NORM_INPUT], ng[U15H_NORM_INPUT], io->eps,
+                               i8 ? nullptr : io->normed, i8 ? io->xq : nullptr,
+                               i8 ? io->sx : nullptr));
+  }
+  if (i8) {
+    U15H_RUN(proj8(H, {U15H_PROJ_Q, U15H_PROJ_K, U15H_PROJ_V}, {io->q, io->k, io->v}));
+  } else {
+    U15H_RUN(proj(io->normed, H, {U15H_PROJ_Q, U15H_PROJ_K, U15H_PROJ_V},
+                  {io->q, io->k, io->v}));
+  }
+  const u15h_qk_norm qn_u = {nu[U15H_NORM_Q], nu[U15H_NORM_Q_HW], nu[U15H_NORM_K],
+                             nu[U15H_NORM_K_HW]};
+  const u15h_qk_norm qn_g = {ng[U15H_NORM_Q], ng[U15H_NORM_Q_HW], ng[U15H_NORM_K],
+                             ng[U15H_NORM_K_HW]};
+  U15H_RUN(u15h_mot_attention_prologue(ctx, stream, io->q, io->k, io->v,
+                                       M_und > 0 ? &qn_u : nullptr,
+                                       M_gen > 0 ? &qn_g : nullptr, io->cos_tab,
+                                       io->sin_tab, M_und, M_gen, st->heads,
+                                       st->kv_heads, st->head_dim, io->d_t, io->d_h,
+                                       io->eps, io->k_cache, io->v_cache, io->cap,
+                                       io->kv_off));
+  U15H_RUN(u15h_attention_token_major(ctx, stream, io->q, io->k_cache, io->v_cache,
+                                      io->attn, io->t_index, st->heads, st->kv_heads,
+                                      M, io->kv_len, st->head_dim, io->cap,
+                                      io->kv_off, io->mode));
+  if (i8) {
+    U15H_RUN(u15h_quant_rows_i8(ctx, stream, io->attn, M, st->qdim, io->xq, io->sx));
+    U15H_RUN(proj8(st->qdim, {U15H_PROJ_O}, {io->proj}));
+    // x += o; the post norm's codes
+    U15H_RUN(u15h_mot_rms_norm(ctx, stream, io->x, io->proj, M_und, M_gen, H,
+                               nu[U15H_NORM_POST], ng[U15H_NORM_POST], io->eps,
+                               nullptr, io->xq, io->sx));
+    U15H_RUN(proj8(H, {U15H_PROJ_GATE, U15H_PROJ_UP}, {io->h, io->up}));
+    U15H_RUN(u15h_swiglu_quant_i8(ctx, stream, io->h, io->up, M, I, nullptr, io->xq,
+                                  io->sx));
+    U15H_RUN(proj8(I, {U15H_PROJ_DOWN}, {io->proj}));
+  } else {
+    U15H_RUN(proj(io->attn, st->qdim, {U15H_PROJ_O}, {io->proj}));
+    // x += o; normed = the post norm
+    U15H_RUN(u15h_mot_rms_norm(ctx, stream, io->x, io->proj, M_und, M_gen, H,
+                               nu[U15H_NORM_POST], ng[U15H_NORM_POST], io->eps,
+                               io->normed, nullptr, nullptr));
+    const auto& gu = st->at(layer, U15H_UND, U15H_PROJ_GATE);
+    const auto& uu = st->at(layer, U15H_UND, U15H_PROJ_UP);
+    const auto& gg = st->at(layer, U15H_GEN, U15H_PROJ_GATE);
+    const auto& ug = st->at(layer, U15H_GEN, U15H_PROJ_UP);
+    U15H_RUN(u15h_mot_gate_up_swiglu(ctx, stream, io->normed, M_und, M_gen, H, gu.w,
+                                     uu.w, gg.w, ug.w, io->h, I));
+    U15H_RUN(proj(io->h, I, {U15H_PROJ_DOWN}, {io->proj}));
+  }
+  if (next < 0) {
+    U15H_RUN(u15h_add(ctx, stream, io->x, io->proj, (int64_t)M * H));
+  } else {
+    // x += down; the next layer's input norm (its codes for the int8 tier)
+    const u15h_bf16* const* xu = &st->norms[((size_t)next * 2 + U15H_UND) * U15H_NNORM];
+    const u15h_bf16* const* xg = &st->norms[((size_t)next * 2 + U15H_GEN) * U15H_NNORM];
+    U15H_RUN(u15h_mot_rms_norm(ctx, stream, io->x, io->proj, M_und, M_gen, H,
+                               xu[U15H_NORM_INPUT], xg[U15H_NORM_INPUT], io->eps,
+                               i8 ? nullptr : io->normed, i8 ? io->xq : nullptr,
+                               i8 ? io->sx : nullptr));
+  }
+#undef U15H_RUN
+  return U15H_OK;
+}
+
 
 }  // namespace
 
@@ -680,89 +794,44 @@ u15h_stack_layer_full(u15h_ctx* ctx, u15h_stream stream, const u15h_stack* st,
   if (const char* why = check_full_call(st, layer, io, M_und, M_gen, tier)) {
     return u15h::set_error(ctx, U15H_EINVAL, why);
   }
-  const int M = M_und + M_gen;
-  if (M == 0) { return u15h::set_error(ctx, U15H_OK, ""); }
-  const bool i8 = tier == U15H_TIER_I8;
-  const u15h_bf16* const* nu = &st->norms[((size_t)layer * 2 + U15H_UND) * U15H_NNORM];
-  const u15h_bf16* const* ng = &st->norms[((size_t)layer * 2 + U15H_GEN) * U15H_NNORM];
-  const int H = st->hidden, I = st->inter;
-  u15h_status r = U15H_OK;
-#define U15H_RUN(call)                     \
-  do {                                     \
-    r = (call);                            \
-    if (r != U15H_OK) { return r; }        \
-  } while (0)
-  auto proj = [&](const u15h_bf16* in, int K, std::initializer_list<int> ids,
-                  std::initializer_list<u15h_bf16*> outs) {
-    u15h_mot_proj p[3];
-    int n = 0;
-    auto o = outs.begin();
-    for (int id : ids) { p[n++] = bf16_proj(st, layer, id, *o++); }
-    return u15h_mot_linear(ctx, stream, in, M_und, M_gen, K, p, n);
-  };
-  auto proj8 = [&](int K, std::initializer_list<int> ids,
-                   std::initializer_list<u15h_bf16*> outs) {
-    u15h_mot_proj_i8 p[3];
-    int n = 0;
-    auto o = outs.begin();
-    for (int id : ids) { p[n++] = i8_proj(st, layer, id, *o++); }
-    return u15h_mot_gemm_i8(ctx, stream, io->xq, io->sx, M_und, M_gen, K, p, n);
-  };
-  // attention: the input norm, q|k|v, the prologue, attention, o
-  if (i8) {
-    U15H_RUN(u15h_mot_rms_norm(ctx, stream, io->x, nullptr, M_und, M_gen, H,
-                               nu[U15H_NORM_INPUT], ng[U15H_NORM_INPUT], io->eps,
-                               nullptr, io->xq, io->sx));
-    U15H_RUN(proj8(H, {U15H_PROJ_Q, U15H_PROJ_K, U15H_PROJ_V}, {io->q, io->k, io->v}));
-  } else {
-    U15H_RUN(u15h_mot_rms_norm(ctx, stream, io->x, nullptr, M_und, M_gen, H,
-                               nu[U15H_NORM_INPUT], ng[U15H_NORM_INPUT], io->eps,
-                               io->normed, nullptr, nullptr));
-    U15H_RUN(proj(io->normed, H, {U15H_PROJ_Q, U15H_PROJ_K, U15H_PROJ_V},
-                  {io->q, io->k, io->v}));
+  if (M_und + M_gen == 0) { return u15h::set_error(ctx, U15H_OK, ""); }
+  return run_full_layer(ctx, stream, st, layer, io, M_und, M_gen, tier, false, -1);
+}
+
+u15h_status
+u15h_stack_forward_full(u15h_ctx* ctx, u15h_stream stream, const u15h_stack* st,
+                        int first, int count, const u15h_layer_full_io* io,
+                        u15h_bf16* const* k_caches, u15h_bf16* const* v_caches,
+                        int M_und, int M_gen, int tier)
+{
+  if (ctx == nullptr) { return U15H_EINVAL; }
+  if (st == nullptr || io == nullptr || k_caches == nullptr || v_caches == nullptr) {
+    return u15h::set_error(ctx, U15H_EINVAL, "null stack, io or cache array");
   }
-  const u15h_qk_norm qn_u = {nu[U15H_NORM_Q], nu[U15H_NORM_Q_HW], nu[U15H_NORM_K],
-                             nu[U15H_NORM_K_HW]};
-  const u15h_qk_norm qn_g = {ng[U15H_NORM_Q], ng[U15H_NORM_Q_HW], ng[U15H_NORM_K],
-                             ng[U15H_NORM_K_HW]};
-  U15H_RUN(u15h_mot_attention_prologue(ctx, stream, io->q, io->k, io->v,
-                                       M_und > 0 ? &qn_u : nullptr,
-                                       M_gen > 0 ? &qn_g : nullptr, io->cos_tab,
-                                       io->sin_tab, M_und, M_gen, st->heads,
-                                       st->kv_heads, st->head_dim, io->d_t, io->d_h,
-                                       io->eps, io->k_cache, io->v_cache, io->cap,
-                                       io->kv_off));
-  U15H_RUN(u15h_attention_token_major(ctx, stream, io->q, io->k_cache, io->v_cache,
-                                      io->attn, io->t_index, st->heads, st->kv_heads,
-                                      M, io->kv_len, st->head_dim, io->cap,
-                                      io->kv_off, io->mode));
-  if (i8) {
-    U15H_RUN(u15h_quant_rows_i8(ctx, stream, io->attn, M, st->qdim, io->xq, io->sx));
-    U15H_RUN(proj8(st->qdim, {U15H_PROJ_O}, {io->proj}));
-    // x += o; the post norm's codes
-    U15H_RUN(u15h_mot_rms_norm(ctx, stream, io->x, io->proj, M_und, M_gen, H,
-                               nu[U15H_NORM_POST], ng[U15H_NORM_POST], io->eps,
-                               nullptr, io->xq, io->sx));
-    U15H_RUN(proj8(H, {U15H_PROJ_GATE, U15H_PROJ_UP}, {io->h, io->up}));
-    U15H_RUN(u15h_swiglu_quant_i8(ctx, stream, io->h, io->up, M, I, nullptr, io->xq,
-                                  io->sx));
-    U15H_RUN(proj8(I, {U15H_PROJ_DOWN}, {io->proj}));
-  } else {
-    U15H_RUN(proj(io->attn, st->qdim, {U15H_PROJ_O}, {io->proj}));
-    // x += o; normed = the post norm
-    U15H_RUN(u15h_mot_rms_norm(ctx, stream, io->x, io->proj, M_und, M_gen, H,
-                               nu[U15H_NORM_POST], ng[U15H_NORM_POST], io->eps,
-                               io->normed, nullptr, nullptr));
-    const auto& gu = st->at(layer, U15H_UND, U15H_PROJ_GATE);
-    const auto& uu = st->at(layer, U15H_UND, U15H_PROJ_UP);
-    const auto& gg = st->at(layer, U15H_GEN, U15H_PROJ_GATE);
-    const auto& ug = st->at(layer, U15H_GEN, U15H_PROJ_UP);
-    U15H_RUN(u15h_mot_gate_up_swiglu(ctx, stream, io->normed, M_und, M_gen, H, gu.w,
-                                     uu.w, gg.w, ug.w, io->h, I));
-    U15H_RUN(proj(io->h, I, {U15H_PROJ_DOWN}, {io->proj}));
+  if (count < 1 || first < 0 || (long long)first + count > st->n_layers) {
+    return u15h::set_error(ctx, U15H_EINVAL, "layers [first, first + count) outside the stack");
   }
-  U15H_RUN(u15h_add(ctx, stream, io->x, io->proj, (int64_t)M * H));
-#undef U15H_RUN
+  // every layer's call is checked before the first launch
+  for (int i = 0; i < count; ++i) {
+    u15h_layer_full_io li = *io;
+    li.k_cache = k_caches[i];
+    li.v_cache = v_caches[i];
+    if (const char* why = check_full_call(st, first + i, &li, M_und, M_gen, tier)) {
+      char msg[320];
+      std::snprintf(msg, sizeof msg, "layer %d: %s", first + i, why);
+      return u15h::set_error(ctx, U15H_EINVAL, msg);
+    }
+  }
+  if (M_und + M_gen == 0) { return u15h::set_error(ctx, U15H_OK, ""); }
+  for (int i = 0; i < count; ++i) {
+    u15h_layer_full_io li = *io;
+    li.k_cache = k_caches[i];
+    li.v_cache = v_caches[i];
+    const int next = i + 1 < count ? first + i + 1 : -1;
+    const u15h_status r =
+        run_full_layer(ctx, stream, st, first + i, &li, M_und, M_gen, tier, i > 0, next);
+    if (r != U15H_OK) { return r; }
+  }
   return U15H_OK;
 }
 

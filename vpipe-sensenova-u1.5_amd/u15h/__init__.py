@@ -177,6 +177,8 @@ def load_library() -> ctypes.CDLL:
         "u15h_stack_check_full": (i, [vp, i, i, i, ctypes.c_char_p, ctypes.c_size_t]),
         "u15h_stack_layer_full": (i, [vp, vp, vp, i, ctypes.POINTER(_LayerFullIO), i, i,
                                       i]),
+        "u15h_stack_forward_full": (i, [vp, vp, vp, i, i, ctypes.POINTER(_LayerFullIO),
+                                        ctypes.POINTER(vp), ctypes.POINTER(vp), i, i, i]),
         "u15h_stack_layer": (i, [vp, vp, vp, i, ctypes.POINTER(_LayerIO), i,
                                  i, i, i, i]),
         "u15h_stack_forward": (i, [vp, vp, vp, ctypes.POINTER(_LayerIO), i,
@@ -944,6 +946,49 @@ class Ops:
         st = self._lib.u15h_stack_layer_full(self._ctx, _stream(stream), stack._h, layer,
                                              ctypes.byref(io), M_und, M_gen, tier)
         self._check(st, "u15h_stack_layer_full")
+        return scratch
+
+    def stack_forward_full(self, stack, first, count, M_und, M_gen, x, k_caches,
+                           v_caches, cos, sin, kv_off=0, kv_len=None, mode=0,
+                           t_index=None, d_t=None, d_h=None, eps=1e-6, tier=TIER_BF16,
+                           scratch=None, stream=None):
+        """u15h_stack_forward_full: whole layers [first, first + count) on
+        the residual stream x [M][hidden] (updated in place), layer first + i
+        attending k_caches[i] / v_caches[i] ([kv_heads][cap][head_dim], one
+        capacity) over keys [0, kv_len) with the pass at kv_off.  Between
+        layers the residual add and the next input norm run as one pass.
+        `scratch` (a dict from layer_scratch) is made when not given and
+        returned."""
+        M = M_und + M_gen
+        hd = stack.head_dim
+        d_t = hd // 2 if d_t is None else d_t
+        d_h = hd // 4 if d_h is None else d_h
+        kv_len = kv_off + M if kv_len is None else kv_len
+        if len(k_caches) != count or len(v_caches) != count:
+            raise ValueError(f"k_caches and v_caches must hold {count} caches")
+        _need(x, torch.bfloat16, (M, stack.hidden), "x")
+        cap = k_caches[0].shape[1]
+        for n, c in enumerate(list(k_caches) + list(v_caches)):
+            _need(c, torch.bfloat16, (stack.kv_heads, cap, hd), f"cache {n}")
+        _need(cos, torch.float32, (M, hd), "cos")
+        _need(sin, torch.float32, (M, hd), "sin")
+        if mode == 2 and (t_index is None or t_index.dtype != torch.int32 or
+                          t_index.numel() < max(kv_len, kv_off + M)):
+            raise ValueError("t_index: int32 covering max(kv_len, kv_off + M)")
+        if scratch is None:
+            scratch = layer_scratch(stack, M, tier)
+        sc = scratch
+        io = _LayerFullIO(
+            _ptr(x), _ptr(sc.get("normed")), _ptr(sc["q"]), _ptr(sc["k"]), _ptr(sc["v"]),
+            _ptr(sc["attn"]), _ptr(sc["proj"]), _ptr(sc["h"]), _ptr(sc.get("up")),
+            _ptr(sc.get("xq")), _ptr(sc.get("sx")), None, None,
+            cap, kv_off, kv_len, mode, _ptr(t_index), _ptr(cos), _ptr(sin), d_t, d_h, eps)
+        kc = (ctypes.c_void_p * count)(*[_ptr(c) for c in k_caches])
+        vc = (ctypes.c_void_p * count)(*[_ptr(c) for c in v_caches])
+        st = self._lib.u15h_stack_forward_full(self._ctx, _stream(stream), stack._h, first,
+                                               count, ctypes.byref(io), kc, vc, M_und,
+                                               M_gen, tier)
+        self._check(st, "u15h_stack_forward_full")
         return scratch
 
     # ---- the layer norms and the residual add --------------------------
