@@ -8,8 +8,8 @@
 //      ONE u15h_mot_linear launch;
 //   2. MetalOps::linear's replacement, u15h_linear, on the o projection of
 //      the gen expert;
-//   3. the layer stack: all 14 matrices bound by the reference's tensor
-//      names, u15h_stack_layer over the four steps;
+//   3. the layer stack: all 14 matrices of each of two layers bound by the
+//      reference's tensor names, u15h_stack_layer over the four steps;
 // and checks sampled rows of every output against the oracle's restatement
 // of ref::linear (max-rel <= 1e-2, rel-L2 < 4e-3); then
 //   4. the whole layer: the 12 norm vectors bound by their names too, one
@@ -17,7 +17,11 @@
 //      the layer's cache), checked bit for bit against the same layer made
 //      of the public calls (u15h_mot_rms_norm, u15h_mot_linear,
 //      u15h_mot_attention_prologue, u15h_attention_token_major,
-//      u15h_mot_gate_up_swiglu, u15h_add).
+//      u15h_mot_gate_up_swiglu, u15h_add);
+//   5. forward_many's loop: both layers of the stack (the second bound to
+//      the first's tensors) in one u15h_stack_forward_full call, checked
+//      bit for bit against two u15h_stack_layer_full calls (output and
+//      each layer's caches).
 // Exit status 0 = pass.
 #include <hip/hip_runtime_api.h>
 
@@ -197,19 +201,21 @@ main()
 
   // ---- 3. the layer stack, bound by the reference's tensor names -------
   u15h_stack* stk = nullptr;
-  check(u15h_stack_create(1, H, NH, KV, HD, I, &stk) == U15H_OK, "stack create");
+  check(u15h_stack_create(2, H, NH, KV, HD, I, &stk) == U15H_OK, "stack create");
   static const char* kAttn[4] = {"q", "k", "v", "o"};
   static const char* kMlp[3] = {"gate", "up", "down"};
-  for (int e = 0; e < 2; ++e) {
-    const std::string sfx = e ? "_mot_gen" : "";
-    for (int p = 0; p < U15H_NPROJ; ++p) {
-      const std::string name =
-          p < 4 ? "language_model.model.layers.0.self_attn." + std::string(kAttn[p]) +
-                      "_proj" + sfx + ".weight"
-                : "language_model.model.layers.0.mlp" + sfx + "." +
-                      std::string(kMlp[p - 4]) + "_proj.weight";
-      if (u15h_stack_bind(stk, name.c_str(), W(e, p)) != U15H_OK) {
-        check(false, "bind " + name);
+  // two layers, the second bound to the first's tensors
+  for (int layer = 0; layer < 2; ++layer) {
+    const std::string pre = "language_model.model.layers." + std::to_string(layer) + ".";
+    for (int e = 0; e < 2; ++e) {
+      const std::string sfx = e ? "_mot_gen" : "";
+      for (int p = 0; p < U15H_NPROJ; ++p) {
+        const std::string name =
+            p < 4 ? pre + "self_attn." + std::string(kAttn[p]) + "_proj" + sfx + ".weight"
+                  : pre + "mlp" + sfx + "." + std::string(kMlp[p - 4]) + "_proj.weight";
+        if (u15h_stack_bind(stk, name.c_str(), W(e, p)) != U15H_OK) {
+          check(false, "bind " + name);
+        }
       }
     }
   }
@@ -251,11 +257,13 @@ main()
     for (int n = 0; n < U15H_NNORM; ++n) {
       const size_t len = n < 2 ? (size_t)H : (size_t)HD / 2;
       nd[e][n] = upload(randn_bf16_mean(300u + 10u * e + n, len, 1.0f, 0.2f));
-      const std::string name = "language_model.model.layers.0." + std::string(kNorm[n]) +
-                               sfx + ".weight";
-      if (u15h_stack_bind_norm(stk, name.c_str(), nd[e][n]->as<const u15h_bf16>()) !=
-          U15H_OK) {
-        check(false, "bind " + name);
+      for (int layer = 0; layer < 2; ++layer) {
+        const std::string name = "language_model.model.layers." + std::to_string(layer) +
+                                 "." + std::string(kNorm[n]) + sfx + ".weight";
+        if (u15h_stack_bind_norm(stk, name.c_str(), nd[e][n]->as<const u15h_bf16>()) !=
+            U15H_OK) {
+          check(false, "bind " + name);
+        }
       }
     }
   }
@@ -339,6 +347,43 @@ main()
   check(ya == yb && download(kca, kca.bytes / 2) == download(kcb, kcb.bytes / 2) &&
             download(vca, vca.bytes / 2) == download(vcb, vcb.bytes / 2),
         "whole layer: bit-equal to the public calls (output and both caches)");
+
+  // ---- 5. both layers in one call: forward_many's loop -----------------
+  Dev xc((size_t)M * H * 2), xd((size_t)M * H * 2);
+  HIP_OK(hipMemcpy(xc.p, x->p, xc.bytes, hipMemcpyDeviceToDevice));
+  HIP_OK(hipMemcpy(xd.p, x->p, xd.bytes, hipMemcpyDeviceToDevice));
+  Dev* kv2[4][2];
+  for (auto& pair : kv2) {
+    for (Dev*& d : pair) { d = new Dev((size_t)KV * M * HD * 2); }
+  }
+  u15h_bf16* kf[2] = {kv2[0][0]->as<u15h_bf16>(), kv2[1][0]->as<u15h_bf16>()};
+  u15h_bf16* vf[2] = {kv2[0][1]->as<u15h_bf16>(), kv2[1][1]->as<u15h_bf16>()};
+  fio.x = xc.as<u15h_bf16>();
+  st = u15h_stack_forward_full(ctx, stream, stk, 0, 2, &fio, kf, vf, Mu, Mg,
+                               U15H_TIER_BF16);
+  check(st == U15H_OK, std::string("u15h_stack_forward_full: ") + u15h_last_error(ctx));
+  fio.x = xd.as<u15h_bf16>();
+  for (int layer = 0; layer < 2; ++layer) {
+    fio.k_cache = kv2[2 + layer][0]->as<u15h_bf16>();
+    fio.v_cache = kv2[2 + layer][1]->as<u15h_bf16>();
+    run(u15h_stack_layer_full(ctx, stream, stk, layer, &fio, Mu, Mg, U15H_TIER_BF16));
+  }
+  check(calls_ok, std::string("two u15h_stack_layer_full calls: ") + u15h_last_error(ctx));
+  HIP_OK(hipStreamSynchronize(stream));
+  bool caches_equal = true;
+  for (int layer = 0; layer < 2; ++layer) {
+    for (int c = 0; c < 2; ++c) {
+      caches_equal = caches_equal &&
+                     download(*kv2[layer][c], kv2[layer][c]->bytes / 2) ==
+                         download(*kv2[2 + layer][c], kv2[2 + layer][c]->bytes / 2);
+    }
+  }
+  const std::vector<uint16_t> yc = download(xc, (size_t)M * H);
+  check(yc != ya && yc == download(xd, (size_t)M * H) && caches_equal,
+        "two layers in one forward_full call: bit-equal to the per-layer calls");
+  for (auto& pair : kv2) {
+    for (Dev* d : pair) { delete d; }
+  }
   for (auto& row : nd) {
     for (Dev* d : row) { delete d; }
   }
