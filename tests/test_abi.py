@@ -238,6 +238,11 @@ def test_stack_refusals_without_a_device():
     io = u15h.layer_io()
     assert lib.u15h_stack_layer(None, None, h, 0, ctypes.byref(io), 0, 1, 15, 0, 0) == u15h.EINVAL
     assert lib.u15h_stack_forward(None, None, h, ctypes.byref(io), 0, 1, 0, 0) == u15h.EINVAL
+    fio = u15h._LayerFullIO()
+    caches = (ctypes.c_void_p * 2)()
+    assert lib.u15h_stack_layer_full(None, None, h, 0, ctypes.byref(fio), 0, 1, 0) == u15h.EINVAL
+    assert lib.u15h_stack_forward_full(None, None, h, 0, 2, ctypes.byref(fio), caches, caches,
+                                       0, 1, 0) == u15h.EINVAL
     lib.u15h_stack_destroy(h)
 
 

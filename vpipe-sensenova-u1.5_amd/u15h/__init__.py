@@ -964,6 +964,8 @@ class Ops:
         d_t = hd // 2 if d_t is None else d_t
         d_h = hd // 4 if d_h is None else d_h
         kv_len = kv_off + M if kv_len is None else kv_len
+        if count < 1:
+            raise ValueError("count must be at least 1")
         if len(k_caches) != count or len(v_caches) != count:
             raise ValueError(f"k_caches and v_caches must hold {count} caches")
         _need(x, torch.bfloat16, (M, stack.hidden), "x")
