@@ -500,16 +500,18 @@ def _stack_of(ops, n, seed):
 
 
 @pytest.mark.parametrize("tier", [u15h.TIER_BF16, u15h.TIER_I8])
-def test_stack_forward_full_equals_the_layer_calls(ops, tier):
+@pytest.mark.parametrize("Mu,Mg", [(64, 192), (0, 256), (96, 0)])
+def test_stack_forward_full_equals_the_layer_calls(ops, tier, Mu, Mg):
     """u15h_stack_forward_full over layers [0, 3) and over [1, 3) of a
-    3-layer stack, a two-group MoT pass after a cached prefix (kv_off 16,
-    block-causal): bit-equal to u15h_stack_layer_full layer by layer (the
-    residual add fused with the next layer's input norm gives the same
-    bits), the output and every layer's two caches slot for slot."""
-    n, Mu, Mg, pre = 3, 64, 192, 16
+    3-layer stack, a MoT pass after a cached prefix (kv_off 16,
+    block-causal) with both groups or one: bit-equal to
+    u15h_stack_layer_full layer by layer (the residual add fused with the
+    next layer's input norm gives the same bits), the output and every
+    layer's two caches slot for slot."""
+    n, pre = 3, 16
     T = Mu + Mg
     cap = pre + T + 8
-    st, g = _stack_of(ops, n, 5600 + tier)
+    st, g = _stack_of(ops, n, 5600 + tier + Mu)
     assert st.check_full(tier=tier) is None
     pos_t = np.array(list(range(pre + Mu)) + [pre + Mu] * Mg, np.int32)
     pos_h = np.array([0] * (pre + Mu) + [i // 16 for i in range(Mg)], np.int32)
